@@ -1,0 +1,106 @@
+/*
+ * lm_internal.h — private declarations shared by the C host runtime
+ * (lm_runtime.c, lm_weights.c, C99) and the HIP kernel translation units
+ * (k_*.hip).  Kernel launchers are plain C functions: raw device pointers,
+ * sizes and a hipStream_t, returning a hipError_t value (0 = success).
+ */
+#ifndef LM_INTERNAL_H
+#define LM_INTERNAL_H
+
+#include "../../include/stories_lm.h"
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Tensor order of a llama2.c weight file (training/model.h:94-160). */
+enum {
+    LMH_T_EMBED = 0, LMH_T_RMS_ATT, LMH_T_WQ, LMH_T_WK, LMH_T_WV, LMH_T_WO,
+    LMH_T_RMS_FFN, LMH_T_W1, LMH_T_W2, LMH_T_W3, LMH_T_RMS_FINAL, LMH_T_WCLS,
+    LMH_NTENSORS
+};
+
+uint16_t lmh_f32_to_f16(float f);
+float lmh_f16_to_f32(uint16_t h);
+int lmh_check_config(const Config *c);
+void lmh_tensor_sizes(const Config *c, int untied, size_t sz[LMH_NTENSORS]);
+const void *lmh_weights_ptr(const LMWeights *w, int t);
+int lmh_weights_untied(const LMWeights *w);
+int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data);
+
+/* Rows of W1 and W3 are stored interleaved in blocks of LMK_GATE_BLOCK rows:
+ * block j = [W1 rows j*G .. j*G+G-1, W3 rows j*G .. j*G+G-1], so any 2G-wide
+ * output tile of the fused W1|W3 product holds matching h1/h3 columns. */
+#define LMK_GATE_BLOCK 16
+
+/* Positions handled by one decode-attention work-group (one KV split). */
+#define LMK_ATTN_CHUNK 64
+
+/* Argmax partial: best value and its index (lowest index on ties). */
+typedef struct { float val; int idx; } LMArgPart;
+
+/* ---- decode kernels (k_decode.hip) ---------------------------------------
+ * Activations are fp32 [B, ...]; weights fp16 row-major W[out, in].
+ * KV cache of one layer: [max_batch][Hkv][max_seq][hd] fp16, slot b = row b. */
+
+/* x[b, :] = fp32(embed[tok[b], :]) */
+int lmk_embed(hipStream_t s, const uint16_t *embed, const int *tok, float *x,
+              int B, int D);
+
+/* xn = rmsnorm(x[b]) * w; rows of [Wq;Wk;Wv] . xn; RoPE on q,k rows at pos[b];
+ * q -> q[b, :NQ] fp32, k,v -> cache[b][h][pos[b]][:] (fp16, or fp32 when
+ * kv_f32). */
+int lmk_qkv_rope(hipStream_t s, const float *x, const float *rms_w,
+                 const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
+                 const float *rope_cos, const float *rope_sin, const int *pos,
+                 int B, float *q, void *kc, void *vc, int kv_f32, int max_seq);
+
+/* Split-KV decode attention: work-group (split, h, b) covers positions
+ * [split*CHUNK, min(pos[b]+1, (split+1)*CHUNK)) and writes (max, sum, o[hd])
+ * to part[((b*H + h)*nsplit + split)*(hd+2)]. */
+int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
+                    const void *vc, int kv_f32, const int *pos, int B, int H, int Hkv,
+                    int hd, int max_seq, int nsplit, float *part);
+
+/* Merge the attention partials per head, then x[b, r] += Wo[r, :] . attn[b]. */
+int lmk_wo_residual(hipStream_t s, const float *part, int nsplit,
+                    const uint16_t *wo, int D, int H, int hd, int B, float *x);
+
+/* xn = rmsnorm(x[b]) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
+int lmk_ffn13(hipStream_t s, const float *x, const float *rms_w,
+              const uint16_t *w13, int D, int F, int B, float *g);
+
+/* x[b, r] += W2[r, :] . g[b, :] */
+int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
+                    int F, int B, float *x);
+
+/* xn = rmsnorm(x[b]) * w; logits[b, v] = Wcls[v] . xn (logits may be NULL);
+ * per work-group argmax partials into part[b * nblk + blk]. Returns nblk via
+ * *nblk_out when non-NULL (same value as lmk_cls_nblk). */
+int lmk_cls_nblk(int V);
+int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
+            const uint16_t *wcls, int D, int V, int B, float *logits,
+            LMArgPart *part);
+
+/* Reduce argmax partials of each row b: tok[b] = argmax; when hist != NULL,
+ * hist[b*hist_stride + pos[b] + 1] = tok[b] and pos[b] += 1 (device-resident
+ * greedy loop state). */
+int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,
+                     int *tok, int *pos, int *hist, int hist_stride);
+
+/* ---- diagnostics kernels (k_decode.hip) ---------------------------------- */
+
+/* Wave-reduction self-check: out[0..3] = sums computed with the production
+ * DPP reduction and with a shuffle reduction over in[0..63]. */
+int lmk_selftest_reduce(hipStream_t s, const float *in, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LM_INTERNAL_H */

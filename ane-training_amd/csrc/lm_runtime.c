@@ -1,0 +1,665 @@
+/*
+ * lm_runtime.c — the C-ABI runtime of the Stories token loop (C99 over the HIP
+ * C runtime API).  It owns device memory, the stream, the per-batch decode
+ * graphs and the host-facing entry points of stories_lm.h; every kernel is
+ * reached through the lmk_* launchers of the HIP translation units.
+ *
+ * Device layout (all row-major, W[out, in]):
+ *   layer block l (one allocation for all layers, layer after layer):
+ *     Wqkv [NQ + 2*NKV, D]   Wq rows, then Wk rows, then Wv rows
+ *     Wo   [D, NQ]
+ *     W13  [2F, D]           W1/W3 rows interleaved in blocks of 16
+ *     W2   [D, F]
+ *   embed [V, D], wcls [V, D] (the embedding itself when tied)   fp16
+ *   rms_att [L, D], rms_ffn [L, D], rms_final [D]                  fp32
+ *   RoPE cos/sin [max_seq, hd/2]                                   fp32
+ *   K/V cache, per layer [max_batch][Hkv][max_seq][hd]             fp16
+ *   residual x [rows, D], q [rows, NQ], gate g [rows, F],
+ *   logits [rows, V]                                               fp32
+ */
+#include "lm_internal.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define HIPCHK(call)                                                                 \
+    do {                                                                             \
+        hipError_t e_ = (call);                                                      \
+        if (e_ != hipSuccess) {                                                      \
+            fprintf(stderr, "stories_lm: %s failed at %s:%d: %s\n", #call, __FILE__, \
+                    __LINE__, hipGetErrorString(e_));                                \
+            return LM_ERR_HIP;                                                       \
+        }                                                                            \
+    } while (0)
+
+#define MAX_GEMV_B 4
+
+struct LMModel {
+    Config cfg;                 /* vocab_size positive */
+    int untied;
+    int D, F, L, H, Hkv, hd, NQ, NKV, V;
+    int max_batch, max_seq, max_rows;
+    int nsplit, cls_nblk;
+    size_t layer_elems, off_wo, off_w13, off_w2;
+    hipStream_t stream;
+    hipEvent_t ev0, ev1;
+    /* weights */
+    uint16_t *d_layers, *d_embed, *d_wcls;
+    float *d_rms_att, *d_rms_ffn, *d_rms_final;
+    float *d_rope_cos, *d_rope_sin;
+    /* cache + activations */
+    void *d_kc, *d_vc;
+    size_t kv_layer_elems;
+    int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
+    float *d_x, *d_q, *d_part, *d_g, *d_logits;
+    LMArgPart *d_amax;
+    int *d_tok, *d_pos, *d_hist;
+    /* pinned host staging */
+    float *h_logits;
+    int *h_io;
+    /* graphs, index = B (GEMV path) */
+    hipGraphExec_t step_graph[MAX_GEMV_B + 1];
+    int use_graph, decode_path;
+};
+
+static int g_init_status = 1; /* 1 = not attempted */
+
+const char *lm_strerror(int status)
+{
+    switch (status) {
+    case LM_OK: return "ok";
+    case LM_ERR_NO_DEVICE: return "no HIP device";
+    case LM_ERR_NOT_GFX950: return "device is not gfx950";
+    case LM_ERR_INVALID: return "invalid argument";
+    case LM_ERR_OOM: return "out of memory";
+    case LM_ERR_HIP: return "HIP runtime error";
+    case LM_ERR_IO: return "I/O error";
+    case LM_ERR_FORMAT: return "bad or truncated weight file";
+    case LM_ERR_RANGE: return "token, position, slot or length out of range";
+    case LM_ERR_UNSUPPORTED: return "shape not supported by the kernels";
+    case LM_ERR_NOT_INIT: return "lm_init not called or failed";
+    default: return "unknown status";
+    }
+}
+
+int lm_init(void)
+{
+    if (g_init_status <= 0) return g_init_status;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        fprintf(stderr, "stories_lm: no HIP device visible\n");
+        g_init_status = LM_ERR_NO_DEVICE;
+        return g_init_status;
+    }
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) != hipSuccess) {
+        g_init_status = LM_ERR_NO_DEVICE;
+        return g_init_status;
+    }
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+        fprintf(stderr, "stories_lm: device 0 is %s, kernels are built for gfx950\n",
+                p.gcnArchName);
+        g_init_status = LM_ERR_NOT_GFX950;
+        return g_init_status;
+    }
+    if (hipSetDevice(0) != hipSuccess) {
+        g_init_status = LM_ERR_NO_DEVICE;
+        return g_init_status;
+    }
+    g_init_status = LM_OK;
+    return LM_OK;
+}
+
+int lm_device_info(LMDeviceInfo *out)
+{
+    if (!out) return LM_ERR_INVALID;
+    int rc = lm_init();
+    if (rc) return rc;
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, 0));
+    memset(out, 0, sizeof(*out));
+    snprintf(out->name, sizeof(out->name), "%.63s", p.name);
+    snprintf(out->arch, sizeof(out->arch), "%.31s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->clock_khz = p.clockRate;
+    out->l2_bytes = p.l2CacheSize;
+    out->total_mem = p.totalGlobalMem;
+    return LM_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* creation                                                                   */
+/* ------------------------------------------------------------------------- */
+
+static int dev_alloc(void **p, size_t bytes)
+{
+    *p = NULL;
+    if (bytes == 0) return LM_OK;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        fprintf(stderr, "stories_lm: hipMalloc(%zu) failed: %s\n", bytes, hipGetErrorString(e));
+        *p = NULL;
+        return LM_ERR_OOM;
+    }
+    return LM_OK;
+}
+
+/* Copy n elements of tensor src (fp32 or fp16) as fp16 into dst (host). */
+static void to_f16(const void *src, LMDType dt, size_t off, size_t n, uint16_t *dst)
+{
+    if (dt == LM_DTYPE_F16)
+        memcpy(dst, (const uint16_t *)src + off, n * 2);
+    else
+        lm_f32_to_f16((const float *)src + off, dst, n);
+}
+
+static void to_f32(const void *src, LMDType dt, size_t off, size_t n, float *dst)
+{
+    if (dt == LM_DTYPE_F32)
+        memcpy(dst, (const float *)src + off, n * 4);
+    else
+        lm_f16_to_f32((const uint16_t *)src + off, dst, n);
+}
+
+static int upload_weights(LMModel *m, const LMWeights *w)
+{
+    const size_t D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, V = m->V, L = m->L;
+    const size_t GB = LMK_GATE_BLOCK;
+    uint16_t *stage = (uint16_t *)malloc(m->layer_elems * 2);
+    float *nf = (float *)malloc(L * D * 4);
+    if (!stage || !nf) { free(stage); free(nf); return LM_ERR_OOM; }
+    int rc = LM_OK;
+    for (size_t l = 0; l < L && rc == LM_OK; l++) {
+        uint16_t *p = stage;
+        to_f16(w->wq, w->dtype, l * NQ * D, NQ * D, p);              p += NQ * D;
+        to_f16(w->wk, w->dtype, l * NKV * D, NKV * D, p);            p += NKV * D;
+        to_f16(w->wv, w->dtype, l * NKV * D, NKV * D, p);            p += NKV * D;
+        to_f16(w->wo, w->dtype, l * D * NQ, D * NQ, p);              p += D * NQ;
+        for (size_t j = 0; j < F / GB; j++) {
+            to_f16(w->w1, w->dtype, l * F * D + j * GB * D, GB * D, p); p += GB * D;
+            to_f16(w->w3, w->dtype, l * F * D + j * GB * D, GB * D, p); p += GB * D;
+        }
+        to_f16(w->w2, w->dtype, l * D * F, D * F, p);
+        if (hipMemcpy(m->d_layers + l * m->layer_elems, stage, m->layer_elems * 2,
+                      hipMemcpyHostToDevice) != hipSuccess)
+            rc = LM_ERR_HIP;
+    }
+    free(stage);
+    if (rc == LM_OK) {
+        uint16_t *e16 = (uint16_t *)malloc(V * D * 2);
+        if (!e16) rc = LM_ERR_OOM;
+        if (rc == LM_OK) {
+            to_f16(w->token_embedding, w->dtype, 0, V * D, e16);
+            if (hipMemcpy(m->d_embed, e16, V * D * 2, hipMemcpyHostToDevice) != hipSuccess)
+                rc = LM_ERR_HIP;
+            if (rc == LM_OK && m->untied) {
+                to_f16(w->wcls, w->dtype, 0, V * D, e16);
+                if (hipMemcpy(m->d_wcls, e16, V * D * 2, hipMemcpyHostToDevice) != hipSuccess)
+                    rc = LM_ERR_HIP;
+            }
+        }
+        free(e16);
+    }
+    if (rc == LM_OK) {
+        to_f32(w->rms_att_w, w->dtype, 0, L * D, nf);
+        if (hipMemcpy(m->d_rms_att, nf, L * D * 4, hipMemcpyHostToDevice) != hipSuccess) rc = LM_ERR_HIP;
+        to_f32(w->rms_ffn_w, w->dtype, 0, L * D, nf);
+        if (rc == LM_OK && hipMemcpy(m->d_rms_ffn, nf, L * D * 4, hipMemcpyHostToDevice) != hipSuccess)
+            rc = LM_ERR_HIP;
+        to_f32(w->rms_final_w, w->dtype, 0, D, nf);
+        if (rc == LM_OK && hipMemcpy(m->d_rms_final, nf, D * 4, hipMemcpyHostToDevice) != hipSuccess)
+            rc = LM_ERR_HIP;
+    }
+    free(nf);
+    return rc;
+}
+
+static size_t kv_bytes(const LMModel *m)
+{
+    return (size_t)m->L * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
+}
+
+/* (Re)allocate the K/V cache in the current element type, zero-filled. */
+static int alloc_kv(LMModel *m)
+{
+    if (m->d_kc) { hipFree(m->d_kc); m->d_kc = NULL; }
+    if (m->d_vc) { hipFree(m->d_vc); m->d_vc = NULL; }
+    int st = dev_alloc(&m->d_kc, kv_bytes(m));
+    if (!st) st = dev_alloc(&m->d_vc, kv_bytes(m));
+    if (st) return st;
+    if (hipMemset(m->d_kc, 0, kv_bytes(m)) != hipSuccess ||
+        hipMemset(m->d_vc, 0, kv_bytes(m)) != hipSuccess)
+        return LM_ERR_HIP;
+    return LM_OK;
+}
+
+static void drop_graphs(LMModel *m)
+{
+    for (int b = 0; b <= MAX_GEMV_B; b++)
+        if (m->step_graph[b]) {
+            hipGraphExecDestroy(m->step_graph[b]);
+            m->step_graph[b] = NULL;
+        }
+}
+
+static int supported_k(int k)
+{
+    return k == 256 || k == 512 || k == 768 || k == 1024 || k == 2048 || k == 5632;
+}
+
+LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max_seq, int *status)
+{
+    int st = LM_OK;
+    LMModel *m = NULL;
+#define FAIL(code)      \
+    do {                \
+        st = (code);    \
+        goto fail;      \
+    } while (0)
+    if (!cfg || !w || max_batch < 1 || max_seq < 1) FAIL(LM_ERR_INVALID);
+    if ((st = lm_init()) != LM_OK) goto fail;
+    if ((st = lmh_check_config(cfg)) != LM_OK) {
+        fprintf(stderr, "stories_lm: inconsistent Config\n");
+        goto fail;
+    }
+    if (w->dtype != LM_DTYPE_F32 && w->dtype != LM_DTYPE_F16) FAIL(LM_ERR_INVALID);
+    for (int t = 0; t < LMH_NTENSORS - 1; t++)
+        if (!lmh_weights_ptr(w, t)) {
+            fprintf(stderr, "stories_lm: weight tensor %d is NULL\n", t);
+            FAIL(LM_ERR_INVALID);
+        }
+    m = (LMModel *)calloc(1, sizeof(LMModel));
+    if (!m) FAIL(LM_ERR_OOM);
+    m->cfg = *cfg;
+    m->V = cfg->vocab_size < 0 ? -cfg->vocab_size : cfg->vocab_size;
+    m->cfg.vocab_size = m->V;
+    m->untied = lmh_weights_untied(w);
+    m->D = cfg->dim; m->F = cfg->hidden_dim; m->L = cfg->n_layers;
+    m->H = cfg->n_heads; m->Hkv = cfg->n_kv_heads;
+    m->hd = m->D / m->H;
+    m->NQ = m->H * m->hd;
+    m->NKV = m->Hkv * m->hd;
+    if ((m->hd != 64 && m->hd != 128) || !supported_k(m->D) || !supported_k(m->F)) {
+        fprintf(stderr, "stories_lm: unsupported shape dim=%d hidden=%d head_dim=%d "
+                "(need head_dim 64/128, dim and hidden in {256,512,768,1024,2048,5632})\n",
+                m->D, m->F, m->hd);
+        FAIL(LM_ERR_UNSUPPORTED);
+    }
+    if (max_seq > (1 << 16) || max_batch > 4096) FAIL(LM_ERR_RANGE);
+    m->max_batch = max_batch;
+    m->max_seq = max_seq;
+    m->max_rows = max_batch;
+    m->nsplit = (max_seq + LMK_ATTN_CHUNK - 1) / LMK_ATTN_CHUNK;
+    m->cls_nblk = lmk_cls_nblk(m->V);
+    m->use_graph = 1;
+    m->decode_path = 0;
+
+    const size_t D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, V = m->V, L = m->L;
+    m->off_wo = (NQ + 2 * NKV) * D;
+    m->off_w13 = m->off_wo + D * NQ;
+    m->off_w2 = m->off_w13 + 2 * F * D;
+    m->layer_elems = m->off_w2 + D * F;
+    m->kv_layer_elems = (size_t)max_batch * m->Hkv * max_seq * m->hd;
+    const size_t R = m->max_rows;
+
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) FAIL(LM_ERR_HIP);
+    if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
+        FAIL(LM_ERR_HIP);
+    if ((st = dev_alloc((void **)&m->d_layers, L * m->layer_elems * 2))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_embed, V * D * 2))) goto fail;
+    if (m->untied) {
+        if ((st = dev_alloc((void **)&m->d_wcls, V * D * 2))) goto fail;
+    } else {
+        m->d_wcls = m->d_embed;
+    }
+    if ((st = dev_alloc((void **)&m->d_rms_att, L * D * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_rms_ffn, L * D * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_rms_final, D * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_rope_cos, (size_t)max_seq * m->hd / 2 * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_rope_sin, (size_t)max_seq * m->hd / 2 * 4))) goto fail;
+    if ((st = alloc_kv(m))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_x, R * D * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_q, R * NQ * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_g, R * F * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_logits, R * V * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_part,
+                        (size_t)max_batch * m->H * m->nsplit * (m->hd + 2) * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_amax, R * m->cls_nblk * sizeof(LMArgPart)))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_tok, R * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_pos, R * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
+    if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
+    if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
+
+    if ((st = upload_weights(m, w))) goto fail;
+    {
+        size_t n = (size_t)max_seq * m->hd / 2;
+        float *c = (float *)malloc(n * 4), *s = (float *)malloc(n * 4);
+        if (!c || !s) { free(c); free(s); FAIL(LM_ERR_OOM); }
+        lm_rope_table(max_seq, m->hd, c, s);
+        hipError_t e1 = hipMemcpy(m->d_rope_cos, c, n * 4, hipMemcpyHostToDevice);
+        hipError_t e2 = hipMemcpy(m->d_rope_sin, s, n * 4, hipMemcpyHostToDevice);
+        free(c); free(s);
+        if (e1 != hipSuccess || e2 != hipSuccess) FAIL(LM_ERR_HIP);
+    }
+    if (hipMemset(m->d_hist, 0, (size_t)max_batch * (max_seq + 1) * 4) != hipSuccess ||
+        hipMemset(m->d_pos, 0, R * 4) != hipSuccess || hipMemset(m->d_tok, 0, R * 4) != hipSuccess)
+        FAIL(LM_ERR_HIP);
+    if (hipDeviceSynchronize() != hipSuccess) FAIL(LM_ERR_HIP);
+    if (status) *status = LM_OK;
+    return m;
+fail:
+    if (status) *status = st;
+    if (st != LM_OK) fprintf(stderr, "stories_lm: lm_create failed: %s\n", lm_strerror(st));
+    lm_free(m);
+    return NULL;
+#undef FAIL
+}
+
+LMModel *lm_load_llama2c(const char *path, int max_batch, int max_seq, int *status)
+{
+    if (!path) {
+        if (status) *status = LM_ERR_INVALID;
+        return NULL;
+    }
+    Config cfg;
+    int untied = 0;
+    float *data = NULL;
+    int rc = lmh_read_llama2c(path, &cfg, &untied, &data);
+    if (rc) {
+        if (status) *status = rc;
+        return NULL;
+    }
+    LMWeights w;
+    lm_weights_view(&cfg, LM_DTYPE_F32, data, untied, &w);
+    LMModel *m = lm_create(&cfg, &w, max_batch, max_seq, status);
+    free(data);
+    return m;
+}
+
+void lm_free(LMModel *m)
+{
+    if (!m) return;
+    if (m->stream) hipStreamSynchronize(m->stream);
+    drop_graphs(m);
+    void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
+                   m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
+                   m->d_vc, m->d_x, m->d_q, m->d_g, m->d_logits, m->d_part, m->d_amax,
+                   m->d_tok, m->d_pos, m->d_hist};
+    for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
+        if (dev[i]) hipFree(dev[i]);
+    if (m->h_logits) hipHostFree(m->h_logits);
+    if (m->h_io) hipHostFree(m->h_io);
+    if (m->ev0) hipEventDestroy(m->ev0);
+    if (m->ev1) hipEventDestroy(m->ev1);
+    if (m->stream) hipStreamDestroy(m->stream);
+    free(m);
+}
+
+int lm_get_config(const LMModel *m, Config *out)
+{
+    if (!m || !out) return LM_ERR_INVALID;
+    *out = m->cfg;
+    return LM_OK;
+}
+
+int lm_set_option(LMModel *m, int option, int value)
+{
+    if (!m) return LM_ERR_INVALID;
+    switch (option) {
+    case LM_OPT_DECODE_PATH:
+        if (value < 0 || value > 2) return LM_ERR_INVALID;
+        m->decode_path = value;
+        return LM_OK;
+    case LM_OPT_USE_GRAPH:
+        m->use_graph = value ? 1 : 0;
+        return LM_OK;
+    case LM_OPT_KV_F32:
+        if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        drop_graphs(m);
+        m->kv_f32 = value ? 1 : 0;
+        return alloc_kv(m);
+    default:
+        return LM_ERR_INVALID;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* decode step                                                                */
+/* ------------------------------------------------------------------------- */
+
+#define KCHK(call)                                                                    \
+    do {                                                                              \
+        int e_ = (call);                                                              \
+        if (e_ != 0) {                                                                \
+            fprintf(stderr, "stories_lm: launch %s failed: %s\n", #call,              \
+                    hipGetErrorString((hipError_t)e_));                               \
+            return LM_ERR_HIP;                                                        \
+        }                                                                             \
+    } while (0)
+
+/* Queue one decode step for rows 0..B-1 (tokens in d_tok, positions in d_pos);
+ * logits go to `logits` (device, B x V, may be NULL), argmax to d_tok. */
+static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
+{
+    hipStream_t s = m->stream;
+    const int D = m->D, F = m->F;
+    KCHK(lmk_embed(s, m->d_embed, m->d_tok, m->d_x, B, D));
+    for (int l = 0; l < m->L; l++) {
+        const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
+        const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
+        void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
+        KCHK(lmk_qkv_rope(s, m->d_x, m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
+                          m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
+                          m->max_seq));
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
+                             m->max_seq, m->nsplit, m->d_part));
+        KCHK(lmk_wo_residual(s, m->d_part, m->nsplit, lw + m->off_wo, D, m->H, m->hd, B, m->d_x));
+        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
+        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
+    }
+    KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
+    KCHK(lmk_argmax_final(s, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
+                          m->max_seq + 1));
+    return LM_OK;
+}
+
+static int run_decode_step(LMModel *m, int B)
+{
+    if (B > MAX_GEMV_B) {
+        fprintf(stderr, "stories_lm: decode batch %d > %d not supported yet\n", B, MAX_GEMV_B);
+        return LM_ERR_UNSUPPORTED;
+    }
+    if (!m->use_graph) return enqueue_decode_gemv(m, B, m->d_logits);
+    if (!m->step_graph[B]) {
+        hipGraph_t g;
+        HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_decode_gemv(m, B, m->d_logits);
+        hipError_t e = hipStreamEndCapture(m->stream, &g);
+        if (rc) return rc;
+        HIPCHK(e);
+        e = hipGraphInstantiate(&m->step_graph[B], g, NULL, NULL, 0);
+        hipGraphDestroy(g);
+        HIPCHK(e);
+    }
+    HIPCHK(hipGraphLaunch(m->step_graph[B], m->stream));
+    return LM_OK;
+}
+
+static int check_tok_pos(const LMModel *m, const int *tokens, const int *pos, int B)
+{
+    for (int b = 0; b < B; b++) {
+        if (tokens[b] < 0 || tokens[b] >= m->V) {
+            fprintf(stderr, "stories_lm: token %d out of range [0,%d)\n", tokens[b], m->V);
+            return LM_ERR_RANGE;
+        }
+        if (pos[b] < 0 || pos[b] >= m->max_seq) {
+            fprintf(stderr, "stories_lm: position %d out of range [0,%d)\n", pos[b], m->max_seq);
+            return LM_ERR_RANGE;
+        }
+    }
+    return LM_OK;
+}
+
+int lm_forward_batch(LMModel *m, const int *tokens, const int *pos, int B, float *logits, int *argmax)
+{
+    if (!m || !tokens || !pos || B < 1) return LM_ERR_INVALID;
+    if (B > m->max_batch) return LM_ERR_RANGE;
+    int rc = check_tok_pos(m, tokens, pos, B);
+    if (rc) return rc;
+    int *hio = m->h_io;
+    memcpy(hio, tokens, B * 4);
+    memcpy(hio + B, pos, B * 4);
+    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    if ((rc = run_decode_step(m, B))) return rc;
+    if (argmax)
+        HIPCHK(hipMemcpyAsync(hio + 2 * B, m->d_tok, B * 4, hipMemcpyDeviceToHost, m->stream));
+    if (logits)
+        HIPCHK(hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)B * m->V * 4,
+                              hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    if (argmax) memcpy(argmax, hio + 2 * B, B * 4);
+    if (logits) memcpy(logits, m->h_logits, (size_t)B * m->V * 4);
+    return LM_OK;
+}
+
+const float *lm_forward(LMModel *m, int token, int pos)
+{
+    if (!m) {
+        fprintf(stderr, "stories_lm: lm_forward on NULL handle\n");
+        return NULL;
+    }
+    if (check_tok_pos(m, &token, &pos, 1)) return NULL;
+    int *hio = m->h_io;
+    hio[0] = token;
+    hio[1] = pos;
+    if (hipMemcpyAsync(m->d_tok, hio, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+        hipMemcpyAsync(m->d_pos, hio + 1, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
+        return NULL;
+    if (run_decode_step(m, 1)) return NULL;
+    if (hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
+                       m->stream) != hipSuccess ||
+        hipStreamSynchronize(m->stream) != hipSuccess) {
+        fprintf(stderr, "stories_lm: lm_forward: HIP error\n");
+        return NULL;
+    }
+    return m->h_logits;
+}
+
+int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *pos0, int n_steps,
+                       int *out_tokens)
+{
+    if (!m || !first_tokens || !pos0 || !out_tokens || B < 1 || n_steps < 0) return LM_ERR_INVALID;
+    if (B > m->max_batch) return LM_ERR_RANGE;
+    int rc = check_tok_pos(m, first_tokens, pos0, B);
+    if (rc) return rc;
+    for (int b = 0; b < B; b++)
+        if (pos0[b] + n_steps > m->max_seq) {
+            fprintf(stderr, "stories_lm: pos0 %d + %d steps exceeds max_seq %d\n", pos0[b], n_steps,
+                    m->max_seq);
+            return LM_ERR_RANGE;
+        }
+    if (n_steps == 0) return LM_OK;
+    int *hio = m->h_io;
+    memcpy(hio, first_tokens, B * 4);
+    memcpy(hio + B, pos0, B * 4);
+    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    for (int t = 0; t < n_steps; t++)
+        if ((rc = run_decode_step(m, B))) return rc;
+    const size_t stride = (size_t)m->max_seq + 1;
+    int *h = (int *)malloc((size_t)B * stride * 4);
+    if (!h) return LM_ERR_OOM;
+    hipError_t e = hipMemcpyAsync(h, m->d_hist, (size_t)B * stride * 4, hipMemcpyDeviceToHost, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) {
+        free(h);
+        fprintf(stderr, "stories_lm: lm_generate_greedy: %s\n", hipGetErrorString(e));
+        return LM_ERR_HIP;
+    }
+    for (int t = 0; t < n_steps; t++)
+        for (int b = 0; b < B; b++) out_tokens[(size_t)t * B + b] = h[b * stride + pos0[b] + 1 + t];
+    free(h);
+    return LM_OK;
+}
+
+/* Prefill by decode steps (KV-cache semantics, training/dashboard.py:205-267):
+ * row t of the S x V logits is the step at position pos0 + t. */
+int lm_prefill(LMModel *m, int slot, int pos0, const int *tokens, int S, float *logits)
+{
+    if (!m || !tokens || S < 1) return LM_ERR_INVALID;
+    if (slot < 0 || slot >= m->max_batch || pos0 < 0 || pos0 + S > m->max_seq) return LM_ERR_RANGE;
+    if (slot != 0) {
+        fprintf(stderr, "stories_lm: lm_prefill: slot %d needs the batched path\n", slot);
+        return LM_ERR_UNSUPPORTED;
+    }
+    for (int t = 0; t < S; t++) {
+        int p = pos0 + t;
+        const float *row = lm_forward(m, tokens[t], p);
+        if (!row) return LM_ERR_HIP;
+        if (logits) memcpy(logits + (size_t)t * m->V, row, (size_t)m->V * 4);
+    }
+    return LM_OK;
+}
+
+int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens, int S,
+                     int logits_mode, float *logits)
+{
+    (void)m; (void)nseq; (void)slots; (void)tokens; (void)S; (void)logits_mode; (void)logits;
+    return LM_ERR_UNSUPPORTED;
+}
+
+int lm_read_logits(LMModel *m, int row0, int nrows, float *dst)
+{
+    if (!m || !dst || row0 < 0 || nrows < 0) return LM_ERR_INVALID;
+    if (row0 + nrows > m->max_rows) return LM_ERR_RANGE;
+    HIPCHK(hipMemcpy(dst, m->d_logits + (size_t)row0 * m->V, (size_t)nrows * m->V * 4,
+                     hipMemcpyDeviceToHost));
+    return LM_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* timing                                                                     */
+/* ------------------------------------------------------------------------- */
+
+int lm_sync(LMModel *m)
+{
+    if (!m) return LM_ERR_INVALID;
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return LM_OK;
+}
+
+int lm_timer_begin(LMModel *m)
+{
+    if (!m) return LM_ERR_INVALID;
+    HIPCHK(hipEventRecord(m->ev0, m->stream));
+    return LM_OK;
+}
+
+int lm_timer_end(LMModel *m, float *ms)
+{
+    if (!m || !ms) return LM_ERR_INVALID;
+    HIPCHK(hipEventRecord(m->ev1, m->stream));
+    HIPCHK(hipEventSynchronize(m->ev1));
+    HIPCHK(hipEventElapsedTime(ms, m->ev0, m->ev1));
+    return LM_OK;
+}
+
+/* Diagnostics: run the DPP reduction self-test (no model needed). */
+int lm_selftest_reduce(const float *in64, float *out4)
+{
+    if (!in64 || !out4) return LM_ERR_INVALID;
+    int rc = lm_init();
+    if (rc) return rc;
+    float *d = NULL;
+    HIPCHK(hipMalloc((void **)&d, 68 * 4));
+    hipError_t e = hipMemcpy(d, in64, 64 * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = (hipError_t)lmk_selftest_reduce(0, d, d + 64);
+    if (e == hipSuccess) e = hipMemcpy(out4, d + 64, 16, hipMemcpyDeviceToHost);
+    hipFree(d);
+    HIPCHK(e);
+    return LM_OK;
+}

@@ -1,0 +1,337 @@
+"""ctypes binding of libstories_lm.so (the C ABI in include/stories_lm.h).
+
+Mirrors the reference's model surface: a llama2.c ``Config`` (training/model.h:19-21),
+weight buffers in llama2.c order (training/model.h:78-164) and a token step
+``forward(token, pos) -> logits`` (the body of training/training_dynamic/generate.m:437-487).
+numpy arrays in and out; no torch.  Loading fails loudly when the shared library has
+not been built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libstories_lm.so")
+
+LM_OK = 0
+LM_ERR_NO_DEVICE = -1
+LM_ERR_NOT_GFX950 = -2
+LM_ERR_INVALID = -3
+LM_ERR_OOM = -4
+LM_ERR_HIP = -5
+LM_ERR_IO = -6
+LM_ERR_FORMAT = -7
+LM_ERR_RANGE = -8
+LM_ERR_UNSUPPORTED = -9
+LM_ERR_NOT_INIT = -10
+
+LM_DTYPE_F32 = 0
+LM_DTYPE_F16 = 1
+
+LM_OPT_DECODE_PATH = 1
+LM_OPT_USE_GRAPH = 2
+LM_OPT_KV_F32 = 3
+
+LM_LOGITS_ALL = 0
+LM_LOGITS_LAST = 1
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int) for n in
+                ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size", "seq_len")]
+
+    def astuple(self):
+        return tuple(getattr(self, n) for n, _ in self._fields_)
+
+
+class LMWeights(C.Structure):
+    _fields_ = [("dtype", C.c_int)] + [(n, C.c_void_p) for n in (
+        "token_embedding", "rms_att_w", "wq", "wk", "wv", "wo", "rms_ffn_w",
+        "w1", "w2", "w3", "rms_final_w", "wcls")]
+
+
+class LMDeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32), ("compute_units", C.c_int),
+                ("clock_khz", C.c_int), ("l2_bytes", C.c_int), ("total_mem", C.c_size_t)]
+
+
+class LMError(RuntimeError):
+    def __init__(self, status, what=""):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} ({status})")
+
+
+_lib = None
+
+
+def lib():
+    """Load libstories_lm.so once; raise if it is missing (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() or make -C ane-training_amd")
+    L = C.CDLL(LIB_PATH)
+    P, I, F = C.c_void_p, C.c_int, C.c_float
+    ip, fp = C.POINTER(C.c_int), C.POINTER(C.c_float)
+    sig = {
+        "lm_strerror": (C.c_char_p, [I]),
+        "lm_init": (I, []),
+        "lm_device_info": (I, [C.POINTER(LMDeviceInfo)]),
+        "lm_create": (P, [C.POINTER(Config), C.POINTER(LMWeights), I, I, ip]),
+        "lm_load_llama2c": (P, [C.c_char_p, I, I, ip]),
+        "lm_free": (None, [P]),
+        "lm_get_config": (I, [P, C.POINTER(Config)]),
+        "lm_forward": (fp, [P, I, I]),
+        "lm_forward_batch": (I, [P, ip, ip, I, fp, ip]),
+        "lm_prefill": (I, [P, I, I, ip, I, fp]),
+        "lm_prefill_batch": (I, [P, I, ip, ip, I, I, fp]),
+        "lm_read_logits": (I, [P, I, I, fp]),
+        "lm_generate_greedy": (I, [P, I, ip, ip, I, ip]),
+        "lm_sync": (I, [P]),
+        "lm_timer_begin": (I, [P]),
+        "lm_timer_end": (I, [P, fp]),
+        "lm_set_option": (I, [P, I, I]),
+        "lm_weights_numel": (C.c_size_t, [C.POINTER(Config), I]),
+        "lm_weights_view": (I, [C.POINTER(Config), I, P, I, C.POINTER(LMWeights)]),
+        "lm_synth_weights_f16": (I, [C.POINTER(Config), C.c_uint64, F, I, C.POINTER(C.c_uint16)]),
+        "lm_write_llama2c": (I, [C.c_char_p, C.POINTER(Config), C.POINTER(LMWeights)]),
+        "lm_f32_to_f16": (None, [fp, C.POINTER(C.c_uint16), C.c_size_t]),
+        "lm_f16_to_f32": (None, [C.POINTER(C.c_uint16), fp, C.c_size_t]),
+        "lm_rope_table": (I, [I, I, fp, fp]),
+        "lm_selftest_reduce": (I, [fp, fp]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def strerror(status: int) -> str:
+    return lib().lm_strerror(int(status)).decode()
+
+
+def _ip(a):
+    return a.ctypes.data_as(C.POINTER(C.c_int))
+
+
+def _fp(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _u16p(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+
+def make_config(dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len) -> Config:
+    return Config(dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len)
+
+
+STORIES_110M = dict(dim=768, hidden_dim=2048, n_layers=12, n_heads=12, n_kv_heads=12,
+                    vocab_size=32000, seq_len=256)
+SCALED_2048 = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16,
+                   vocab_size=32000, seq_len=640)
+
+
+def weights_numel(cfg: Config, untied: bool) -> int:
+    return int(lib().lm_weights_numel(C.byref(cfg), int(untied)))
+
+
+def synth_weights_f16(cfg: Config, seed: int, std: float = 0.02, untied: bool = True) -> np.ndarray:
+    """Seeded fp16 weights (bit patterns as uint16) in llama2.c order."""
+    n = weights_numel(cfg, untied)
+    if n == 0:
+        raise LMError(LM_ERR_FORMAT, "synth_weights_f16")
+    out = np.empty(n, dtype=np.uint16)
+    rc = lib().lm_synth_weights_f16(C.byref(cfg), C.c_uint64(seed), std, int(untied), _u16p(out))
+    if rc:
+        raise LMError(rc, "lm_synth_weights_f16")
+    return out
+
+
+def weights_view(cfg: Config, buf: np.ndarray, untied: bool) -> LMWeights:
+    if buf.dtype == np.uint16:
+        dt = LM_DTYPE_F16
+    elif buf.dtype == np.float32:
+        dt = LM_DTYPE_F32
+    else:
+        raise TypeError("weights must be uint16 (fp16 bits) or float32")
+    if not buf.flags.c_contiguous:
+        raise ValueError("weights must be contiguous")
+    w = LMWeights()
+    rc = lib().lm_weights_view(C.byref(cfg), dt, buf.ctypes.data, int(untied), C.byref(w))
+    if rc:
+        raise LMError(rc, "lm_weights_view")
+    return w
+
+
+def f32_to_f16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().lm_f32_to_f16(_fp(a), _u16p(out), a.size)
+    return out
+
+
+def f16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().lm_f16_to_f32(_u16p(a), _fp(out), a.size)
+    return out
+
+
+def rope_table(max_seq: int, head_dim: int):
+    c = np.empty((max_seq, head_dim // 2), dtype=np.float32)
+    s = np.empty_like(c)
+    rc = lib().lm_rope_table(max_seq, head_dim, _fp(c), _fp(s))
+    if rc:
+        raise LMError(rc, "lm_rope_table")
+    return c, s
+
+
+def write_llama2c(path: str, cfg: Config, buf: np.ndarray, untied: bool) -> None:
+    w = weights_view(cfg, buf, untied)
+    rc = lib().lm_write_llama2c(path.encode(), C.byref(cfg), C.byref(w))
+    if rc:
+        raise LMError(rc, "lm_write_llama2c")
+
+
+def init() -> int:
+    return int(lib().lm_init())
+
+
+def device_info() -> dict:
+    info = LMDeviceInfo()
+    rc = lib().lm_device_info(C.byref(info))
+    if rc:
+        raise LMError(rc, "lm_device_info")
+    return dict(name=info.name.decode(), arch=info.arch.decode(), compute_units=info.compute_units,
+                clock_khz=info.clock_khz, l2_bytes=info.l2_bytes, total_mem=info.total_mem)
+
+
+def selftest_reduce(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size == 64
+    out = np.zeros(4, dtype=np.float32)
+    rc = lib().lm_selftest_reduce(_fp(x), _fp(out))
+    if rc:
+        raise LMError(rc, "lm_selftest_reduce")
+    return out
+
+
+class Model:
+    """Owning wrapper of an LMModel handle."""
+
+    def __init__(self, handle, cfg: Config):
+        self._h = handle
+        self.cfg = cfg
+        self.vocab = abs(cfg.vocab_size)
+
+    @classmethod
+    def create(cls, cfg: Config, weights: np.ndarray, untied: bool, max_batch: int, max_seq: int):
+        w = weights_view(cfg, weights, untied)
+        st = C.c_int(0)
+        h = lib().lm_create(C.byref(cfg), C.byref(w), max_batch, max_seq, C.byref(st))
+        if not h:
+            raise LMError(st.value, "lm_create")
+        return cls(h, cfg)
+
+    @classmethod
+    def load_llama2c(cls, path: str, max_batch: int, max_seq: int):
+        st = C.c_int(0)
+        h = lib().lm_load_llama2c(path.encode(), max_batch, max_seq, C.byref(st))
+        if not h:
+            raise LMError(st.value, "lm_load_llama2c")
+        cfg = Config()
+        lib().lm_get_config(h, C.byref(cfg))
+        return cls(h, cfg)
+
+    def close(self):
+        if self._h:
+            lib().lm_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc, what):
+        if rc:
+            raise LMError(rc, what)
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        p = lib().lm_forward(self._h, int(token), int(pos))
+        if not p:
+            raise LMError(LM_ERR_INVALID, "lm_forward")
+        return np.ctypeslib.as_array(p, shape=(self.vocab,)).copy()
+
+    def forward_batch(self, tokens, pos, want_logits=True):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        B = tokens.size
+        logits = np.empty((B, self.vocab), dtype=np.float32) if want_logits else None
+        am = np.empty(B, dtype=np.int32)
+        rc = lib().lm_forward_batch(self._h, _ip(tokens), _ip(pos), B,
+                                    _fp(logits) if logits is not None else None, _ip(am))
+        self._check(rc, "lm_forward_batch")
+        return logits, am
+
+    def prefill(self, tokens, slot=0, pos0=0, want_logits=True):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        S = tokens.size
+        logits = np.empty((S, self.vocab), dtype=np.float32) if want_logits else None
+        rc = lib().lm_prefill(self._h, slot, pos0, _ip(tokens), S,
+                              _fp(logits) if logits is not None else None)
+        self._check(rc, "lm_prefill")
+        return logits
+
+    def prefill_batch(self, tokens, slots=None, mode=LM_LOGITS_ALL, want_logits=True):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        nseq, S = tokens.shape
+        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.int32)
+        rows = nseq * S if mode == LM_LOGITS_ALL else nseq
+        logits = np.empty((rows, self.vocab), dtype=np.float32) if want_logits else None
+        rc = lib().lm_prefill_batch(self._h, nseq, _ip(sl) if sl is not None else None, _ip(tokens),
+                                    S, mode, _fp(logits) if logits is not None else None)
+        self._check(rc, "lm_prefill_batch")
+        return logits
+
+    def read_logits(self, row0, nrows):
+        out = np.empty((nrows, self.vocab), dtype=np.float32)
+        self._check(lib().lm_read_logits(self._h, row0, nrows, _fp(out)), "lm_read_logits")
+        return out
+
+    def generate_greedy(self, first_tokens, pos0, n_steps):
+        ft = np.ascontiguousarray(first_tokens, dtype=np.int32)
+        p0 = np.ascontiguousarray(pos0, dtype=np.int32)
+        B = ft.size
+        out = np.empty((n_steps, B), dtype=np.int32)
+        rc = lib().lm_generate_greedy(self._h, B, _ip(ft), _ip(p0), n_steps, _ip(out))
+        self._check(rc, "lm_generate_greedy")
+        return out
+
+    def set_option(self, opt, value):
+        self._check(lib().lm_set_option(self._h, opt, value), "lm_set_option")
+
+    def sync(self):
+        self._check(lib().lm_sync(self._h), "lm_sync")
+
+    def timer_begin(self):
+        self._check(lib().lm_timer_begin(self._h), "lm_timer_begin")
+
+    def timer_end(self) -> float:
+        ms = C.c_float(0)
+        self._check(lib().lm_timer_end(self._h, C.byref(ms)), "lm_timer_end")
+        return float(ms.value)

@@ -1,0 +1,255 @@
+/*
+ * stories_lm.h — C ABI of the MI355X (gfx950) Stories / Llama-2 token loop.
+ *
+ * Plain C types only: no HIP, no torch, no C++ in any signature.  One opaque
+ * handle (LMModel) owns every device buffer, one HIP stream and the captured
+ * per-step graphs.  Conventions follow libane's C ABI (libane/ane.h:95-231):
+ * opaque handle, NULL on failed creation with a status code, negative int
+ * status on failure, caller-owned host buffers, a message on stderr for every
+ * failure.  A handle is single-threaded and not re-entrant; distinct handles
+ * may be used from distinct threads.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   Config                  training/model.h:19-21 (= Llama2Config,
+ *                           training/stories_config.h:107-110)
+ *   LMWeights               weight members of Model, training/model.h:27-39
+ *   lm_init                 ane_init, libane/ane.h:97-100
+ *   lm_create               model_load_weights + model_compile_kernels,
+ *                           training/model.h:78-205; compile_fwd_kernels +
+ *                           weight staging, training/training_dynamic/generate.m:251-277,386-392
+ *   lm_load_llama2c         model_load_weights, training/model.h:78-164
+ *   lm_forward              the per-token body of generate.m:437-487 (KV-cache
+ *                           form of training/dashboard.py:205-267)
+ *   lm_forward_batch        the same step for B independent sequences
+ *   lm_prefill(_batch)      model_forward, training/forward.h:104-170
+ *   lm_generate_greedy      the greedy token loop, generate.m:427-516 with
+ *                           sample_argmax generate.m:129-136
+ *   lm_free                 ane_free, libane/ane.h:230-231
+ */
+#ifndef STORIES_LM_H
+#define STORIES_LM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Model configuration — the llama2.c file header, same field order
+ * (training/model.h:19-21).  In a llama2.c file a negative vocab_size marks an
+ * untied classifier that follows rms_final (training/model.h:85-86,155-160).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    int dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+} Config;
+
+typedef enum { LM_DTYPE_F32 = 0, LM_DTYPE_F16 = 1 } LMDType;
+
+/* Host weight buffers, one element type for all (fp32, or IEEE binary16 bit
+ * patterns stored as uint16).  Per-layer tensors are contiguous over layers in
+ * the llama2.c file order (training/model.h:94-160):
+ *   token_embedding [vocab, dim]          rms_att_w [L, dim]
+ *   wq [L, n_heads*hd, dim]               wk, wv [L, n_kv_heads*hd, dim]
+ *   wo [L, dim, n_heads*hd]               rms_ffn_w [L, dim]
+ *   w1 [L, hidden, dim]  w2 [L, dim, hidden]  w3 [L, hidden, dim]
+ *   rms_final_w [dim]                     wcls [vocab, dim] (NULL = tied)
+ * Every matrix is W[out, in] row-major: y = W x (training/forward.h:35-44).
+ * fp32 input is rounded to fp16 (round-to-nearest-even) on upload. */
+typedef struct {
+    LMDType dtype;
+    const void *token_embedding;
+    const void *rms_att_w;
+    const void *wq, *wk, *wv, *wo;
+    const void *rms_ffn_w;
+    const void *w1, *w2, *w3;
+    const void *rms_final_w;
+    const void *wcls;
+} LMWeights;
+
+typedef struct LMModel LMModel;
+
+/* Status codes.  0 / -1 / -2 keep ane_init's meaning (libane/ane.h:99). */
+#define LM_OK               0
+#define LM_ERR_NO_DEVICE   (-1)   /* no HIP device visible                        */
+#define LM_ERR_NOT_GFX950  (-2)   /* device present but not gfx950 (CDNA4)        */
+#define LM_ERR_INVALID     (-3)   /* NULL handle / pointer, bad count             */
+#define LM_ERR_OOM         (-4)   /* host or device allocation failed             */
+#define LM_ERR_HIP         (-5)   /* a HIP runtime call failed                    */
+#define LM_ERR_IO          (-6)   /* file open / read / write failed              */
+#define LM_ERR_FORMAT      (-7)   /* truncated or inconsistent weight file        */
+#define LM_ERR_RANGE       (-8)   /* token, position, slot or length out of range */
+#define LM_ERR_UNSUPPORTED (-9)   /* shape outside what the kernels are built for */
+#define LM_ERR_NOT_INIT    (-10)  /* lm_init was not called or failed             */
+
+/* Human-readable text for a status code (static storage). */
+const char *lm_strerror(int status);
+
+/* ---------------------------------------------------------------------------
+ * Device
+ * ------------------------------------------------------------------------- */
+
+/* Select device 0 and check it is gfx950.  0 on success, LM_ERR_NO_DEVICE,
+ * LM_ERR_NOT_GFX950.  Idempotent.  Replaces ane_init (libane/ane.h:97-100). */
+int lm_init(void);
+
+typedef struct {
+    char name[64];          /* marketing name from the runtime         */
+    char arch[32];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int  compute_units;
+    int  clock_khz;
+    int  l2_bytes;
+    size_t total_mem;
+} LMDeviceInfo;
+
+/* Fill *out for device 0.  Replaces ane_device_info (libane/ane.h:108-109). */
+int lm_device_info(LMDeviceInfo *out);
+
+/* ---------------------------------------------------------------------------
+ * Model lifetime
+ * ------------------------------------------------------------------------- */
+
+/* Build a device model from host weights.  The weights are copied (fp16 on
+ * device); the caller keeps ownership of *w.  max_batch sequences ("slots") of
+ * up to max_seq positions each get an fp16 KV cache.  Requires dim % 64 == 0,
+ * head_dim in {64, 128}, hidden_dim % 64 == 0, n_heads % n_kv_heads == 0.
+ * Returns NULL and sets *status (if non-NULL) on failure. */
+LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch,
+                   int max_seq, int *status);
+
+/* Read a llama2.c model file (fp32 values, header as Config, file order of
+ * training/model.h:78-164, negative vocab_size = untied) and lm_create it.
+ * Truncated files and inconsistent headers fail with LM_ERR_FORMAT. */
+LMModel *lm_load_llama2c(const char *path, int max_batch, int max_seq,
+                         int *status);
+
+/* Release every host and device resource of the handle.  NULL is a no-op. */
+void lm_free(LMModel *m);
+
+/* Copy the model's Config (vocab_size always positive) into *out. */
+int lm_get_config(const LMModel *m, Config *out);
+
+/* ---------------------------------------------------------------------------
+ * Forward
+ * ------------------------------------------------------------------------- */
+
+/* One decode step of slot 0: embed `token` at position `pos`, append its K/V
+ * to the cache, attend over positions 0..pos, return the vocab_size fp32
+ * logits.  The pointer is an internal host buffer valid until the next call on
+ * the handle; NULL on error (message on stderr).  Positions 0..pos-1 of slot 0
+ * must have been filled by earlier steps or by lm_prefill. */
+const float *lm_forward(LMModel *m, int token, int pos);
+
+/* One decode step for B sequences: row b uses KV slot b, token tokens[b] at
+ * position pos[b].  logits (B x vocab, may be NULL) and argmax (B, may be NULL;
+ * lowest index on ties, generate.m:129-136) are host buffers. */
+int lm_forward_batch(LMModel *m, const int *tokens, const int *pos, int B,
+                     float *logits, int *argmax);
+
+/* Causal forward of S tokens of one sequence at positions pos0..pos0+S-1 into
+ * KV slot `slot` (positions < pos0 must already be cached).  Writes the S x
+ * vocab_size fp32 logits to `logits` when non-NULL; they always stay readable
+ * on the device through lm_read_logits until the next forward call. */
+int lm_prefill(LMModel *m, int slot, int pos0, const int *tokens, int S,
+               float *logits);
+
+/* nseq independent sequences of S tokens each from position 0, sequence i
+ * into KV slot slots[i] (slots NULL = 0..nseq-1); tokens is nseq x S row-major.
+ * logits_mode LM_LOGITS_ALL computes all nseq*S logit rows (the training-shape
+ * forward, training/forward.h:104-170); LM_LOGITS_LAST only the last row of
+ * each sequence (what a decode that follows needs).  `logits` (host, may be
+ * NULL) receives nseq*S or nseq rows.  Rows go through the GEMMs together, in
+ * chunks of whole sequences when nseq*S exceeds the handle's row capacity; the
+ * device keeps the last chunk's logits for lm_read_logits. */
+#define LM_LOGITS_ALL  0
+#define LM_LOGITS_LAST 1
+int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens,
+                     int S, int logits_mode, float *logits);
+
+/* Copy rows [row0, row0+nrows) of the last forward's device logits to dst. */
+int lm_read_logits(LMModel *m, int row0, int nrows, float *dst);
+
+/* Greedy decode of n_steps tokens for B sequences (slot b), entirely on the
+ * device: step t feeds the argmax of step t-1 back as the next token without
+ * a host round trip (one captured graph replayed per step).  Sequence b starts
+ * from first_tokens[b] at position pos0[b] (earlier positions already cached);
+ * out_tokens (n_steps x B, row-major by step) receives the generated ids.
+ * EOS is not a stop condition here (every step is run); callers that want
+ * generate.m's EOS break (generate.m:501) scan out_tokens. */
+int lm_generate_greedy(LMModel *m, int B, const int *first_tokens,
+                       const int *pos0, int n_steps, int *out_tokens);
+
+/* ---------------------------------------------------------------------------
+ * Timing on the model's stream (hipEvents), for benchmarks
+ * ------------------------------------------------------------------------- */
+
+/* Block until all work queued on the handle's stream is done. */
+int lm_sync(LMModel *m);
+
+/* Record a start event on the handle's stream. */
+int lm_timer_begin(LMModel *m);
+
+/* Record a stop event, wait for it, return elapsed ms since lm_timer_begin. */
+int lm_timer_end(LMModel *m, float *ms);
+
+/* Execution knobs.  LM_OPT_DECODE_PATH selects the B=1 decode step: 0 = auto,
+ * 1 = chain of per-op kernels, 2 = persistent single-kernel step.
+ * LM_OPT_USE_GRAPH: 1 (default) replays captured hipGraphs, 0 launches
+ * kernels directly (debugging / per-kernel timing). */
+#define LM_OPT_DECODE_PATH 1
+#define LM_OPT_USE_GRAPH   2
+/* LM_OPT_KV_F32: 1 stores the K/V cache in fp32 (the reference forward keeps
+ * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
+ * Changing it reallocates and clears the cache of every slot. */
+#define LM_OPT_KV_F32      3
+int lm_set_option(LMModel *m, int option, int value);
+
+/* ---------------------------------------------------------------------------
+ * Weight utilities (host only, no device needed)
+ * ------------------------------------------------------------------------- */
+
+/* Number of scalars in the llama2.c-ordered weight set of cfg (untied adds a
+ * classifier of vocab x dim).  Uses |vocab_size|. */
+size_t lm_weights_numel(const Config *cfg, int untied);
+
+/* Point *out at the tensors of a contiguous llama2.c-ordered buffer `base` of
+ * element type dtype (fp32 or fp16 bits).  untied=0 makes wcls NULL (tied). */
+int lm_weights_view(const Config *cfg, LMDType dtype, const void *base,
+                    int untied, LMWeights *out);
+
+/* Fill a contiguous fp16 buffer (lm_weights_numel(cfg, untied) elements, file
+ * order) with seeded weights: every matrix entry is round-to-nearest-even fp16
+ * of std * N(0,1), the normal drawn by Box-Muller from SplitMix64 counters keyed
+ * by (seed, tensor index, element index); norm gains are exactly 1.0.  The
+ * result is identical for any thread count. */
+int lm_synth_weights_f16(const Config *cfg, uint64_t seed, float std,
+                         int untied, uint16_t *out);
+
+/* Write a llama2.c file (fp32 values; vocab_size written negative when
+ * w->wcls is non-NULL and distinct from the embedding). */
+int lm_write_llama2c(const char *path, const Config *cfg, const LMWeights *w);
+
+/* IEEE binary16 <-> binary32 (round to nearest, ties to even). */
+void lm_f32_to_f16(const float *src, uint16_t *dst, size_t n);
+void lm_f16_to_f32(const uint16_t *src, float *dst, size_t n);
+
+/* The fp32 RoPE rotation table used on the device, built on the host with the
+ * reference's expressions (training/forward.h:58-61): for position p and pair
+ * i (i = 0..head_dim/2-1), freq = 1/powf(10000, 2i/head_dim), angle = p*freq,
+ * cos_out[p*(hd/2)+i] = cosf(angle), sin_out[...] = sinf(angle). */
+int lm_rope_table(int max_seq, int head_dim, float *cos_out, float *sin_out);
+
+/* ---------------------------------------------------------------------------
+ * Diagnostics (no counterpart in the reference)
+ * ------------------------------------------------------------------------- */
+
+/* Run the device wave-reduction self-test on 64 inputs: out4 = {sum of lanes
+ * 0..31, sum of lanes 32..63, wave sum (DPP), wave sum (shuffles)}. */
+int lm_selftest_reduce(const float *in64, float *out4);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STORIES_LM_H */

@@ -1,0 +1,72 @@
+"""Write the committed golden fixtures of the token loop.
+
+The reference commits no numeric fixtures and cannot run here (its forward
+needs Apple frameworks), so the fixtures are produced by the CPU oracle
+(oracle/oracle.c, a restatement of training/forward.h:36-184) after that oracle
+has been pinned by the closed-form checks in tests/test_oracle_kat.py.  They
+freeze the oracle's outputs on seeded weights so later changes to the oracle or
+to the device path are caught, and so GPU tests need no long CPU runs.
+
+  tiny_*.npz       tiny configs: full-forward logits of 40 seeded tokens
+                   (fp32 K/V and binary16 K/V), greedy ids from token 1
+  stories_c0.npz   Stories-110M config C0 (seed 1, N(0,0.02) fp16 weights,
+                   untied classifier): 256 greedy ids from token 1 at positions
+                   0..255 with fp32 K/V and with binary16 K/V, and per step the
+                   top-32 (logit, id) pairs plus logit sum / sum of squares.
+
+Run:  python tests/golden/make_fixtures.py   (about a minute on 8 cores)
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path[:0] = [os.path.join(ROOT, "ane-training_amd"), os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
+
+import oracle as O  # noqa: E402
+import stories_lm as S  # noqa: E402
+from conftest import TINY, TINY_GQA, TINY_HD128, cfg7  # noqa: E402
+
+TOPK = 32
+
+
+def tiny(name, d, seed):
+    cfg = S.make_config(**d)
+    w16 = S.synth_weights_f16(cfg, seed, 0.02, True)
+    w32 = S.f16_to_f32(w16)
+    toks = np.random.default_rng(seed).integers(0, d["vocab_size"], 40).astype(np.int32)
+    out = dict(cfg=np.array(cfg7(d), np.int32), seed=np.int64(seed), tokens=toks)
+    for kv in (0, 1):
+        o = O.Oracle(cfg7(d), w32, True, d["seq_len"], kv_f16=bool(kv))
+        out[f"logits_kv{16 if kv else 32}"] = o.forward_full(toks)
+        o2 = O.Oracle(cfg7(d), w32, True, d["seq_len"], kv_f16=bool(kv))
+        out[f"greedy_kv{16 if kv else 32}"] = o2.greedy(1, 0, 48)
+    np.savez_compressed(os.path.join(HERE, f"tiny_{name}.npz"), **out)
+    print("wrote", name)
+
+
+def stories_c0():
+    cfg = S.make_config(**S.STORIES_110M)
+    w32 = S.f16_to_f32(S.synth_weights_f16(cfg, 1, 0.02, True))
+    out = dict(seed=np.int64(1), n_steps=np.int32(256), first_token=np.int32(1))
+    for kv in (0, 1):
+        o = O.Oracle(cfg7(S.STORIES_110M), w32, True, 256, kv_f16=bool(kv))
+        ids, lg = o.greedy(1, 0, 256, want_logits=True)
+        idx = np.argsort(-lg, axis=1, kind="stable")[:, :TOPK].astype(np.int32)
+        tag = "kv16" if kv else "kv32"
+        out[f"ids_{tag}"] = ids
+        out[f"top_idx_{tag}"] = idx
+        out[f"top_val_{tag}"] = np.take_along_axis(lg, idx, axis=1).astype(np.float32)
+        out[f"sum_{tag}"] = lg.astype(np.float64).sum(1)
+        out[f"sumsq_{tag}"] = (lg.astype(np.float64) ** 2).sum(1)
+    np.savez_compressed(os.path.join(HERE, "stories_c0.npz"), **out)
+    print("wrote stories_c0")
+
+
+if __name__ == "__main__":
+    tiny("mha", TINY, 11)
+    tiny("gqa", TINY_GQA, 12)
+    tiny("hd128", TINY_HD128, 13)
+    stories_c0()

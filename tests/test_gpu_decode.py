@@ -1,0 +1,177 @@
+"""Decode path on the GPU against the oracle (through the C ABI).
+
+Tolerances: with the K/V cache in the oracle's precision only the summation
+order differs (measured <= 6e-6 on Stories logits), so logits must agree to
+atol 1e-4 and greedy ids exactly.  Against the fp32-cache oracle (the
+reference's own forward) a binary16 cache is held to the north-star bound,
+atol 2e-2 + rtol 1e-2.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, TINY, TINY_GQA, TINY_HD128, cfg7
+
+pytestmark = pytest.mark.gpu
+
+TIGHT = dict(rtol=1e-4, atol=1e-4)
+NORTH_STAR = dict(rtol=1e-2, atol=2e-2)
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def make(lm, d, seed, max_batch, max_seq, kv32):
+    cfg = lm.make_config(**d)
+    w16 = lm.synth_weights_f16(cfg, seed, 0.02, True)
+    m = lm.Model.create(cfg, w16, True, max_batch, max_seq)
+    if kv32:
+        m.set_option(lm.LM_OPT_KV_F32, 1)
+    return m, w16
+
+
+def test_dpp_wave_reductions(lm):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(64).astype(np.float32)
+    out = lm.selftest_reduce(x)
+    x64 = x.astype(np.float64)
+    assert abs(out[0] - x64[:32].sum()) < 1e-5
+    assert abs(out[1] - x64[32:].sum()) < 1e-5
+    assert abs(out[2] - x64.sum()) < 1e-5 and abs(out[3] - x64.sum()) < 1e-5
+
+
+@pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
+@pytest.mark.parametrize("kv", [32, 16])
+def test_tiny_decode_steps_match_oracle(lm, name, d, kv):
+    _say(f"[tiny decode {name} kv{kv}]")
+    fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
+    m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
+    got = np.stack([m.forward(int(t), p) for p, t in enumerate(fx["tokens"])])
+    np.testing.assert_allclose(got, fx[f"logits_kv{kv}"], **TIGHT)
+    np.testing.assert_allclose(got, fx["logits_kv32"], **NORTH_STAR)
+    g = m.generate_greedy([1], [0], 48)[:, 0]
+    assert np.array_equal(g, fx[f"greedy_kv{kv}"])
+    m.close()
+
+
+@pytest.mark.parametrize("B", [2, 3, 4])
+def test_tiny_batch_decode_matches_oracle(lm, orc, B):
+    """B slots in one batched step, first in lock-step, then at different
+    positions (slot b advances every b+1 steps; a repeated (token, pos) step
+    rewrites the same cache entry)."""
+    _say(f"[tiny batch decode B={B}]")
+    d = TINY
+    m, w16 = make(lm, d, 21, B, 64, True)
+    w32 = lm.f16_to_f32(w16)
+    seqs = np.random.default_rng(B).integers(0, d["vocab_size"], (B, 40)).astype(np.int32)
+    orcs = [orc.Oracle(cfg7(d), w32, True, 64) for _ in range(B)]
+    plan = [np.full(B, p, np.int32) for p in range(10)]
+    plan += [np.array([10 + t // (b + 1) for b in range(B)], np.int32) for t in range(12)]
+    for pos in plan:
+        toks = seqs[np.arange(B), pos]
+        lg, am = m.forward_batch(toks, pos)
+        for b in range(B):
+            ref = orcs[b].decode_step(int(toks[b]), int(pos[b]))
+            np.testing.assert_allclose(lg[b], ref, **TIGHT)
+            assert am[b] == orc.argmax(ref)
+    m.close()
+
+
+def test_batch_slots_are_independent(lm):
+    _say("[slot independence]")
+    d = TINY
+    m, _ = make(lm, d, 22, 4, 64, False)
+    rng = np.random.default_rng(9)
+    toks = rng.integers(0, d["vocab_size"], (4, 12)).astype(np.int32)
+    rows = []
+    for p in range(12):
+        lg, _ = m.forward_batch(toks[:, p], np.full(4, p, np.int32))
+        rows.append(lg)
+    m1, _ = make(lm, d, 22, 1, 64, False)
+    for p in range(12):
+        lg1 = m1.forward(int(toks[2, p]), p)
+        np.testing.assert_allclose(rows[p][2], lg1, rtol=0, atol=1e-5)
+    m.close()
+    m1.close()
+
+
+def test_host_validation_errors(lm):
+    d = TINY
+    m, _ = make(lm, d, 23, 2, 32, False)
+    with pytest.raises(lm.LMError) as e:
+        m.forward_batch([0, 600], [0, 0])          # token >= vocab
+    assert e.value.status == lm.LM_ERR_RANGE
+    with pytest.raises(lm.LMError) as e:
+        m.forward_batch([0, 1], [0, 32])           # pos >= max_seq
+    assert e.value.status == lm.LM_ERR_RANGE
+    with pytest.raises(lm.LMError) as e:
+        m.forward_batch([0, 1, 2], [0, 0, 0])      # B > max_batch
+    assert e.value.status == lm.LM_ERR_RANGE
+    with pytest.raises(lm.LMError) as e:
+        m.generate_greedy([1], [30], 5)            # runs past max_seq
+    assert e.value.status == lm.LM_ERR_RANGE
+    with pytest.raises(lm.LMError):
+        m.forward(-1, 0)
+    m.close()
+
+
+def _stories(lm, kv32):
+    return make(lm, lm.STORIES_110M, 1, 1, 256, kv32)
+
+
+def test_stories_c0_greedy_ids_fp32_cache(lm):
+    """Config 0: 256 greedy tokens from id 1 == the reference forward's ids."""
+    _say("[stories C0 greedy kv32]")
+    fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
+    m, _ = _stories(lm, True)
+    ids = m.generate_greedy([1], [0], 256)[:, 0]
+    bad = np.where(ids != fx["ids_kv32"])[0]
+    assert bad.size == 0, f"first divergence at step {bad[:5]}"
+    m.close()
+
+
+def test_stories_c0_greedy_ids_fp16_cache(lm):
+    _say("[stories C0 greedy kv16]")
+    fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
+    m, _ = _stories(lm, False)
+    ids = m.generate_greedy([1], [0], 256)[:, 0]
+    bad = np.where(ids != fx["ids_kv16"])[0]
+    assert bad.size == 0, f"first divergence at step {bad[:5]}"
+    m.close()
+
+
+@pytest.mark.parametrize("kv", [32, 16])
+def test_stories_c0_teacher_forced_logits(lm, kv):
+    """Teacher-forced on the reference trajectory: top-32 logits and row moments."""
+    _say(f"[stories C0 teacher forced kv{kv}]")
+    fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
+    m, _ = _stories(lm, kv == 32)
+    ids = fx["ids_kv32"]
+    inputs = np.concatenate([[1], ids[:-1]])
+    tol = TIGHT if kv == 32 else NORTH_STAR
+    for p, t in enumerate(inputs):
+        lg = m.forward(int(t), p)
+        np.testing.assert_allclose(np.take_along_axis(lg, fx["top_idx_kv32"][p], 0), fx["top_val_kv32"][p], **tol)
+        assert abs(lg.astype(np.float64).sum() - fx["sum_kv32"][p]) < (1e-1 if kv == 32 else 5.0)
+        assert abs((lg.astype(np.float64) ** 2).sum() - fx["sumsq_kv32"][p]) < 1e-3 * fx["sumsq_kv32"][p]
+    m.close()
+
+
+def test_graph_replay_equals_direct_launches(lm):
+    _say("[graph vs direct]")
+    d = TINY_HD128
+    m, _ = make(lm, d, 24, 2, 64, False)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, d["vocab_size"], (2, 16)).astype(np.int32)
+    a = [m.forward_batch(toks[:, p], np.full(2, p, np.int32))[0] for p in range(16)]
+    m2, _ = make(lm, d, 24, 2, 64, False)
+    m2.set_option(lm.LM_OPT_USE_GRAPH, 0)
+    b = [m2.forward_batch(toks[:, p], np.full(2, p, np.int32))[0] for p in range(16)]
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    m.close()
+    m2.close()

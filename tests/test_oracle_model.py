@@ -1,0 +1,87 @@
+"""The oracle's full model: self-consistency, an independent fp64 forward, and
+the committed fixtures (which GPU tests compare against)."""
+import os
+
+import numpy as np
+import pytest
+
+import numpy_ref
+from conftest import GOLDEN, TINY, TINY_GQA, TINY_HD128, cfg7
+
+
+def _weights(lm, d, seed, untied=True, random_gains=False):
+    cfg = lm.make_config(**d)
+    w = lm.f16_to_f32(lm.synth_weights_f16(cfg, seed, 0.02, untied))
+    if random_gains:
+        rng = np.random.default_rng(seed)
+        view = lm.weights_view(cfg, w, untied)
+        base = w.ctypes.data
+        D, L = d["dim"], d["n_layers"]
+        for ptr, n in ((view.rms_att_w, L * D), (view.rms_ffn_w, L * D), (view.rms_final_w, D)):
+            off = (ptr - base) // 4
+            w[off:off + n] = rng.uniform(0.6, 1.4, n).astype(np.float32)
+    return w
+
+
+@pytest.mark.parametrize("d", [TINY, TINY_GQA, TINY_HD128], ids=["mha", "gqa", "hd128"])
+@pytest.mark.parametrize("kv16", [False, True])
+def test_full_forward_equals_kv_decode_bitwise(lm, orc, d, kv16):
+    w = _weights(lm, d, 5)
+    toks = np.random.default_rng(5).integers(0, d["vocab_size"], 33)
+    full = orc.Oracle(cfg7(d), w, True, 64, kv_f16=kv16).forward_full(toks)
+    dec = orc.Oracle(cfg7(d), w, True, 64, kv_f16=kv16)
+    rows = np.stack([dec.decode_step(int(t), i) for i, t in enumerate(toks)])
+    assert np.array_equal(full, rows)
+
+
+def test_causality(lm, orc):
+    w = _weights(lm, TINY, 6)
+    o = orc.Oracle(cfg7(TINY), w, True, 64)
+    toks = np.random.default_rng(6).integers(0, 512, 20)
+    a = o.forward_full(toks)
+    toks2 = toks.copy()
+    toks2[12] = (toks2[12] + 1) % 512
+    b = o.forward_full(toks2)
+    assert np.array_equal(a[:12], b[:12]) and not np.array_equal(a[12:], b[12:])
+
+
+@pytest.mark.parametrize("d", [TINY, TINY_GQA, TINY_HD128], ids=["mha", "gqa", "hd128"])
+@pytest.mark.parametrize("untied", [True, False])
+def test_oracle_matches_independent_fp64_forward(lm, orc, d, untied):
+    w = _weights(lm, d, 7, untied=untied, random_gains=True)
+    toks = np.random.default_rng(7).integers(0, d["vocab_size"], 24)
+    got = orc.Oracle(cfg7(d), w, untied, 64).forward_full(toks)
+    ref = numpy_ref.forward(cfg7(d), w, untied, toks)
+    assert np.allclose(got, ref, rtol=0, atol=2e-5), np.abs(got - ref).max()
+
+
+def test_kv16_emulation_is_close_not_identical(lm, orc):
+    w = _weights(lm, TINY, 8)
+    toks = np.random.default_rng(8).integers(0, 512, 30)
+    a = orc.Oracle(cfg7(TINY), w, True, 64).forward_full(toks)
+    b = orc.Oracle(cfg7(TINY), w, True, 64, kv_f16=True).forward_full(toks)
+    d = np.abs(a - b).max()
+    assert 0 < d < 5e-3
+
+
+@pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
+def test_oracle_reproduces_tiny_fixtures(lm, orc, name, d):
+    fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
+    assert tuple(fx["cfg"]) == cfg7(d)
+    w = _weights(lm, d, int(fx["seed"]))
+    for kv in (32, 16):
+        o = orc.Oracle(cfg7(d), w, True, d["seq_len"], kv_f16=(kv == 16))
+        assert np.array_equal(o.forward_full(fx["tokens"]), fx[f"logits_kv{kv}"])
+        o = orc.Oracle(cfg7(d), w, True, d["seq_len"], kv_f16=(kv == 16))
+        assert np.array_equal(o.greedy(1, 0, 48), fx[f"greedy_kv{kv}"])
+
+
+@pytest.mark.slow
+def test_oracle_reproduces_stories_c0_fixture(lm, orc):
+    fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
+    cfg = lm.make_config(**lm.STORIES_110M)
+    w = lm.f16_to_f32(lm.synth_weights_f16(cfg, int(fx["seed"]), 0.02, True))
+    o = orc.Oracle(cfg7(lm.STORIES_110M), w, True, 256)
+    ids, lg = o.greedy(1, 0, 256, want_logits=True)
+    assert np.array_equal(ids, fx["ids_kv32"])
+    assert np.array_equal(np.take_along_axis(lg, fx["top_idx_kv32"], 1), fx["top_val_kv32"])
