@@ -1,23 +1,27 @@
 /*
- * k_decode.hip — per-op decode kernels for small batches (B <= 4), gfx950.
+ * k_decode.hip — small-batch (B <= 4) decode kernels for gfx950.
  *
  * One decode step of one layer is five launches, shaped after the reference's
- * fused forward programs (training/training_dynamic/mil_dynamic.h:56-288) but
- * cut where a full-vector dependency forces a grid-wide boundary:
+ * fused forward programs (training/training_dynamic/mil_dynamic.h:56-288) and
+ * cut only where every output needs the whole of the previous vector:
  *   qkv_rope   rmsnorm prologue (forward.h:46-53) + [Wq;Wk;Wv] GEMV
- *              (forward.h:122-124) + interleaved RoPE (forward.h:55-70) + KV append
- *   attn       split-KV causal attention over the fp16 cache (forward.h:72-99)
- *   wo         split merge + Wo GEMV + residual (forward.h:134-136)
+ *              (forward.h:122-124) + interleaved RoPE (forward.h:55-70) + KV
+ *              append; layer 0 also gathers the embedding row (forward.h:108-110)
+ *   attn       causal attention of one (sequence, head) per work-group over the
+ *              cached positions 0..pos (forward.h:72-99)
+ *   wo         Wo GEMV + residual (forward.h:134-136)
  *   ffn13      rmsnorm prologue + W1/W3 GEMV + SiLU gate (forward.h:139-151)
  *   w2         W2 GEMV + residual (forward.h:157-159)
- * and per token embed (forward.h:108-110), classifier + argmax partials
- * (forward.h:163-170, generate.m:474-493) and the argmax merge.
+ * and per token the classifier (forward.h:163-170) with per-work-group argmax
+ * partials, and their reduction (generate.m:129-136, 474-493).
  *
  * GEMV mapping: a wave owns a pair of weight rows, each 32-lane half one row;
- * a lane streams 16-byte (8 x fp16) chunks (c*32 + lane) of its row, multiplies
- * against the fp32 activation held in LDS and the half-wave sum is formed with
- * DPP.  Pairs line up with RoPE pairs (rows 2i, 2i+1) and with the gate pairs
- * (row i of W1 in half 0, row i of W3 in half 1).
+ * a lane streams 16-byte (8 x fp16) chunks (c*32 + lane) of its row.  Every
+ * kernel issues its weight loads first, before it reads the activation vector
+ * that the previous launch produced, so the HBM latency of the weights overlaps
+ * the prologue.  The fp32 activation vector is staged in LDS and the half-wave
+ * sums are formed with DPP.  Pairs line up with RoPE pairs (rows 2i, 2i+1) and
+ * with the gate pairs (row i of W1 in half 0, row i of W3 in half 1).
  */
 #include "k_common.h"
 #include "lm_internal.h"
@@ -27,25 +31,71 @@
 
 /* ---- prologues ---------------------------------------------------------- */
 
-/* xs[b*K + i] = x[b*K + i] * (1/sqrt(mean(x_b^2) + 1e-5)) * w[i] for b < B,
- * zero rows for B <= b < NB (forward.h:46-53). */
+/* Every global load of a prologue is issued up front (K / WG is a compile-time
+ * trip count), so a prologue costs one memory latency, which the weight loads
+ * issued before it also cover. */
+
+/* Raw input rows of a normalising prologue, loaded into registers: src_b is
+ * x[b*K ..] (fp32) or, when emb != NULL, the fp16 embedding row emb[tok[b]*K ..];
+ * rows B <= b < NB are zero.  wv holds the gain w[i] of this thread's columns. */
 template <int K, int NB>
-__device__ __forceinline__ void rmsnorm_to_lds(const float *__restrict__ x,
-                                               const float *__restrict__ w, int B,
-                                               float *xs)
+struct NormIn {
+    float v[NB][K / WG];
+    float w[K / WG];
+};
+
+template <int K, int NB>
+__device__ __forceinline__ void norm_load(const float *__restrict__ x, const u16 *__restrict__ emb,
+                                          const int *__restrict__ tok, const float *__restrict__ w,
+                                          int B, NormIn<K, NB> &in)
 {
+    constexpr int PER = K / WG;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < PER; j++) in.w[j] = w[tid + j * WG];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (b < B) {
+            if (emb) {
+                const u16 *er = emb + (size_t)tok[b] * K;
+#pragma unroll
+                for (int j = 0; j < PER; j++) in.v[b][j] = h2f(er[tid + j * WG]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < PER; j++) in.v[b][j] = x[(size_t)b * K + tid + j * WG];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER; j++) in.v[b][j] = 0.f;
+        }
+    }
+}
+
+/* xs[b*K + i] = src_b[i] * (1/sqrt(mean(src_b^2) + 1e-5)) * w[i]
+ * (forward.h:46-53).  With store_x, work-group 0 also writes the raw rows to x
+ * (the residual stream starts as the embedding). */
+template <int K, int NB>
+__device__ __forceinline__ void norm_to_lds(const NormIn<K, NB> &in, int B, float *__restrict__ x,
+                                            bool store_x, float *xs)
+{
+    constexpr int PER = K / WG;
     __shared__ float red[NB][NWAVE];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         float ss = 0.f;
-        for (int i = tid; i < K; i += WG) {
-            float v = b < B ? x[(size_t)b * K + i] : 0.f;
-            xs[b * K + i] = v;
-            ss = fmaf(v, v, ss);
-        }
+#pragma unroll
+        for (int j = 0; j < PER; j++) ss = fmaf(in.v[b][j], in.v[b][j], ss);
         ss = wave_sum(ss);
         if (lane == 0) red[b][wv] = ss;
+    }
+    if (store_x && blockIdx.x == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if (b < B) {
+#pragma unroll
+                for (int j = 0; j < PER; j++) x[(size_t)b * K + tid + j * WG] = in.v[b][j];
+            }
     }
     __syncthreads();
 #pragma unroll
@@ -53,36 +103,59 @@ __device__ __forceinline__ void rmsnorm_to_lds(const float *__restrict__ x,
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NWAVE; i++) tot += red[b][i];
-        float scale = 1.0f / sqrtf(tot / K + 1e-5f);
-        for (int i = tid; i < K; i += WG) xs[b * K + i] = xs[b * K + i] * scale * w[i];
+        const float scale = 1.0f / sqrtf(tot / K + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < PER; j++) xs[b * K + tid + j * WG] = in.v[b][j] * scale * in.w[j];
     }
     __syncthreads();
 }
 
+/* NB rows of K fp32 from src (rows >= B zero), loaded into registers. */
 template <int K, int NB>
-__device__ __forceinline__ void rows_to_lds(const float *__restrict__ src, int B, float *xs)
+struct RowsIn {
+    float v[NB][K / WG];
+};
+
+template <int K, int NB>
+__device__ __forceinline__ void rows_load(const float *__restrict__ src, int B, RowsIn<K, NB> &in)
 {
-    for (int i = threadIdx.x; i < NB * K; i += WG) xs[i] = (i / K) < B ? src[i] : 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < K / WG; j++)
+            in.v[b][j] = b < B ? src[(size_t)b * K + threadIdx.x + j * WG] : 0.f;
+}
+
+template <int K, int NB>
+__device__ __forceinline__ void rows_to_lds(const RowsIn<K, NB> &in, float *xs)
+{
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < K / WG; j++) xs[b * K + threadIdx.x + j * WG] = in.v[b][j];
     __syncthreads();
 }
 
 /* ---- GEMV core ------------------------------------------------------------ */
 
-/* Half-wave dot products of one fp16 row (length K) with NB fp32 vectors in
- * LDS.  hl = lane within the half (0..31); acc[b] is this lane's partial. */
+/* Issue the loads of one fp16 row (length K) for half-wave lane hl. */
+template <int K>
+__device__ __forceinline__ void hw_load(const u16 *__restrict__ wrow, int hl, uint4 wv[K / 256])
+{
+#pragma unroll
+    for (int c = 0; c < K / 256; c++)
+        wv[c] = *(const uint4 *)(wrow + (size_t)(c * 32 + hl) * 8);
+}
+
+/* Half-wave partial dot products of a prefetched row with NB fp32 LDS rows. */
 template <int K, int NB>
-__device__ __forceinline__ void hw_dot(const u16 *__restrict__ wrow, const float *xs, int hl,
+__device__ __forceinline__ void hw_dot(const uint4 wv[K / 256], const float *xs, int hl,
                                        float acc[NB])
 {
-    constexpr int CPL = K / 256;
-    uint4 wv[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; c++)
-        wv[c] = *(const uint4 *)(wrow + (size_t)(c * 32 + hl) * 8);
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[b] = 0.f;
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
+    for (int c = 0; c < K / 256; c++) {
         float w[8];
         unpack8(wv[c], w);
         const int k0 = (c * 32 + hl) * 8;
@@ -113,93 +186,117 @@ __device__ __forceinline__ void pair_reduce(const float acc[NB], float r0[NB], f
     }
 }
 
-/* ---- embed ----------------------------------------------------------------- */
-
-__global__ void __launch_bounds__(WG) k_embed(const u16 *__restrict__ E, const int *__restrict__ tok,
-                                              float *__restrict__ x, int D)
-{
-    const int b = blockIdx.y;
-    const int t = tok[b];
-    for (int i = blockIdx.x * WG + threadIdx.x; i < D; i += gridDim.x * WG)
-        x[(size_t)b * D + i] = h2f(E[(size_t)t * D + i]);
-}
-
 /* ---- QKV + RoPE + KV append ------------------------------------------------ */
 
 template <int D, int NB, typename KT>
 __global__ void __launch_bounds__(WG) k_qkv_rope(
-    const float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W,
-    int NQ, int NKV, int hd, const float *__restrict__ rc, const float *__restrict__ rs,
-    const int *__restrict__ pos, int B, float *__restrict__ q, KT *__restrict__ kc,
-    KT *__restrict__ vc, int max_seq, int npairs)
+    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
+    const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV, int hd,
+    const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
+    int B, float *__restrict__ q, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq,
+    int npairs)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
-    rmsnorm_to_lds<D, NB>(x, rms_w, B, xs);
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
-    if (p >= npairs) return;
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
-    const int r = 2 * p;
+    const int r = 2 * min(p, npairs - 1);
+    uint4 wv[D / 256];
+    hw_load<D>(W + (size_t)(r + half) * D, hl, wv);
+    NormIn<D, NB> in;
+    norm_load<D, NB>(x, emb, tok, rms_w, B, in);
+    /* epilogue operands: position and rotation of this row pair per sequence */
+    const int half_hd = hd >> 1;
+    const bool rot = r < NQ + NKV;
+    const int rr = r < NQ ? r : (rot ? r - NQ : r - NQ - NKV);
+    int ps[NB];
+    float cr[NB], sr[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        ps[b] = b < B ? pos[b] : 0;
+        const int ti = ps[b] * half_hd + ((rr % hd) >> 1);
+        cr[b] = rot ? rc[ti] : 1.f;
+        sr[b] = rot ? rs[ti] : 0.f;
+    }
+    norm_to_lds<D, NB>(in, B, x, emb != nullptr, xs);
+    if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
-    hw_dot<D, NB>(W + (size_t)(r + half) * D, xs, hl, acc);
+    hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
     if (lane != 0) return;
-    const int half_hd = hd >> 1;
     const int Hkv = NKV / hd;
+    const int h = rr / hd, d = rr % hd;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         if (b >= B) break;
-        const int ps = pos[b];
-        if (r < NQ + NKV) {
-            const int rr = r < NQ ? r : r - NQ;
-            const int i = (rr % hd) >> 1;
-            const float c = rc[ps * half_hd + i], s = rs[ps * half_hd + i];
-            const float a = r0[b], e = r1[b];
-            const float o0 = fmaf(a, c, -(e * s));   /* forward.h:64 */
-            const float o1 = fmaf(a, s, e * c);      /* forward.h:65 */
+        if (rot) {
+            const float a = r0[b], e = r1[b], c = cr[b], sn = sr[b];
+            const float o0 = fmaf(a, c, -(e * sn));  /* forward.h:64 */
+            const float o1 = fmaf(a, sn, e * c);     /* forward.h:65 */
             if (r < NQ) {
-                q[(size_t)b * NQ + r] = o0;
-                q[(size_t)b * NQ + r + 1] = o1;
+                *(float2 *)(q + (size_t)b * NQ + r) = make_float2(o0, o1);
             } else {
-                const int h = rr / hd, d = rr % hd;
-                KT *dst = kc + (((size_t)b * Hkv + h) * max_seq + ps) * hd + d;
+                KT *dst = kc + (((size_t)b * Hkv + h) * max_seq + ps[b]) * hd + d;
                 dst[0] = kv_pack<KT>(o0);
                 dst[1] = kv_pack<KT>(o1);
             }
         } else {
-            const int rr = r - NQ - NKV;
-            const int h = rr / hd, d = rr % hd;
-            KT *dst = vc + (((size_t)b * Hkv + h) * max_seq + ps) * hd + d;
+            KT *dst = vc + (((size_t)b * Hkv + h) * max_seq + ps[b]) * hd + d;
             dst[0] = kv_pack<KT>(r0[b]);
             dst[1] = kv_pack<KT>(r1[b]);
         }
     }
 }
 
-/* ---- split-KV decode attention --------------------------------------------- */
+/* ---- decode attention ------------------------------------------------------- */
 
-template <int HD, typename KT>
-__global__ void __launch_bounds__(64) k_attn_decode(
-    const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
-    const int *__restrict__ pos, int H, int Hkv, int max_seq, int nsplit,
-    float *__restrict__ part)
+/* 8 cache elements at p as raw bits (fp16: one 16-byte load; fp32: two). */
+struct KV8h { uint4 a; };
+struct KV8f { float4 a, b; };
+template <typename KT> struct KVRaw;
+template <> struct KVRaw<u16> { typedef KV8h T; };
+template <> struct KVRaw<float> { typedef KV8f T; };
+
+__device__ __forceinline__ void kv_raw_load(const u16 *p, KV8h &r) { r.a = *(const uint4 *)p; }
+__device__ __forceinline__ void kv_raw_load(const float *p, KV8f &r)
 {
-    constexpr int CH = LMK_ATTN_CHUNK;
+    r.a = *(const float4 *)p;
+    r.b = *(const float4 *)(p + 4);
+}
+__device__ __forceinline__ void kv_raw_zero(KV8h &r) { r.a = make_uint4(0, 0, 0, 0); }
+__device__ __forceinline__ void kv_raw_zero(KV8f &r) { r.a = r.b = make_float4(0, 0, 0, 0); }
+__device__ __forceinline__ void kv_raw_unpack(const KV8h &r, float f[8]) { unpack8(r.a, f); }
+__device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
+{
+    f[0] = r.a.x; f[1] = r.a.y; f[2] = r.a.z; f[3] = r.a.w;
+    f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
+}
+
+/* Work-group (h, b), 4 waves.  The positions 0..pos[b] are cut in tiles;
+ * wave w takes tiles w, w+4, ...  Within a tile a group of HD/8 lanes holds one
+ * position (8 dims per lane): K and V of the tile are loaded together, scores
+ * are q.k * (1/sqrt(hd)) (forward.h:84), then an online softmax keeps the
+ * running (max, sum, weighted V).  The four waves merge through LDS and the
+ * normalised head output (forward.h:95-97) goes to out[b, h*HD ..]. */
+template <int HD, typename KT>
+__global__ void __launch_bounds__(WG) k_attn_decode(
+    const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
+    const int *__restrict__ pos, int H, int Hkv, int max_seq, float *__restrict__ out)
+{
+    /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
+     * would take 256 registers per lane */
+    constexpr int TILE = (sizeof(KT) == 4 && HD == 128) ? 32 : 64;
     constexpr int G = HD / 8;        /* lanes per position            */
     constexpr int PP = 64 / G;       /* positions per pass            */
-    constexpr int NPASS = CH / PP;
-    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x;
+    constexpr int NP = TILE / PP;    /* passes per tile               */
+    typedef typename KVRaw<KT>::T Raw;
+    __shared__ float sm[NWAVE], sl[NWAVE];
+    __shared__ __attribute__((aligned(16))) float so[NWAVE][HD];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ctx = pos[b] + 1;
-    const int p0 = split * CH;
-    float *out = part + ((size_t)(b * H + h) * nsplit + split) * (HD + 2);
-    if (p0 >= ctx) {
-        for (int i = lane; i < HD + 2; i += 64) out[i] = i == 0 ? -INFINITY : 0.f;
-        return;
-    }
-    const int p1 = min(ctx, p0 + CH);
+    const int ntiles = (ctx + TILE - 1) / TILE;
     const int dq = lane % G, pp = lane / G;
-    const int kvh = h / (H / Hkv);
-    const size_t base = ((size_t)b * Hkv + kvh) * max_seq * HD;
+    const size_t base = ((size_t)b * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
     const KT *K = kc + base;
     const KT *V = vc + base;
     const float scale = 1.0f / sqrtf((float)HD);
@@ -210,40 +307,54 @@ __global__ void __launch_bounds__(64) k_attn_decode(
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
         qf[4] = c.x; qf[5] = c.y; qf[6] = c.z; qf[7] = c.w;
     }
-    float s[NPASS];
-#pragma unroll
-    for (int i = 0; i < NPASS; i++) {
-        const int p = p0 + pp + PP * i;
-        float d = 0.f;
-        if (p < p1) {
-            float kf[8];
-            kv_load8(K + (size_t)p * HD + dq * 8, kf);
-#pragma unroll
-            for (int j = 0; j < 8; j++) d = fmaf(qf[j], kf[j], d);
-        }
-#pragma unroll
-        for (int off = 1; off < G; off <<= 1) d += __shfl_xor(d, off, 64);
-        s[i] = p < p1 ? d * scale : -INFINITY;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NPASS; i++) m = fmaxf(m, s[i]);
-#pragma unroll
-    for (int off = G; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float l = 0.f, o[8];
+    float m = -INFINITY, l = 0.f, o[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) o[j] = 0.f;
+    for (int t = wv; t < ntiles; t += NWAVE) {
+        Raw kr[NP], vr[NP];
 #pragma unroll
-    for (int i = 0; i < NPASS; i++) {
-        const int p = p0 + pp + PP * i;
-        if (p < p1) {
-            const float e = expf(s[i] - m);
+        for (int i = 0; i < NP; i++) {
+            const int p = t * TILE + pp + PP * i;
+            if (p < ctx) {
+                kv_raw_load(K + (size_t)p * HD, kr[i]);
+                kv_raw_load(V + (size_t)p * HD, vr[i]);
+            } else {
+                kv_raw_zero(kr[i]);
+                kv_raw_zero(vr[i]);
+            }
+        }
+        float s[NP];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            float kf[8];
+            kv_raw_unpack(kr[i], kf);
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) d = fmaf(qf[j], kf[j], d);
+#pragma unroll
+            for (int off = 1; off < G; off <<= 1) d += __shfl_xor(d, off, 64);
+            const int p = t * TILE + pp + PP * i;
+            s[i] = p < ctx ? d * scale : -INFINITY;
+            tmax = fmaxf(tmax, s[i]);
+        }
+#pragma unroll
+        for (int off = G; off < 64; off <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off, 64));
+        const float mn = fmaxf(m, tmax);
+        const float corr = expf(m - mn);
+        l *= corr;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] *= corr;
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const float e = expf(s[i] - mn);   /* 0 for masked positions */
             l += e;
             float vf[8];
-            kv_load8(V + (size_t)p * HD + dq * 8, vf);
+            kv_raw_unpack(vr[i], vf);
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = fmaf(e, vf[j], o[j]);
         }
+        m = mn;
     }
 #pragma unroll
     for (int off = G; off < 64; off <<= 1) {
@@ -253,60 +364,55 @@ __global__ void __launch_bounds__(64) k_attn_decode(
     }
     if (lane < G) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) out[2 + dq * 8 + j] = o[j];
+        for (int j = 0; j < 8; j++) so[wv][dq * 8 + j] = o[j];
     }
-    if (lane == 0) { out[0] = m; out[1] = l; }
+    if (lane == 0) { sm[wv] = m; sl[wv] = l; }
+    __syncthreads();
+    if (threadIdx.x < HD) {
+        const int d = threadIdx.x;
+        float M = sm[0];
+#pragma unroll
+        for (int w = 1; w < NWAVE; w++) M = fmaxf(M, sm[w]);
+        float L = 0.f, acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) {
+            const float f = sm[w] == -INFINITY ? 0.f : expf(sm[w] - M);
+            L = fmaf(sl[w], f, L);
+            acc = fmaf(so[w][d], f, acc);
+        }
+        out[(size_t)b * H * HD + h * HD + d] = acc / L;
+    }
 }
 
 /* ---- Wo + residual ---------------------------------------------------------- */
 
-/* attn[b, h*hd + d] from the split partials of (b, h). */
-template <int D, int NB>
-__device__ __forceinline__ void merge_attn_to_lds(const float *__restrict__ part, int nsplit,
-                                                  int H, int hd, int B, float *xs)
-{
-    const int HDp = hd + 2;
-    for (int e = threadIdx.x; e < NB * D; e += WG) {
-        const int b = e / D, c = e % D;
-        float v = 0.f;
-        if (b < B) {
-            const int h = c / hd, d = c % hd;
-            const float *pb = part + (size_t)(b * H + h) * nsplit * HDp;
-            float M = -INFINITY;
-            for (int s = 0; s < nsplit; s++) M = fmaxf(M, pb[s * HDp]);
-            float L = 0.f, acc = 0.f;
-            for (int s = 0; s < nsplit; s++) {
-                const float w = expf(pb[s * HDp] - M);
-                L = fmaf(pb[s * HDp + 1], w, L);
-                acc = fmaf(pb[s * HDp + 2 + d], w, acc);
-            }
-            v = acc / L;
-        }
-        xs[e] = v;
-    }
-    __syncthreads();
-}
-
 template <int D, int NB>
 __global__ void __launch_bounds__(WG) k_wo_residual(
-    const float *__restrict__ part, int nsplit, const u16 *__restrict__ W, int H, int hd,
-    int B, float *__restrict__ x, int npairs)
+    const float *__restrict__ attn, const u16 *__restrict__ W, int B, float *__restrict__ x,
+    int npairs)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
-    merge_attn_to_lds<D, NB>(part, nsplit, H, hd, B, xs);
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
-    if (p >= npairs) return;
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
-    const int r = 2 * p;
+    const int r = 2 * min(p, npairs - 1);
+    uint4 wv[D / 256];
+    hw_load<D>(W + (size_t)(r + half) * D, hl, wv);
+    RowsIn<D, NB> in;
+    rows_load<D, NB>(attn, B, in);
+    float2 xo[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        xo[b] = b < B ? *(const float2 *)(x + (size_t)b * D + r) : make_float2(0.f, 0.f);
+    rows_to_lds<D, NB>(in, xs);
+    if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
-    hw_dot<D, NB>(W + (size_t)(r + half) * D, xs, hl, acc);
+    hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
     if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
-            x[(size_t)b * D + r] += r0[b];
-            x[(size_t)b * D + r + 1] += r1[b];
+            *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
         }
     }
 }
@@ -315,18 +421,23 @@ __global__ void __launch_bounds__(WG) k_wo_residual(
 
 template <int D, int NB>
 __global__ void __launch_bounds__(WG) k_ffn13(
-    const float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W13,
+    float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W13,
     int F, int B, float *__restrict__ g)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
-    rmsnorm_to_lds<D, NB>(x, rms_w, B, xs);
-    const int i = blockIdx.x * NWAVE + (threadIdx.x >> 6);
-    if (i >= F) return;
+    const int i0 = blockIdx.x * NWAVE + (threadIdx.x >> 6);
+    const int i = min(i0, F - 1);
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
     constexpr int GB = LMK_GATE_BLOCK;
     const size_t row = (size_t)(i / GB) * (2 * GB) + half * GB + (i % GB);
+    uint4 wv[D / 256];
+    hw_load<D>(W13 + row * D, hl, wv);
+    NormIn<D, NB> in;
+    norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
+    norm_to_lds<D, NB>(in, B, x, false, xs);
+    if (i0 >= F) return;
     float acc[NB], h1[NB], h3[NB];
-    hw_dot<D, NB>(W13 + row * D, xs, hl, acc);
+    hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, h1, h3);
     if (lane == 0) {
 #pragma unroll
@@ -346,27 +457,34 @@ __global__ void __launch_bounds__(WG) k_w2_residual(
     float *__restrict__ x, int npairs)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * F];
-    rows_to_lds<F, NB>(g, B, xs);
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
-    if (p >= npairs) return;
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
-    const int r = 2 * p;
+    const int r = 2 * min(p, npairs - 1);
+    uint4 wv[F / 256];
+    hw_load<F>(W + (size_t)(r + half) * F, hl, wv);
+    RowsIn<F, NB> in;
+    rows_load<F, NB>(g, B, in);
+    float2 xo[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        xo[b] = b < B ? *(const float2 *)(x + (size_t)b * D + r) : make_float2(0.f, 0.f);
+    rows_to_lds<F, NB>(in, xs);
+    if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
-    hw_dot<F, NB>(W + (size_t)(r + half) * F, xs, hl, acc);
+    hw_dot<F, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
     if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
-            x[(size_t)b * D + r] += r0[b];
-            x[(size_t)b * D + r + 1] += r1[b];
+            *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
         }
     }
 }
 
-/* ---- classifier + argmax partials ------------------------------------------ */
+/* ---- classifier + argmax ----------------------------------------------------- */
 
-#define CLS_PAIRS_PER_WAVE 16
+#define CLS_PAIRS_PER_WAVE 4
 #define CLS_ROWS_PER_WG (2 * CLS_PAIRS_PER_WAVE * NWAVE)
 
 template <int D, int NB>
@@ -377,32 +495,43 @@ __global__ void __launch_bounds__(WG) k_cls(
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     __shared__ float bvs[NB][NWAVE];
     __shared__ int bis[NB][NWAVE];
-    rmsnorm_to_lds<D, NB>(x, rms_w, B, xs);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
+    const int row0 = blockIdx.x * CLS_ROWS_PER_WG + wv * 2 * CLS_PAIRS_PER_WAVE;
+    uint4 wr[CLS_PAIRS_PER_WAVE][D / 256];
+#pragma unroll
+    for (int pp = 0; pp < CLS_PAIRS_PER_WAVE; pp++) {
+        const int rl = min(row0 + 2 * pp + half, V - 1);
+        hw_load<D>(W + (size_t)rl * D, hl, wr[pp]);
+    }
+    NormIn<D, NB> in;
+    norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
+    norm_to_lds<D, NB>(in, B, nullptr, false, xs);
     float bv[NB];
     int bi[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) { bv[b] = -INFINITY; bi[b] = 0x7FFFFFFF; }
-    const int row0 = blockIdx.x * CLS_ROWS_PER_WG + wv * 2 * CLS_PAIRS_PER_WAVE;
+#pragma unroll
     for (int pp = 0; pp < CLS_PAIRS_PER_WAVE; pp++) {
         const int r = row0 + 2 * pp;
-        if (r >= V) break;
-        const int rl = min(r + half, V - 1);
         float acc[NB], r0[NB], r1[NB];
-        hw_dot<D, NB>(W + (size_t)rl * D, xs, hl, acc);
+        hw_dot<D, NB>(wr[pp], xs, hl, acc);
         pair_reduce<NB>(acc, r0, r1);
-        const bool has1 = r + 1 < V;
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            argmax_combine(bv[b], bi[b], r0[b], r);
-            if (has1) argmax_combine(bv[b], bi[b], r1[b], r + 1);
-        }
-        if (logits && lane == 0) {
+        if (r < V) {
+            const bool has1 = r + 1 < V;
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                if (b >= B) break;
-                logits[(size_t)b * V + r] = r0[b];
-                if (has1) logits[(size_t)b * V + r + 1] = r1[b];
+                argmax_combine(bv[b], bi[b], r0[b], r);
+                if (has1) argmax_combine(bv[b], bi[b], r1[b], r + 1);
+            }
+            if (logits && lane == 0) {
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    if (b >= B) break;
+                    if (has1)
+                        *(float2 *)(logits + (size_t)b * V + r) = make_float2(r0[b], r1[b]);
+                    else
+                        logits[(size_t)b * V + r] = r0[b];
+                }
             }
         }
     }
@@ -420,8 +549,9 @@ __global__ void __launch_bounds__(WG) k_cls(
     }
 }
 
-/* ---- argmax merge + greedy loop state ---------------------------------------- */
-
+/* Work-group b reduces the nblk argmax partials of row b: tok[b] = argmax
+ * (lowest index on ties); with hist, also hist[b*stride + pos[b] + 1] = tok[b]
+ * and pos[b] += 1 (device-resident greedy loop state). */
 __global__ void __launch_bounds__(WG) k_argmax_final(
     const LMArgPart *__restrict__ part, int nblk, int *__restrict__ tok, int *__restrict__ pos,
     int *__restrict__ hist, int hist_stride)
@@ -490,88 +620,80 @@ __global__ void k_selftest_reduce(const float *in, float *out)
     default: return hipErrorInvalidValue;                             \
     }
 
+/* Model widths (dim) the kernels are instantiated for; hidden widths add 5632. */
+#define DISPATCH_D(K, ...)                                            \
+    switch (K) {                                                      \
+    case 256: { constexpr int K_ = 256; __VA_ARGS__; } break;         \
+    case 512: { constexpr int K_ = 512; __VA_ARGS__; } break;         \
+    case 768: { constexpr int K_ = 768; __VA_ARGS__; } break;         \
+    case 1024: { constexpr int K_ = 1024; __VA_ARGS__; } break;       \
+    case 2048: { constexpr int K_ = 2048; __VA_ARGS__; } break;       \
+    default: return hipErrorInvalidValue;                             \
+    }
+
 /* LDS budget of the GEMV kernels: NB rows of K fp32. */
 #define GEMV_LDS_OK(K_, NB_) ((size_t)(K_) * (NB_) * 4 <= 65536)
 
-extern "C" int lmk_embed(hipStream_t s, const uint16_t *embed, const int *tok, float *x, int B, int D)
+extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
+                            const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV,
+                            int hd, const float *rope_cos, const float *rope_sin, const int *pos,
+                            int B, float *q, void *kc, void *vc, int kv_f32, int max_seq)
 {
-    if (B <= 0 || D <= 0) return hipErrorInvalidValue;
-    dim3 grid((D + WG - 1) / WG, B);
-    hipLaunchKernelGGL(k_embed, grid, dim3(WG), 0, s, embed, tok, x, D);
-    return hipGetLastError();
-}
-
-extern "C" int lmk_qkv_rope(hipStream_t s, const float *x, const float *rms_w, const uint16_t *wqkv,
-                            int D, int NQ, int NKV, int hd, const float *rope_cos,
-                            const float *rope_sin, const int *pos, int B, float *q, void *kc,
-                            void *vc, int kv_f32, int max_seq)
-{
-    if (B < 1 || B > 4 || NQ != D || (hd & 1) || NKV % hd) return hipErrorInvalidValue;
+    if (B < 1 || B > 4 || NQ != D || (hd & 1) || NKV % hd || (emb && !tok))
+        return hipErrorInvalidValue;
     const int npairs = (NQ + 2 * NKV) / 2;
     dim3 grid((npairs + NWAVE - 1) / NWAVE);
-    DISPATCH_K(D, DISPATCH_NB(B, {
+    DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
         if (kv_f32)
-            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, float>), grid, dim3(WG), 0, s, x, rms_w, wqkv, NQ,
-                               NKV, hd, rope_cos, rope_sin, pos, B, q, (float *)kc, (float *)vc,
-                               max_seq, npairs);
+            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, float>), grid, dim3(WG), 0, s, x, emb, tok,
+                               rms_w, wqkv, NQ, NKV, hd, rope_cos, rope_sin, pos, B, q,
+                               (float *)kc, (float *)vc, max_seq, npairs);
         else
-            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, u16>), grid, dim3(WG), 0, s, x, rms_w, wqkv, NQ,
-                               NKV, hd, rope_cos, rope_sin, pos, B, q, (u16 *)kc, (u16 *)vc,
-                               max_seq, npairs);
+            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, u16>), grid, dim3(WG), 0, s, x, emb, tok,
+                               rms_w, wqkv, NQ, NKV, hd, rope_cos, rope_sin, pos, B, q,
+                               (u16 *)kc, (u16 *)vc, max_seq, npairs);
     }));
     return hipGetLastError();
-}
-
-template <int HD, typename KT>
-static void launch_attn_decode(hipStream_t s, dim3 grid, const float *q, const void *kc,
-                               const void *vc, const int *pos, int H, int Hkv, int max_seq,
-                               int nsplit, float *part)
-{
-    hipLaunchKernelGGL((k_attn_decode<HD, KT>), grid, dim3(64), 0, s, q, (const KT *)kc,
-                       (const KT *)vc, pos, H, Hkv, max_seq, nsplit, part);
 }
 
 extern "C" int lmk_attn_decode(hipStream_t s, const float *q, const void *kc, const void *vc,
                                int kv_f32, const int *pos, int B, int H, int Hkv, int hd,
-                               int max_seq, int nsplit, float *part)
+                               int max_seq, float *out)
 {
-    if (B < 1 || H < 1 || Hkv < 1 || H % Hkv || nsplit < 1 ||
-        nsplit * LMK_ATTN_CHUNK < max_seq)
-        return hipErrorInvalidValue;
-    dim3 grid(nsplit, H, B);
-    if (hd == 64 && kv_f32)
-        launch_attn_decode<64, float>(s, grid, q, kc, vc, pos, H, Hkv, max_seq, nsplit, part);
-    else if (hd == 64)
-        launch_attn_decode<64, u16>(s, grid, q, kc, vc, pos, H, Hkv, max_seq, nsplit, part);
-    else if (hd == 128 && kv_f32)
-        launch_attn_decode<128, float>(s, grid, q, kc, vc, pos, H, Hkv, max_seq, nsplit, part);
-    else if (hd == 128)
-        launch_attn_decode<128, u16>(s, grid, q, kc, vc, pos, H, Hkv, max_seq, nsplit, part);
-    else
-        return hipErrorInvalidValue;
+    if (B < 1 || H < 1 || Hkv < 1 || H % Hkv) return hipErrorInvalidValue;
+    dim3 grid(H, B);
+#define LAUNCH_ATTN(HD_, KT_)                                                                  \
+    hipLaunchKernelGGL((k_attn_decode<HD_, KT_>), grid, dim3(WG), 0, s, q, (const KT_ *)kc,   \
+                       (const KT_ *)vc, pos, H, Hkv, max_seq, out)
+    if (hd == 64 && kv_f32) LAUNCH_ATTN(64, float);
+    else if (hd == 64) LAUNCH_ATTN(64, u16);
+    else if (hd == 128 && kv_f32) LAUNCH_ATTN(128, float);
+    else if (hd == 128) LAUNCH_ATTN(128, u16);
+    else return hipErrorInvalidValue;
+#undef LAUNCH_ATTN
     return hipGetLastError();
 }
 
-extern "C" int lmk_wo_residual(hipStream_t s, const float *part, int nsplit, const uint16_t *wo, int D,
-                               int H, int hd, int B, float *x)
+extern "C" int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D, int B,
+                               float *x)
 {
-    if (B < 1 || B > 4 || H * hd != D) return hipErrorInvalidValue;
+    if (B < 1 || B > 4 || (D & 1)) return hipErrorInvalidValue;
     const int npairs = D / 2;
     dim3 grid((npairs + NWAVE - 1) / NWAVE);
-    DISPATCH_K(D, DISPATCH_NB(B, {
+    DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_wo_residual<K_, NB_>), grid, dim3(WG), 0, s, part, nsplit, wo, H, hd, B, x, npairs);
+        hipLaunchKernelGGL((k_wo_residual<K_, NB_>), grid, dim3(WG), 0, s, attn, wo, B, x, npairs);
     }));
     return hipGetLastError();
 }
 
-extern "C" int lmk_ffn13(hipStream_t s, const float *x, const float *rms_w, const uint16_t *w13, int D,
+extern "C" int lmk_ffn13(hipStream_t s, float *x, const float *rms_w, const uint16_t *w13, int D,
                          int F, int B, float *g)
 {
     if (B < 1 || B > 4 || F % LMK_GATE_BLOCK) return hipErrorInvalidValue;
     dim3 grid((F + NWAVE - 1) / NWAVE);
-    DISPATCH_K(D, DISPATCH_NB(B, {
+    DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
         hipLaunchKernelGGL((k_ffn13<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, w13, F, B, g);
     }));
@@ -596,20 +718,22 @@ extern "C" int lmk_cls_nblk(int V) { return (V + CLS_ROWS_PER_WG - 1) / CLS_ROWS
 extern "C" int lmk_cls(hipStream_t s, const float *x, const float *rms_w, const uint16_t *wcls, int D,
                        int V, int B, float *logits, LMArgPart *part)
 {
-    if (B < 1 || B > 4 || V < 1) return hipErrorInvalidValue;
+    if (B < 1 || B > 4 || V < 1 || !part) return hipErrorInvalidValue;
     dim3 grid(lmk_cls_nblk(V));
-    DISPATCH_K(D, DISPATCH_NB(B, {
+    DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_cls<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, wcls, V, B, logits, part);
+        hipLaunchKernelGGL((k_cls<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, wcls, V, B, logits,
+                           part);
     }));
     return hipGetLastError();
 }
 
-extern "C" int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B, int *tok, int *pos,
-                                int *hist, int hist_stride)
+extern "C" int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B, int *tok,
+                                int *pos, int *hist, int hist_stride)
 {
-    if (B < 1 || nblk < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_argmax_final, dim3(B), dim3(WG), 0, s, part, nblk, tok, pos, hist, hist_stride);
+    if (B < 1 || nblk < 1 || !tok || (hist && !pos)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax_final, dim3(B), dim3(WG), 0, s, part, nblk, tok, pos, hist,
+                       hist_stride);
     return hipGetLastError();
 }
 

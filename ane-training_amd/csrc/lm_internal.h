@@ -38,41 +38,35 @@ int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data);
  * output tile of the fused W1|W3 product holds matching h1/h3 columns. */
 #define LMK_GATE_BLOCK 16
 
-/* Positions handled by one decode-attention work-group (one KV split). */
-#define LMK_ATTN_CHUNK 64
-
 /* Argmax partial: best value and its index (lowest index on ties). */
 typedef struct { float val; int idx; } LMArgPart;
 
 /* ---- decode kernels (k_decode.hip) ---------------------------------------
  * Activations are fp32 [B, ...]; weights fp16 row-major W[out, in].
- * KV cache of one layer: [max_batch][Hkv][max_seq][hd] fp16, slot b = row b. */
-
-/* x[b, :] = fp32(embed[tok[b], :]) */
-int lmk_embed(hipStream_t s, const uint16_t *embed, const int *tok, float *x,
-              int B, int D);
+ * KV cache of one layer: [max_batch][Hkv][max_seq][hd] fp16 (or fp32), slot b
+ * = row b. */
 
 /* xn = rmsnorm(x[b]) * w; rows of [Wq;Wk;Wv] . xn; RoPE on q,k rows at pos[b];
  * q -> q[b, :NQ] fp32, k,v -> cache[b][h][pos[b]][:] (fp16, or fp32 when
- * kv_f32). */
-int lmk_qkv_rope(hipStream_t s, const float *x, const float *rms_w,
-                 const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
+ * kv_f32).  With emb != NULL the input rows are the fp16 embedding rows
+ * emb[tok[b]] instead of x, and x[b] is set to them (first layer). */
+int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
+                 const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                  const float *rope_cos, const float *rope_sin, const int *pos,
                  int B, float *q, void *kc, void *vc, int kv_f32, int max_seq);
 
-/* Split-KV decode attention: work-group (split, h, b) covers positions
- * [split*CHUNK, min(pos[b]+1, (split+1)*CHUNK)) and writes (max, sum, o[hd])
- * to part[((b*H + h)*nsplit + split)*(hd+2)]. */
+/* Causal decode attention, one work-group per (head, row): out[b, h*hd ..] =
+ * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V. */
 int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
                     const void *vc, int kv_f32, const int *pos, int B, int H, int Hkv,
-                    int hd, int max_seq, int nsplit, float *part);
+                    int hd, int max_seq, float *out);
 
-/* Merge the attention partials per head, then x[b, r] += Wo[r, :] . attn[b]. */
-int lmk_wo_residual(hipStream_t s, const float *part, int nsplit,
-                    const uint16_t *wo, int D, int H, int hd, int B, float *x);
+/* x[b, r] += Wo[r, :] . attn[b] */
+int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D,
+                    int B, float *x);
 
 /* xn = rmsnorm(x[b]) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
-int lmk_ffn13(hipStream_t s, const float *x, const float *rms_w,
+int lmk_ffn13(hipStream_t s, float *x, const float *rms_w,
               const uint16_t *w13, int D, int F, int B, float *g);
 
 /* x[b, r] += W2[r, :] . g[b, :] */
@@ -80,14 +74,14 @@ int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
                     int F, int B, float *x);
 
 /* xn = rmsnorm(x[b]) * w; logits[b, v] = Wcls[v] . xn (logits may be NULL);
- * per work-group argmax partials into part[b * nblk + blk]. Returns nblk via
- * *nblk_out when non-NULL (same value as lmk_cls_nblk). */
+ * argmax partials (lowest index on ties) to part[b * nblk + blk], nblk =
+ * lmk_cls_nblk(V). */
 int lmk_cls_nblk(int V);
 int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
             const uint16_t *wcls, int D, int V, int B, float *logits,
             LMArgPart *part);
 
-/* Reduce argmax partials of each row b: tok[b] = argmax; when hist != NULL,
+/* Reduce the argmax partials of each row b: tok[b] = argmax; when hist != NULL,
  * hist[b*hist_stride + pos[b] + 1] = tok[b] and pos[b] += 1 (device-resident
  * greedy loop state). */
 int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,

@@ -40,7 +40,7 @@ struct LMModel {
     int untied;
     int D, F, L, H, Hkv, hd, NQ, NKV, V;
     int max_batch, max_seq, max_rows;
-    int nsplit, cls_nblk;
+    int cls_nblk;
     size_t layer_elems, off_wo, off_w13, off_w2;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
@@ -52,14 +52,15 @@ struct LMModel {
     void *d_kc, *d_vc;
     size_t kv_layer_elems;
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
-    float *d_x, *d_q, *d_part, *d_g, *d_logits;
+    float *d_x, *d_q, *d_attn, *d_g, *d_logits;
     LMArgPart *d_amax;
     int *d_tok, *d_pos, *d_hist;
     /* pinned host staging */
     float *h_logits;
     int *h_io;
-    /* graphs, index = B (GEMV path) */
-    hipGraphExec_t step_graph[MAX_GEMV_B + 1];
+    /* captured decode graphs of the GEMV path: [B][0] one step, [B][1]
+     * GRAPH_STEPS steps (greedy feedback stays on the device) */
+    hipGraphExec_t step_graph[MAX_GEMV_B + 1][2];
     int use_graph, decode_path;
 };
 
@@ -237,10 +238,11 @@ static int alloc_kv(LMModel *m)
 static void drop_graphs(LMModel *m)
 {
     for (int b = 0; b <= MAX_GEMV_B; b++)
-        if (m->step_graph[b]) {
-            hipGraphExecDestroy(m->step_graph[b]);
-            m->step_graph[b] = NULL;
-        }
+        for (int k = 0; k < 2; k++)
+            if (m->step_graph[b][k]) {
+                hipGraphExecDestroy(m->step_graph[b][k]);
+                m->step_graph[b][k] = NULL;
+            }
 }
 
 static int supported_k(int k)
@@ -280,9 +282,9 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     m->hd = m->D / m->H;
     m->NQ = m->H * m->hd;
     m->NKV = m->Hkv * m->hd;
-    if ((m->hd != 64 && m->hd != 128) || !supported_k(m->D) || !supported_k(m->F)) {
+    if ((m->hd != 64 && m->hd != 128) || !supported_k(m->D) || m->D == 5632 || !supported_k(m->F)) {
         fprintf(stderr, "stories_lm: unsupported shape dim=%d hidden=%d head_dim=%d "
-                "(need head_dim 64/128, dim and hidden in {256,512,768,1024,2048,5632})\n",
+                "(need head_dim 64/128, dim in {256,512,768,1024,2048}, hidden also 5632)\n",
                 m->D, m->F, m->hd);
         FAIL(LM_ERR_UNSUPPORTED);
     }
@@ -290,7 +292,6 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     m->max_batch = max_batch;
     m->max_seq = max_seq;
     m->max_rows = max_batch;
-    m->nsplit = (max_seq + LMK_ATTN_CHUNK - 1) / LMK_ATTN_CHUNK;
     m->cls_nblk = lmk_cls_nblk(m->V);
     m->use_graph = 1;
     m->decode_path = 0;
@@ -323,8 +324,7 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_q, R * NQ * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_g, R * F * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_logits, R * V * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_part,
-                        (size_t)max_batch * m->H * m->nsplit * (m->hd + 2) * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_attn, R * NQ * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_amax, R * m->cls_nblk * sizeof(LMArgPart)))) goto fail;
     if ((st = dev_alloc((void **)&m->d_tok, R * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_pos, R * 4))) goto fail;
@@ -385,7 +385,7 @@ void lm_free(LMModel *m)
     drop_graphs(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_x, m->d_q, m->d_g, m->d_logits, m->d_part, m->d_amax,
+                   m->d_vc, m->d_x, m->d_q, m->d_g, m->d_logits, m->d_attn, m->d_amax,
                    m->d_tok, m->d_pos, m->d_hist};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
@@ -441,22 +441,23 @@ int lm_set_option(LMModel *m, int option, int value)
     } while (0)
 
 /* Queue one decode step for rows 0..B-1 (tokens in d_tok, positions in d_pos);
- * logits go to `logits` (device, B x V, may be NULL), argmax to d_tok. */
+ * logits go to `logits` (device, B x V, may be NULL), the argmax to d_tok, and
+ * the history/position advance to d_hist/d_pos. */
 static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
 {
     hipStream_t s = m->stream;
     const int D = m->D, F = m->F;
-    KCHK(lmk_embed(s, m->d_embed, m->d_tok, m->d_x, B, D));
     for (int l = 0; l < m->L; l++) {
         const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
         const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
         void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
-        KCHK(lmk_qkv_rope(s, m->d_x, m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
+        KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
+                          m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
                           m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
                           m->max_seq));
         KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
-                             m->max_seq, m->nsplit, m->d_part));
-        KCHK(lmk_wo_residual(s, m->d_part, m->nsplit, lw + m->off_wo, D, m->H, m->hd, B, m->d_x));
+                             m->max_seq, m->d_attn));
+        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
         KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
         KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
     }
@@ -466,27 +467,43 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
     return LM_OK;
 }
 
-static int run_decode_step(LMModel *m, int B)
+/* Greedy steps captured per multi-step graph. */
+#define GRAPH_STEPS 16
+
+/* Run `nsteps` (1 or GRAPH_STEPS) decode steps of rows 0..B-1, replaying the
+ * captured graph of that shape (captured on first use). */
+static int run_decode_steps(LMModel *m, int B, int nsteps)
 {
     if (B > MAX_GEMV_B) {
         fprintf(stderr, "stories_lm: decode batch %d > %d not supported yet\n", B, MAX_GEMV_B);
         return LM_ERR_UNSUPPORTED;
     }
-    if (!m->use_graph) return enqueue_decode_gemv(m, B, m->d_logits);
-    if (!m->step_graph[B]) {
+    if (nsteps != 1 && nsteps != GRAPH_STEPS) return LM_ERR_INVALID;
+    if (!m->use_graph) {
+        for (int t = 0; t < nsteps; t++) {
+            int rc = enqueue_decode_gemv(m, B, m->d_logits);
+            if (rc) return rc;
+        }
+        return LM_OK;
+    }
+    hipGraphExec_t *ge = &m->step_graph[B][nsteps == 1 ? 0 : 1];
+    if (!*ge) {
         hipGraph_t g;
         HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        int rc = enqueue_decode_gemv(m, B, m->d_logits);
+        int rc = LM_OK;
+        for (int t = 0; t < nsteps && rc == LM_OK; t++) rc = enqueue_decode_gemv(m, B, m->d_logits);
         hipError_t e = hipStreamEndCapture(m->stream, &g);
         if (rc) return rc;
         HIPCHK(e);
-        e = hipGraphInstantiate(&m->step_graph[B], g, NULL, NULL, 0);
+        e = hipGraphInstantiateWithFlags(ge, g, 0);
         hipGraphDestroy(g);
         HIPCHK(e);
     }
-    HIPCHK(hipGraphLaunch(m->step_graph[B], m->stream));
+    HIPCHK(hipGraphLaunch(*ge, m->stream));
     return LM_OK;
 }
+
+static int run_decode_step(LMModel *m, int B) { return run_decode_steps(m, B, 1); }
 
 static int check_tok_pos(const LMModel *m, const int *tokens, const int *pos, int B)
 {
@@ -568,7 +585,10 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
     memcpy(hio + B, pos0, B * 4);
     HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
     HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
-    for (int t = 0; t < n_steps; t++)
+    int t = 0;
+    for (; t + GRAPH_STEPS <= n_steps; t += GRAPH_STEPS)
+        if ((rc = run_decode_steps(m, B, GRAPH_STEPS))) return rc;
+    for (; t < n_steps; t++)
         if ((rc = run_decode_step(m, B))) return rc;
     const size_t stride = (size_t)m->max_seq + 1;
     int *h = (int *)malloc((size_t)B * stride * 4);

@@ -22,6 +22,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--path", type=int, default=0)
+    ap.add_argument("--direct", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -34,6 +35,8 @@ def main():
     w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
     m = S.Model.create(cfg, w16, True, 1, 256)
     m.set_option(S.LM_OPT_KV_F32, 1)
+    if args.direct:
+        m.set_option(S.LM_OPT_USE_GRAPH, 0)
     if args.path:
         m.set_option(S.LM_OPT_DECODE_PATH, args.path)
 
