@@ -440,38 +440,67 @@ int lm_set_option(LMModel *m, int option, int value)
         }                                                                             \
     } while (0)
 
+/* Queue the kernel of family `fam` (LM_KERN_*) of layer l for rows 0..B-1. */
+static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
+{
+    hipStream_t s = m->stream;
+    const int D = m->D, F = m->F;
+    const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
+    const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
+    void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
+    switch (fam) {
+    case LM_KERN_QKV:
+        KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
+                          m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
+                          m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
+                          m->max_seq));
+        break;
+    case LM_KERN_ATTN:
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
+                             m->max_seq, m->d_attn));
+        break;
+    case LM_KERN_WO:
+        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
+        break;
+    case LM_KERN_W13:
+        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
+        break;
+    case LM_KERN_W2:
+        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
+        break;
+    case LM_KERN_CLS:
+        KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
+        break;
+    case LM_KERN_ARGMAX:
+        KCHK(lmk_argmax_final(s, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
+                              m->max_seq + 1));
+        break;
+    default:
+        return LM_ERR_INVALID;
+    }
+    return LM_OK;
+}
+
 /* Queue one decode step for rows 0..B-1 (tokens in d_tok, positions in d_pos);
  * logits go to `logits` (device, B x V, may be NULL), the argmax to d_tok, and
  * the history/position advance to d_hist/d_pos. */
 static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
 {
-    hipStream_t s = m->stream;
-    const int D = m->D, F = m->F;
-    for (int l = 0; l < m->L; l++) {
-        const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
-        const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
-        void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
-        KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
-                          m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
-                          m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
-                          m->max_seq));
-        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
-                             m->max_seq, m->d_attn));
-        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
-        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
-        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
-    }
-    KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
-    KCHK(lmk_argmax_final(s, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
-                          m->max_seq + 1));
-    return LM_OK;
+    static const int fams[5] = {LM_KERN_QKV, LM_KERN_ATTN, LM_KERN_WO, LM_KERN_W13, LM_KERN_W2};
+    int rc;
+    for (int l = 0; l < m->L; l++)
+        for (int f = 0; f < 5; f++)
+            if ((rc = enqueue_kernel(m, B, fams[f], l, NULL))) return rc;
+    if ((rc = enqueue_kernel(m, B, LM_KERN_CLS, 0, logits))) return rc;
+    return enqueue_kernel(m, B, LM_KERN_ARGMAX, 0, NULL);
 }
 
 /* Greedy steps captured per multi-step graph. */
 #define GRAPH_STEPS 16
 
 /* Run `nsteps` (1 or GRAPH_STEPS) decode steps of rows 0..B-1, replaying the
- * captured graph of that shape (captured on first use). */
+ * captured graph of that shape (captured on first use).  Single steps write
+ * the logits to d_logits; multi-step runs only feed the argmax forward. */
 static int run_decode_steps(LMModel *m, int B, int nsteps)
 {
     if (B > MAX_GEMV_B) {
@@ -481,7 +510,7 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
     if (nsteps != 1 && nsteps != GRAPH_STEPS) return LM_ERR_INVALID;
     if (!m->use_graph) {
         for (int t = 0; t < nsteps; t++) {
-            int rc = enqueue_decode_gemv(m, B, m->d_logits);
+            int rc = enqueue_decode_gemv(m, B, nsteps == 1 ? m->d_logits : NULL);
             if (rc) return rc;
         }
         return LM_OK;
@@ -491,7 +520,8 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
         hipGraph_t g;
         HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         int rc = LM_OK;
-        for (int t = 0; t < nsteps && rc == LM_OK; t++) rc = enqueue_decode_gemv(m, B, m->d_logits);
+        for (int t = 0; t < nsteps && rc == LM_OK; t++)
+            rc = enqueue_decode_gemv(m, B, nsteps == 1 ? m->d_logits : NULL);
         hipError_t e = hipStreamEndCapture(m->stream, &g);
         if (rc) return rc;
         HIPCHK(e);
@@ -682,4 +712,61 @@ int lm_selftest_reduce(const float *in64, float *out4)
     hipFree(d);
     HIPCHK(e);
     return LM_OK;
+}
+
+/* Diagnostics: mean device time per launch of each decode kernel family.  For
+ * family f `reps` rounds of its per-step launches (every layer for the
+ * per-layer kernels) run between two hipEvents on the handle's stream, as one
+ * captured graph (or launched directly when graphs are off); positions pos[b]
+ * are held fixed (the argmax kernel's advance of pos is undone before the
+ * timed run). */
+int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
+                      float *us_per_launch, int *launches_per_step)
+{
+    if (!m || !tokens || !pos || !us_per_launch || B < 1 || reps < 1) return LM_ERR_INVALID;
+    if (B > m->max_batch) return LM_ERR_RANGE;
+    if (B > MAX_GEMV_B) return LM_ERR_UNSUPPORTED;
+    int rc = check_tok_pos(m, tokens, pos, B);
+    if (rc) return rc;
+    int *hio = m->h_io;
+    memcpy(hio, tokens, B * 4);
+    memcpy(hio + B, pos, B * 4);
+    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
+    for (int f = 0; f < LM_KERN_COUNT && rc == LM_OK; f++) {
+        const int per_step = (f == LM_KERN_CLS || f == LM_KERN_ARGMAX) ? 1 : m->L;
+        if (launches_per_step) launches_per_step[f] = per_step;
+        hipGraph_t g = NULL;
+        hipGraphExec_t ge = NULL;
+        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+        HIPCHK(hipStreamSynchronize(m->stream));
+        if (m->use_graph) {
+            HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+            for (int r = 0; r < reps && rc == LM_OK; r++)
+                for (int l = 0; l < per_step && rc == LM_OK; l++) rc = enqueue_kernel(m, B, f, l, NULL);
+            hipError_t e = hipStreamEndCapture(m->stream, &g);
+            if (rc == LM_OK && e != hipSuccess) rc = LM_ERR_HIP;
+            if (rc == LM_OK && hipGraphInstantiateWithFlags(&ge, g, 0) != hipSuccess) rc = LM_ERR_HIP;
+        }
+        float ms = 0.f;
+        for (int it = 0; it < 2 && rc == LM_OK; it++) {   /* warm-up run, timed run */
+            if (f == LM_KERN_ARGMAX &&
+                hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
+                rc = LM_ERR_HIP;
+            if (rc == LM_OK && hipEventRecord(m->ev0, m->stream) != hipSuccess) rc = LM_ERR_HIP;
+            if (rc == LM_OK && ge && hipGraphLaunch(ge, m->stream) != hipSuccess) rc = LM_ERR_HIP;
+            for (int r = 0; !ge && r < reps && rc == LM_OK; r++)
+                for (int l = 0; l < per_step && rc == LM_OK; l++) rc = enqueue_kernel(m, B, f, l, NULL);
+            if (rc == LM_OK && (hipEventRecord(m->ev1, m->stream) != hipSuccess ||
+                                hipEventSynchronize(m->ev1) != hipSuccess ||
+                                hipEventElapsedTime(&ms, m->ev0, m->ev1) != hipSuccess))
+                rc = LM_ERR_HIP;
+        }
+        if (ge) hipGraphExecDestroy(ge);
+        if (g) hipGraphDestroy(g);
+        us_per_launch[f] = ms * 1e3f / (float)(reps * per_step);
+    }
+    if (rc == LM_OK)
+        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return rc;
 }

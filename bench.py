@@ -1,8 +1,25 @@
-"""Benchmark of the Stories-110M token loop on one MI355X (first version).
+"""Benchmark of the Stories / Llama-2 token loop on one MI355X.
 
-A step is one greedy decode token at batch 1 (config C0: 256-token sequences
-from token id 1, fp32 accumulation, fp32 K/V cache), replayed as captured
-hipGraphs with the argmax fed back on the device.
+Headline (``value``): configuration C0 of the baseline — Stories-110M
+(dim 768, 12 layers, 12 heads, SwiGLU 2048, vocab 32000, untied classifier),
+seeded N(0, 0.02) fp16 weights, batch-1 greedy decode of 256-token sequences
+from token id 1, fp32 accumulation, K/V cache in fp32 like the reference
+forward (training/forward.h:118-128) so the greedy ids are the reference's
+(--kv16 switches to a binary16 cache).  A "step" is one
+generated token; the timed region replays captured multi-step hipGraphs with
+the argmax fed back on the device, inputs and weights already resident in HBM.
+
+Alongside the headline the JSON line carries:
+  roofline      the dominant kernel family of the decode step (largest device
+                time per token): algorithmic bytes per launch / mean launch
+                duration, from a captured graph of back-to-back launches of
+                that family (cycling through the layers) timed with hipEvents
+                on the model's stream (lm_profile_decode) after the timed
+                region
+  step_roofline the whole token: algorithmic bytes per token / time per token
+  cpu_baseline  the CPU oracle (a C restatement of the reference's fp32
+                forward, KV-cache decode) timed on this host on the same C0
+                run; its greedy ids are compared with the GPU's
 """
 import argparse
 import json
@@ -15,50 +32,126 @@ sys.path[:0] = [os.path.join(ROOT, "ane-training_amd"), os.path.join(ROOT, "orac
 
 import numpy as np  # noqa: E402
 
+HBM_PEAK_GBS = 8000.0
+# Published reference figure for this metric: Stories-110M B=1 greedy decode on
+# the ANE (libane, fp16), M3 Pro: 41.7 tok/s (full 256-window recompute).
+REF_TOK_S = 41.7
+SEQ = 256
+
+
+def algorithmic_bytes(cfg, B, mean_ctx, kv_bytes=2, logits=False):
+    """Bytes each decode kernel family must move per launch (weights read once,
+    activations read/written once; K/V read over mean_ctx cached positions)."""
+    D, F, V = cfg.dim, cfg.hidden_dim, abs(cfg.vocab_size)
+    hd = D // cfg.n_heads
+    NQ, NKV = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    nblk = (V + 31) // 32          # argmax partials: one per 32 classifier rows
+    return {
+        "qkv": (NQ + 2 * NKV) * D * 2 + D * 4 + B * (D * 4 + NQ * 4 + 2 * NKV * kv_bytes + hd * 4),
+        "attn": B * (2 * mean_ctx * NKV * kv_bytes + 2 * NQ * 4),
+        "wo": D * NQ * 2 + B * (NQ * 4 + 2 * D * 4),
+        "w13": 2 * F * D * 2 + D * 4 + B * (D * 4 + F * 4),
+        "w2": D * F * 2 + B * (F * 4 + 2 * D * 4),
+        "cls": V * D * 2 + D * 4 + B * (D * 4 + nblk * 8 + (V * 4 if logits else 0)),
+        "argmax": B * (nblk * 8 + 12),
+    }
+
+
+def cpu_baseline(cfg7, w16, S, n_tokens):
+    """The oracle's KV-cache greedy decode (fp32, as training/forward.h) of the
+    first n_tokens of C0 on this host; returns (info, ids)."""
+    import oracle as O
+    w32 = S.f16_to_f32(w16)
+    o = O.Oracle(cfg7, w32, True, SEQ)
+    t0 = time.perf_counter()
+    ids = o.greedy(1, 0, n_tokens)
+    dt = time.perf_counter() - t0
+    o.close()
+    return {"value": round(n_tokens / dt, 2), "unit": "tok/s", "cores": O.num_threads(),
+            "kind": "port",
+            "sample": f"C0 first {n_tokens} greedy tokens from id 1, KV-cache decode, fp32 "
+                      f"(oracle/oracle.c restating training/forward.h), {dt:.1f} s"}, ids
+
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=256)
-    ap.add_argument("--path", type=int, default=0)
-    ap.add_argument("--direct", action="store_true")
+    ap.add_argument("--steps", type=int, default=8192, help="timed tokens (multiple of 256)")
+    ap.add_argument("--warmup", type=int, default=512)
+    ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
+    ap.add_argument("--kv16", action="store_true",
+                    help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
+    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (one MI355X per box); "
+              "--gpus must be 1", file=sys.stderr)
         sys.exit(2)
+    steps = max(SEQ, (args.steps + SEQ - 1) // SEQ * SEQ)
+    warm = (args.warmup + SEQ - 1) // SEQ * SEQ
     import stories_lm as S
     rc = S.init()
     if rc:
         raise SystemExit(f"lm_init: {S.strerror(rc)}")
     cfg = S.make_config(**S.STORIES_110M)
     w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
-    m = S.Model.create(cfg, w16, True, 1, 256)
-    m.set_option(S.LM_OPT_KV_F32, 1)
+    m = S.Model.create(cfg, w16, True, 1, SEQ)
+    if not args.kv16:
+        m.set_option(S.LM_OPT_KV_F32, 1)
     if args.direct:
         m.set_option(S.LM_OPT_USE_GRAPH, 0)
-    if args.path:
-        m.set_option(S.LM_OPT_DECODE_PATH, args.path)
 
-    def run(n):
-        done = 0
-        while done < n:
-            k = min(256, n - done)
-            m.generate_greedy([1], [0], k)
-            done += k
-
-    run(args.warmup)
+    for _ in range(warm // SEQ):
+        m.generate_greedy([1], [0], SEQ)
     m.sync()
     m.timer_begin()
     t0 = time.perf_counter()
-    run(args.steps)
+    ids = None
+    for _ in range(steps // SEQ):
+        ids = m.generate_greedy([1], [0], SEQ)[:, 0]
     ms = m.timer_end()
     wall = time.perf_counter() - t0
-    tok_s = args.steps / (ms / 1e3)
-    print(json.dumps({"metric": "Stories-110M decode tok/s at B=1", "value": round(tok_s, 1),
-                      "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-                      "ms_per_step": ms / args.steps, "wall_s": wall, "higher_is_better": True}),
-          flush=True)
+    tok_s = steps / (ms / 1e3)
+    us_tok = ms * 1e3 / steps
+
+    # device time per launch of each kernel family at the run's mean context
+    # (position 128 of 0..255): graphs of back-to-back launches timed with hipEvents
+    us, launches = m.profile_decode([1], [SEQ // 2], 32)
+    mean_ctx = (SEQ + 1) / 2
+    kvb = 2 if args.kv16 else 4
+    algo = algorithmic_bytes(cfg, 1, mean_ctx, kvb)
+    dom = max(us, key=lambda k: us[k] * launches[k])
+    dur_us = us[dom]
+    achieved = algo[dom] / (dur_us * 1e-6) / 1e9
+    step_bytes = sum(algo[k] * launches[k] for k in algo)
+    step_gbs = step_bytes / (us_tok * 1e-6) / 1e9
+    m.close()
+
+    out = {
+        "metric": "Stories-110M decode tok/s at B=1 and B=64; prefill tok/s; % HBM/MFMA roofline",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm, "ms_per_step": round(us_tok / 1e3, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": round(tok_s / REF_TOK_S, 1),
+        "dtype": "f32", "storage": "f16 weights, f%d K/V cache" % (8 * kvb),
+        "data": "synthetic (seeded N(0,0.02) fp16 weights, greedy from token id 1)",
+        "config": {"workload": "C0: Stories-110M batch-1 greedy decode, 256-token sequences "
+                               "from token id 1, untied classifier", "batch": 1, "seq_len": SEQ,
+                   "graphs": not args.direct},
+        "wall_s": round(wall, 3),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": int(algo[dom]),
+                     "launch_us": round(dur_us, 3)},
+        "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1),
+                          "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "kernel_us_per_launch": {k: round(v, 3) for k, v in us.items()},
+    }
+    if not args.no_cpu:
+        cb, cpu_ids = cpu_baseline(cfg.astuple(), w16, S, args.cpu_tokens)
+        cb["ids_match_gpu"] = bool(np.array_equal(cpu_ids, ids[:args.cpu_tokens]))
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

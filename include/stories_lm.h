@@ -248,6 +248,25 @@ int lm_rope_table(int max_seq, int head_dim, float *cos_out, float *sin_out);
  * 0..31, sum of lanes 32..63, wave sum (DPP), wave sum (shuffles)}. */
 int lm_selftest_reduce(const float *in64, float *out4);
 
+/* Kernel families of a decode step (index into lm_profile_decode's output). */
+#define LM_KERN_QKV    0   /* rmsnorm + QKV GEMV + RoPE + KV append          */
+#define LM_KERN_ATTN   1   /* causal attention over the KV cache            */
+#define LM_KERN_WO     2   /* Wo GEMV + residual                            */
+#define LM_KERN_W13    3   /* rmsnorm + W1/W3 GEMV + SiLU gate              */
+#define LM_KERN_W2     4   /* W2 GEMV + residual                            */
+#define LM_KERN_CLS    5   /* final rmsnorm + classifier + argmax partials  */
+#define LM_KERN_ARGMAX 6   /* argmax reduction + greedy loop state          */
+#define LM_KERN_COUNT  7
+
+/* Mean device microseconds per launch of each decode kernel family for B rows
+ * at tokens[b], positions pos[b]: the launches of one family (each layer for
+ * the per-layer families) run `reps` times between hipEvents on the handle's
+ * stream, as one captured graph (directly when LM_OPT_USE_GRAPH is 0).  launches_per_step[k] (may be
+ * NULL) = launches of family k in one decode step.  Leaves the KV cache
+ * entries at pos[b] and the activations overwritten. */
+int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
+                      float *us_per_launch, int *launches_per_step);
+
 #ifdef __cplusplus
 }
 #endif

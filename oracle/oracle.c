@@ -16,6 +16,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 struct OracleModel {
     int D, F, L, H, Hkv, hd, NQ, NKV, V, max_seq, kv_f16;
@@ -352,4 +355,13 @@ int oracle_argmax(const float *logits, int n)
     for (int i = 1; i < n; i++)
         if (logits[i] > best_val) { best_val = logits[i]; best = i; }
     return best;
+}
+
+int oracle_num_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }

@@ -59,6 +59,9 @@ void oracle_rope(float *q, float *k, int S, int n_heads, int n_kv_heads, int hea
 void oracle_attention(float *out, const float *q, const float *k, const float *v, int S,
                       int n_heads, int n_kv_heads, int head_dim);
 
+/* OpenMP threads the oracle's parallel loops use. */
+int oracle_num_threads(void);
+
 /* binary16 round trip used by the kv_f16 mode. */
 float oracle_round_f16(float x);
 

@@ -36,6 +36,7 @@ def lib():
             "oracle_rope": (None, [fp, fp, I, I, I, I, I]),
             "oracle_attention": (None, [fp, fp, fp, fp, I, I, I, I]),
             "oracle_round_f16": (F, [F]),
+            "oracle_num_threads": (I, []),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -148,3 +149,7 @@ def attention(q, k, v, n_heads, n_kv_heads, head_dim):
 
 def round_f16(x: float) -> float:
     return float(lib().oracle_round_f16(float(x)))
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())
