@@ -87,6 +87,36 @@ int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
 int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,
                      int *tok, int *pos, int *hist, int hist_stride);
 
+/* ---- persistent batch-1 decode (k_persist.hip) --------------------------- */
+
+typedef struct {
+    const uint16_t *layers;          /* layer blocks, layout of lm_runtime.c          */
+    size_t layer_elems, off_wo, off_w13, off_w2;
+    const uint16_t *embed, *wcls;
+    const float *rms_att, *rms_ffn, *rms_final, *rope_cos, *rope_sin;
+    void *kc, *vc;                   /* slot-0 cache of layer 0; layer l at +l*kv_layer_elems */
+    size_t kv_layer_elems;
+    int kv_f32;
+    void *ll;                        /* lmk_persist_ll_words() 64-bit tagged words     */
+    float *logits;                   /* V floats of the last step, or NULL            */
+    int *out_tok;                    /* n_steps greedy ids                            */
+    int *state_tok, *state_pos;      /* final token / position                        */
+    int *err;                        /* set on a wait time-out                        */
+    int D, F, V, L, H, Hkv, hd, max_seq;
+    int tok0, pos0, n_steps;
+    unsigned tag0;                   /* tag of the first step; steps use tag0 + t     */
+    int grid;                        /* work-groups, <= lmk_persist_grid()            */
+} LMPersistArgs;
+
+/* Work-groups of the persistent decode (one per CU, at most 256); 0 on error. */
+int lmk_persist_grid(void);
+/* Non-zero when the persistent kernel is instantiated for this shape. */
+int lmk_persist_supported(int D, int F, int hd, int H);
+/* 64-bit words of tagged-word buffers the kernel needs. */
+size_t lmk_persist_ll_words(int D, int F, int L, int H, int Hkv, int hd, int grid);
+/* Run p->n_steps greedy decode steps of slot 0 as one cooperative launch. */
+int lmk_decode_persist(hipStream_t s, const LMPersistArgs *p);
+
 /* ---- diagnostics kernels (k_decode.hip) ---------------------------------- */
 
 /* Wave-reduction self-check: out[0..3] = sums computed with the production

@@ -62,6 +62,12 @@ struct LMModel {
      * GRAPH_STEPS steps (greedy feedback stays on the device) */
     hipGraphExec_t step_graph[MAX_GEMV_B + 1][2];
     int use_graph, decode_path;
+    /* persistent batch-1 decode */
+    int pl_ok, pl_grid;         /* kernel instantiated for this shape; work-groups */
+    void *d_ll;                 /* tagged-word buffers                        */
+    size_t ll_words;
+    unsigned pl_tag;            /* next step tag (buffers start at tag 0)      */
+    int *d_ptok, *d_err;        /* per-step ids [max_seq], wait time-out flag  */
 };
 
 static int g_init_status = 1; /* 1 = not attempted */
@@ -329,6 +335,18 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_tok, R * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_pos, R * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
+    m->pl_grid = lmk_persist_grid();
+    m->pl_ok = m->pl_grid > 0 && lmk_persist_supported(m->D, m->F, m->hd, m->H);
+    if (m->pl_ok) {
+        m->ll_words = lmk_persist_ll_words(m->D, m->F, m->L, m->H, m->Hkv, m->hd, m->pl_grid);
+        if ((st = dev_alloc(&m->d_ll, m->ll_words * 8))) goto fail;
+        if ((st = dev_alloc((void **)&m->d_ptok, (size_t)max_seq * 4))) goto fail;
+        if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
+        if (hipMemset(m->d_ll, 0, m->ll_words * 8) != hipSuccess ||
+            hipMemset(m->d_err, 0, 4) != hipSuccess)
+            FAIL(LM_ERR_HIP);
+        m->pl_tag = 1;
+    }
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
 
@@ -386,7 +404,7 @@ void lm_free(LMModel *m)
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
                    m->d_vc, m->d_x, m->d_q, m->d_g, m->d_logits, m->d_attn, m->d_amax,
-                   m->d_tok, m->d_pos, m->d_hist};
+                   m->d_tok, m->d_pos, m->d_hist, m->d_ll, m->d_ptok, m->d_err};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_logits) hipHostFree(m->h_logits);
@@ -410,6 +428,7 @@ int lm_set_option(LMModel *m, int option, int value)
     switch (option) {
     case LM_OPT_DECODE_PATH:
         if (value < 0 || value > 2) return LM_ERR_INVALID;
+        if (value == 2 && !m->pl_ok) return LM_ERR_UNSUPPORTED;
         m->decode_path = value;
         return LM_OK;
     case LM_OPT_USE_GRAPH:
@@ -535,6 +554,57 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
 
 static int run_decode_step(LMModel *m, int B) { return run_decode_steps(m, B, 1); }
 
+/* Whether a batch-1 step goes to the persistent kernel (LM_OPT_DECODE_PATH 2).
+ * Auto (0) takes the kernel chain: on MI355X its launches cost less than the
+ * persistent kernel's in-kernel hand-offs (206 vs 271 us per Stories token). */
+static int use_persistent(const LMModel *m, int B)
+{
+    return B == 1 && m->pl_ok && m->decode_path == 2;
+}
+
+/* n greedy steps of slot 0 from token tok0 at pos0 as one persistent launch;
+ * logits of the last step to d_logits when want_logits; ids to out (host, may
+ * be NULL); d_tok/d_pos left at the final token/position. */
+static int run_persistent(LMModel *m, int tok0, int pos0, int n, int want_logits, int *out)
+{
+    if (m->pl_tag > 0xFFFFFFF0u - (unsigned)n) {   /* tags would wrap: clear the buffers */
+        HIPCHK(hipMemsetAsync(m->d_ll, 0, m->ll_words * 8, m->stream));
+        m->pl_tag = 1;
+    }
+    LMPersistArgs p;
+    memset(&p, 0, sizeof(p));
+    p.layers = m->d_layers; p.layer_elems = m->layer_elems;
+    p.off_wo = m->off_wo; p.off_w13 = m->off_w13; p.off_w2 = m->off_w2;
+    p.embed = m->d_embed; p.wcls = m->d_wcls;
+    p.rms_att = m->d_rms_att; p.rms_ffn = m->d_rms_ffn; p.rms_final = m->d_rms_final;
+    p.rope_cos = m->d_rope_cos; p.rope_sin = m->d_rope_sin;
+    p.kc = m->d_kc; p.vc = m->d_vc; p.kv_layer_elems = m->kv_layer_elems; p.kv_f32 = m->kv_f32;
+    p.ll = m->d_ll; p.logits = want_logits ? m->d_logits : NULL; p.out_tok = m->d_ptok;
+    p.state_tok = m->d_tok; p.state_pos = m->d_pos; p.err = m->d_err;
+    p.D = m->D; p.F = m->F; p.V = m->V; p.L = m->L; p.H = m->H; p.Hkv = m->Hkv; p.hd = m->hd;
+    p.max_seq = m->max_seq; p.tok0 = tok0; p.pos0 = pos0; p.n_steps = n; p.tag0 = m->pl_tag;
+    p.grid = m->pl_grid;
+    m->pl_tag += (unsigned)n;
+    int e = lmk_decode_persist(m->stream, &p);
+    if (e != 0) {
+        fprintf(stderr, "stories_lm: persistent decode launch failed: %s\n",
+                hipGetErrorString((hipError_t)e));
+        return LM_ERR_HIP;
+    }
+    int *hio = m->h_io;
+    HIPCHK(hipMemcpyAsync(hio, m->d_err, 4, hipMemcpyDeviceToHost, m->stream));
+    if (out) HIPCHK(hipMemcpyAsync(out, m->d_ptok, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    if (hio[0]) {
+        fprintf(stderr, "stories_lm: persistent decode: a hand-off wait timed out\n");
+        HIPCHK(hipMemset(m->d_err, 0, 4));
+        HIPCHK(hipMemset(m->d_ll, 0, m->ll_words * 8));
+        m->pl_tag = 1;
+        return LM_ERR_HIP;
+    }
+    return LM_OK;
+}
+
 static int check_tok_pos(const LMModel *m, const int *tokens, const int *pos, int B)
 {
     for (int b = 0; b < B; b++) {
@@ -557,13 +627,19 @@ int lm_forward_batch(LMModel *m, const int *tokens, const int *pos, int B, float
     int rc = check_tok_pos(m, tokens, pos, B);
     if (rc) return rc;
     int *hio = m->h_io;
-    memcpy(hio, tokens, B * 4);
-    memcpy(hio + B, pos, B * 4);
-    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
-    HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
-    if ((rc = run_decode_step(m, B))) return rc;
-    if (argmax)
-        HIPCHK(hipMemcpyAsync(hio + 2 * B, m->d_tok, B * 4, hipMemcpyDeviceToHost, m->stream));
+    if (use_persistent(m, B)) {
+        int id = 0;
+        if ((rc = run_persistent(m, tokens[0], pos[0], 1, 1, &id))) return rc;
+        hio[2 * B] = id;
+    } else {
+        memcpy(hio, tokens, B * 4);
+        memcpy(hio + B, pos, B * 4);
+        HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
+        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+        if ((rc = run_decode_step(m, B))) return rc;
+        if (argmax)
+            HIPCHK(hipMemcpyAsync(hio + 2 * B, m->d_tok, B * 4, hipMemcpyDeviceToHost, m->stream));
+    }
     if (logits)
         HIPCHK(hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)B * m->V * 4,
                               hipMemcpyDeviceToHost, m->stream));
@@ -581,12 +657,16 @@ const float *lm_forward(LMModel *m, int token, int pos)
     }
     if (check_tok_pos(m, &token, &pos, 1)) return NULL;
     int *hio = m->h_io;
-    hio[0] = token;
-    hio[1] = pos;
-    if (hipMemcpyAsync(m->d_tok, hio, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
-        hipMemcpyAsync(m->d_pos, hio + 1, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
-        return NULL;
-    if (run_decode_step(m, 1)) return NULL;
+    if (use_persistent(m, 1)) {
+        if (run_persistent(m, token, pos, 1, 1, NULL)) return NULL;
+    } else {
+        hio[0] = token;
+        hio[1] = pos;
+        if (hipMemcpyAsync(m->d_tok, hio, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+            hipMemcpyAsync(m->d_pos, hio + 1, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
+            return NULL;
+        if (run_decode_step(m, 1)) return NULL;
+    }
     if (hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
                        m->stream) != hipSuccess ||
         hipStreamSynchronize(m->stream) != hipSuccess) {
@@ -610,6 +690,7 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
             return LM_ERR_RANGE;
         }
     if (n_steps == 0) return LM_OK;
+    if (use_persistent(m, B)) return run_persistent(m, first_tokens[0], pos0[0], n_steps, 0, out_tokens);
     int *hio = m->h_io;
     memcpy(hio, first_tokens, B * 4);
     memcpy(hio + B, pos0, B * 4);

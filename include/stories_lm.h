@@ -193,8 +193,11 @@ int lm_timer_begin(LMModel *m);
 /* Record a stop event, wait for it, return elapsed ms since lm_timer_begin. */
 int lm_timer_end(LMModel *m, float *ms);
 
-/* Execution knobs.  LM_OPT_DECODE_PATH selects the B=1 decode step: 0 = auto,
- * 1 = chain of per-op kernels, 2 = persistent single-kernel step.
+/* Execution knobs.  LM_OPT_DECODE_PATH selects the B=1 decode step: 0 = auto
+ * (currently the chain), 1 = chain of per-op kernels replayed as captured
+ * graphs, 2 = persistent kernel: one cooperative launch runs all requested
+ * steps, work-groups hand activations over through tagged words in memory
+ * (LM_ERR_UNSUPPORTED when it is not built for the model's shape).
  * LM_OPT_USE_GRAPH: 1 (default) replays captured hipGraphs, 0 launches
  * kernels directly (debugging / per-kernel timing). */
 #define LM_OPT_DECODE_PATH 1
