@@ -271,7 +271,8 @@ __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
     f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
 }
 
-/* Work-group (h, b), 4 waves.  The positions 0..pos[b] are cut in tiles;
+/* Work-group (h, b), 4 waves: query row b (q[b], cache slot slot[b] or b when
+ * slot is NULL) attends to positions 0..pos[b].  The positions are cut in tiles;
  * wave w takes tiles w, w+4, ...  Within a tile a group of HD/8 lanes holds one
  * position (8 dims per lane): K and V of the tile are loaded together, scores
  * are q.k * (1/sqrt(hd)) (forward.h:84), then an online softmax keeps the
@@ -280,7 +281,8 @@ __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
 template <int HD, typename KT>
 __global__ void __launch_bounds__(WG) k_attn_decode(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
-    const int *__restrict__ pos, int H, int Hkv, int max_seq, float *__restrict__ out)
+    const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
+    float *__restrict__ out)
 {
     /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
      * would take 256 registers per lane */
@@ -296,7 +298,8 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
     const int ctx = pos[b] + 1;
     const int ntiles = (ctx + TILE - 1) / TILE;
     const int dq = lane % G, pp = lane / G;
-    const size_t base = ((size_t)b * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
+    const int cs = slot ? slot[b] : b;
+    const size_t base = ((size_t)cs * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
     const KT *K = kc + base;
     const KT *V = vc + base;
     const float scale = 1.0f / sqrtf((float)HD);
@@ -658,14 +661,14 @@ extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const 
 }
 
 extern "C" int lmk_attn_decode(hipStream_t s, const float *q, const void *kc, const void *vc,
-                               int kv_f32, const int *pos, int B, int H, int Hkv, int hd,
-                               int max_seq, float *out)
+                               int kv_f32, const int *pos, const int *slot, int B, int H, int Hkv,
+                               int hd, int max_seq, float *out)
 {
-    if (B < 1 || H < 1 || Hkv < 1 || H % Hkv) return hipErrorInvalidValue;
+    if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv) return hipErrorInvalidValue;
     dim3 grid(H, B);
 #define LAUNCH_ATTN(HD_, KT_)                                                                  \
     hipLaunchKernelGGL((k_attn_decode<HD_, KT_>), grid, dim3(WG), 0, s, q, (const KT_ *)kc,   \
-                       (const KT_ *)vc, pos, H, Hkv, max_seq, out)
+                       (const KT_ *)vc, pos, slot, H, Hkv, max_seq, out)
     if (hd == 64 && kv_f32) LAUNCH_ATTN(64, float);
     else if (hd == 64) LAUNCH_ATTN(64, u16);
     else if (hd == 128 && kv_f32) LAUNCH_ATTN(128, float);

@@ -55,11 +55,12 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rope_cos, const float *rope_sin, const int *pos,
                  int B, float *q, void *kc, void *vc, int kv_f32, int max_seq);
 
-/* Causal decode attention, one work-group per (head, row): out[b, h*hd ..] =
- * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V. */
+/* Causal attention, one work-group per (head, row): out[b, h*hd ..] =
+ * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V over cache slot slot[b] (slot
+ * NULL: slot b).  Serves decode rows and prefill rows alike. */
 int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
-                    const void *vc, int kv_f32, const int *pos, int B, int H, int Hkv,
-                    int hd, int max_seq, float *out);
+                    const void *vc, int kv_f32, const int *pos, const int *slot, int B, int H,
+                    int Hkv, int hd, int max_seq, float *out);
 
 /* x[b, r] += Wo[r, :] . attn[b] */
 int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D,
@@ -86,6 +87,42 @@ int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
  * greedy loop state). */
 int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,
                      int *tok, int *pos, int *hist, int hist_stride);
+
+/* ---- MFMA GEMMs (k_gemm.hip) ----------------------------------------------
+ * C[m, n] = sum_k A[m, k] W[n, k], W fp16 [N, K], fp32 accumulation; rows M <= 64
+ * take the skinny (decode) kernel, larger M the LDS-tiled (prefill) kernel.
+ * K must be a multiple of 32. */
+
+#define LMK_A_F16       0   /* A fp16 [M, lda]                                   */
+#define LMK_A_F32       1   /* A fp32 [M, lda], rounded to fp16                   */
+#define LMK_A_F32_NORM  2   /* A fp32, times rstd[m] * gain[k], rounded to fp16   */
+
+#define LMK_EPI_STORE   0   /* out (fp32 [M, ldc], may be NULL) + argmax partials  */
+#define LMK_EPI_RESID   1   /* out[m, n] += C (fp32 residual stream)               */
+#define LMK_EPI_GATE    2   /* g[m, i] = fp16(silu(h1) * h3), W1/W3 interleaved    */
+#define LMK_EPI_QKV     3   /* RoPE; q -> fp32 [M, NQ]; k, v -> cache(slot, pos)   */
+
+typedef struct {
+    float *out;              /* STORE / RESID                                      */
+    int ldc;
+    LMArgPart *part;         /* STORE: [M, ceil(N/32)] argmax partials, or NULL    */
+    uint16_t *g;             /* GATE: [M, F] fp16                                  */
+    int F;
+    float *q;                /* QKV                                                 */
+    void *kc, *vc;           /* layer's cache base: [max_batch][Hkv][max_seq][hd]   */
+    int kv_f32, NQ, NKV, hd, Hkv, max_seq;
+    const int *slot, *pos;   /* per row                                             */
+    const float *rope_cos, *rope_sin;
+} LMEpilogue;
+
+int lmk_gemm(hipStream_t s, int a_kind, const void *A, int lda, const float *rstd,
+             const float *gain, const uint16_t *W, int M, int N, int K, int epi,
+             const LMEpilogue *ep);
+
+/* One wave per row: rstd[m] = 1/sqrt(mean(x[m]^2) + 1e-5); with emb != NULL the
+ * row is first set to the embedding row emb[tok[m]]. */
+int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
+                float *rstd);
 
 /* ---- persistent batch-1 decode (k_persist.hip) --------------------------- */
 

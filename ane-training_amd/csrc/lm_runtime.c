@@ -52,15 +52,19 @@ struct LMModel {
     void *d_kc, *d_vc;
     size_t kv_layer_elems;
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
-    float *d_x, *d_q, *d_attn, *d_g, *d_logits;
+    /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
+    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
+    uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     LMArgPart *d_amax;
-    int *d_tok, *d_pos, *d_hist;
+    int *d_rtok, *d_rpos, *d_rslot;   /* prefill rows: token, position, slot */
+    /* per-slot greedy state */
+    int *d_tok, *d_pos, *d_hist, *d_slot_id;
     /* pinned host staging */
     float *h_logits;
     int *h_io;
-    /* captured decode graphs of the GEMV path: [B][0] one step, [B][1]
-     * GRAPH_STEPS steps (greedy feedback stays on the device) */
-    hipGraphExec_t step_graph[MAX_GEMV_B + 1][2];
+    /* captured decode graphs: [B][0] one step, [B][1] GRAPH_STEPS steps
+     * (greedy feedback stays on the device) */
+    hipGraphExec_t (*step_graph)[2];   /* [max_batch + 1][2]   */
     int use_graph, decode_path;
     /* persistent batch-1 decode */
     int pl_ok, pl_grid;         /* kernel instantiated for this shape; work-groups */
@@ -243,12 +247,50 @@ static int alloc_kv(LMModel *m)
 
 static void drop_graphs(LMModel *m)
 {
-    for (int b = 0; b <= MAX_GEMV_B; b++)
+    if (!m->step_graph) return;
+    for (int b = 0; b <= m->max_batch; b++)
         for (int k = 0; k < 2; k++)
             if (m->step_graph[b][k]) {
                 hipGraphExecDestroy(m->step_graph[b][k]);
                 m->step_graph[b][k] = NULL;
             }
+}
+
+static void free_rows(LMModel *m)
+{
+    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_g16,
+                   m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
+    for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
+        if (dev[i]) hipFree(dev[i]);
+    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = NULL;
+    m->d_g16 = NULL;
+    m->d_amax = NULL;
+    m->d_rtok = m->d_rpos = m->d_rslot = NULL;
+    m->max_rows = 0;
+}
+
+/* (Re)allocate the per-row activation buffers for R rows.  Captured graphs
+ * hold the old addresses, so they are dropped. */
+static int alloc_rows(LMModel *m, int R)
+{
+    if (m->stream && hipStreamSynchronize(m->stream) != hipSuccess) return LM_ERR_HIP;
+    drop_graphs(m);
+    free_rows(m);
+    const size_t r = (size_t)R, D = m->D, F = m->F, NQ = m->NQ, V = m->V;
+    int st;
+    if ((st = dev_alloc((void **)&m->d_x, r * D * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_q, r * NQ * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_attn, r * NQ * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_g, r * F * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_g16, r * F * 2))) return st;
+    if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
+    if ((st = dev_alloc((void **)&m->d_rtok, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_rpos, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_rslot, r * 4))) return st;
+    m->max_rows = R;
+    return LM_OK;
 }
 
 static int supported_k(int k)
@@ -297,7 +339,6 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if (max_seq > (1 << 16) || max_batch > 4096) FAIL(LM_ERR_RANGE);
     m->max_batch = max_batch;
     m->max_seq = max_seq;
-    m->max_rows = max_batch;
     m->cls_nblk = lmk_cls_nblk(m->V);
     m->use_graph = 1;
     m->decode_path = 0;
@@ -308,7 +349,9 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     m->off_w2 = m->off_w13 + 2 * F * D;
     m->layer_elems = m->off_w2 + D * F;
     m->kv_layer_elems = (size_t)max_batch * m->Hkv * max_seq * m->hd;
-    const size_t R = m->max_rows;
+    const size_t NB = (size_t)max_batch;
+    m->step_graph = (hipGraphExec_t(*)[2])calloc(NB + 1, sizeof(*m->step_graph));
+    if (!m->step_graph) FAIL(LM_ERR_OOM);
 
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) FAIL(LM_ERR_HIP);
     if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
@@ -326,14 +369,10 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_rope_cos, (size_t)max_seq * m->hd / 2 * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_rope_sin, (size_t)max_seq * m->hd / 2 * 4))) goto fail;
     if ((st = alloc_kv(m))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_x, R * D * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_q, R * NQ * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_g, R * F * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_logits, R * V * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_attn, R * NQ * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_amax, R * m->cls_nblk * sizeof(LMArgPart)))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_tok, R * 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_pos, R * 4))) goto fail;
+    if ((st = alloc_rows(m, max_batch))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_tok, NB * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
     m->pl_grid = lmk_persist_grid();
     m->pl_ok = m->pl_grid > 0 && lmk_persist_supported(m->D, m->F, m->hd, m->H);
@@ -362,8 +401,16 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
         if (e1 != hipSuccess || e2 != hipSuccess) FAIL(LM_ERR_HIP);
     }
     if (hipMemset(m->d_hist, 0, (size_t)max_batch * (max_seq + 1) * 4) != hipSuccess ||
-        hipMemset(m->d_pos, 0, R * 4) != hipSuccess || hipMemset(m->d_tok, 0, R * 4) != hipSuccess)
+        hipMemset(m->d_pos, 0, NB * 4) != hipSuccess || hipMemset(m->d_tok, 0, NB * 4) != hipSuccess)
         FAIL(LM_ERR_HIP);
+    {
+        int *ids = (int *)malloc(NB * 4);
+        if (!ids) FAIL(LM_ERR_OOM);
+        for (int b = 0; b < max_batch; b++) ids[b] = b;
+        hipError_t e = hipMemcpy(m->d_slot_id, ids, NB * 4, hipMemcpyHostToDevice);
+        free(ids);
+        if (e != hipSuccess) FAIL(LM_ERR_HIP);
+    }
     if (hipDeviceSynchronize() != hipSuccess) FAIL(LM_ERR_HIP);
     if (status) *status = LM_OK;
     return m;
@@ -401,10 +448,12 @@ void lm_free(LMModel *m)
     if (!m) return;
     if (m->stream) hipStreamSynchronize(m->stream);
     drop_graphs(m);
+    free(m->step_graph);
+    free_rows(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_x, m->d_q, m->d_g, m->d_logits, m->d_attn, m->d_amax,
-                   m->d_tok, m->d_pos, m->d_hist, m->d_ll, m->d_ptok, m->d_err};
+                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_ll, m->d_ptok,
+                   m->d_err};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_logits) hipHostFree(m->h_logits);
@@ -475,8 +524,8 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
                           m->max_seq));
         break;
     case LM_KERN_ATTN:
-        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
-                             m->max_seq, m->d_attn));
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
+                             m->hd, m->max_seq, m->d_attn));
         break;
     case LM_KERN_WO:
         KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
@@ -514,6 +563,77 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
     return enqueue_kernel(m, B, LM_KERN_ARGMAX, 0, NULL);
 }
 
+/* ------------------------------------------------------------------------- */
+/* MFMA path: prefill rows and decode batches above MAX_GEMV_B                 */
+/* ------------------------------------------------------------------------- */
+
+/* Largest decode batch of the MFMA decode step (one 64-row tile). */
+#define MAX_GEMM_B 64
+/* Rows per prefill chunk (whole sequences). */
+#define PREFILL_ROWS 2048
+
+/* Queue the layers for M rows (row r: token tok[r], position pos[r], cache slot
+ * slot[r]; the K/V of every row is appended to the cache before attention, so
+ * rows of one sequence attend causally to each other), then with with_cls the
+ * final rmsnorm + classifier of all M rows: logits to `logits` (may be NULL)
+ * and argmax partials to d_amax. */
+static int enqueue_rows(LMModel *m, int M, const int *tok, const int *pos, const int *slot,
+                        float *logits, int with_cls)
+{
+    hipStream_t s = m->stream;
+    const int D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV;
+    LMEpilogue ep;
+    for (int l = 0; l < m->L; l++) {
+        const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
+        const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
+        void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
+        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok, m->d_rstd));
+        memset(&ep, 0, sizeof(ep));
+        ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
+        ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
+        ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
+        KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_att + (size_t)l * D, lw, M,
+                      NQ + 2 * NKV, D, LMK_EPI_QKV, &ep));
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
+                             m->max_seq, m->d_attn));
+        memset(&ep, 0, sizeof(ep));
+        ep.out = m->d_x; ep.ldc = D;
+        KCHK(lmk_gemm(s, LMK_A_F32, m->d_attn, NQ, NULL, NULL, lw + m->off_wo, M, D, NQ,
+                      LMK_EPI_RESID, &ep));
+        KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rstd));
+        memset(&ep, 0, sizeof(ep));
+        ep.g = m->d_g16; ep.F = F;
+        KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_ffn + (size_t)l * D,
+                      lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
+        memset(&ep, 0, sizeof(ep));
+        ep.out = m->d_x; ep.ldc = D;
+        KCHK(lmk_gemm(s, LMK_A_F16, m->d_g16, F, NULL, NULL, lw + m->off_w2, M, D, F,
+                      LMK_EPI_RESID, &ep));
+    }
+    if (!with_cls) return LM_OK;
+    KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rstd));
+    memset(&ep, 0, sizeof(ep));
+    ep.out = logits; ep.ldc = m->V; ep.part = m->d_amax;
+    KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_final, m->d_wcls, M, m->V, D,
+                  LMK_EPI_STORE, &ep));
+    return LM_OK;
+}
+
+/* One greedy decode step of rows 0..B-1 on the MFMA path (slot b = row b). */
+static int enqueue_decode_gemm(LMModel *m, int B, float *logits)
+{
+    int rc = enqueue_rows(m, B, m->d_tok, m->d_pos, m->d_slot_id, logits, 1);
+    if (rc) return rc;
+    KCHK(lmk_argmax_final(m->stream, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
+                          m->max_seq + 1));
+    return LM_OK;
+}
+
+static int enqueue_decode(LMModel *m, int B, float *logits)
+{
+    return B <= MAX_GEMV_B ? enqueue_decode_gemv(m, B, logits) : enqueue_decode_gemm(m, B, logits);
+}
+
 /* Greedy steps captured per multi-step graph. */
 #define GRAPH_STEPS 16
 
@@ -522,14 +642,14 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
  * the logits to d_logits; multi-step runs only feed the argmax forward. */
 static int run_decode_steps(LMModel *m, int B, int nsteps)
 {
-    if (B > MAX_GEMV_B) {
-        fprintf(stderr, "stories_lm: decode batch %d > %d not supported yet\n", B, MAX_GEMV_B);
+    if (B > MAX_GEMM_B) {
+        fprintf(stderr, "stories_lm: decode batch %d > %d not supported\n", B, MAX_GEMM_B);
         return LM_ERR_UNSUPPORTED;
     }
     if (nsteps != 1 && nsteps != GRAPH_STEPS) return LM_ERR_INVALID;
     if (!m->use_graph) {
         for (int t = 0; t < nsteps; t++) {
-            int rc = enqueue_decode_gemv(m, B, nsteps == 1 ? m->d_logits : NULL);
+            int rc = enqueue_decode(m, B, nsteps == 1 ? m->d_logits : NULL);
             if (rc) return rc;
         }
         return LM_OK;
@@ -540,7 +660,7 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
         HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         int rc = LM_OK;
         for (int t = 0; t < nsteps && rc == LM_OK; t++)
-            rc = enqueue_decode_gemv(m, B, nsteps == 1 ? m->d_logits : NULL);
+            rc = enqueue_decode(m, B, nsteps == 1 ? m->d_logits : NULL);
         hipError_t e = hipStreamEndCapture(m->stream, &g);
         if (rc) return rc;
         HIPCHK(e);
@@ -717,30 +837,115 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
     return LM_OK;
 }
 
-/* Prefill by decode steps (KV-cache semantics, training/dashboard.py:205-267):
- * row t of the S x V logits is the step at position pos0 + t. */
+/* Final rmsnorm + classifier of M rows held in x_rows (fp32 [M, D]): logits to
+ * d_logits, argmax partials to d_amax. */
+static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
+{
+    hipStream_t s = m->stream;
+    LMEpilogue ep;
+    KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, m->d_rstd));
+    memset(&ep, 0, sizeof(ep));
+    ep.out = m->d_logits; ep.ldc = m->V; ep.part = m->d_amax;
+    KCHK(lmk_gemm(s, LMK_A_F32_NORM, x_rows, m->D, m->d_rstd, m->d_rms_final, m->d_wcls, M, m->V,
+                  m->D, LMK_EPI_STORE, &ep));
+    return LM_OK;
+}
+
+/* Causal forward of nseq sequences of S tokens (sequence i: slot slots[i],
+ * positions pos0[i] .. pos0[i]+S-1, positions below pos0[i] already cached)
+ * on the MFMA path, in chunks of whole sequences.  logits_mode LM_LOGITS_ALL:
+ * every row's logits; LM_LOGITS_LAST: the last row of each sequence.  Host
+ * `logits` (may be NULL) receives them in sequence order; the last chunk's
+ * logits stay in d_logits. */
+static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, const int *tokens,
+                       int S, int logits_mode, float *logits)
+{
+    const int V = m->V;
+    for (int i = 0; i < nseq; i++) {
+        if (slots[i] < 0 || slots[i] >= m->max_batch || pos0[i] < 0 || pos0[i] + S > m->max_seq) {
+            fprintf(stderr, "stories_lm: prefill sequence %d: slot %d / positions %d..%d out of "
+                    "range (max_batch %d, max_seq %d)\n", i, slots[i], pos0[i], pos0[i] + S - 1,
+                    m->max_batch, m->max_seq);
+            return LM_ERR_RANGE;
+        }
+        for (int t = 0; t < S; t++)
+            if (tokens[(size_t)i * S + t] < 0 || tokens[(size_t)i * S + t] >= V) {
+                fprintf(stderr, "stories_lm: prefill token %d out of range [0,%d)\n",
+                        tokens[(size_t)i * S + t], V);
+                return LM_ERR_RANGE;
+            }
+    }
+    const int cs = S >= PREFILL_ROWS ? 1 : PREFILL_ROWS / S;   /* sequences per chunk */
+    const int chunk_rows = (nseq < cs ? nseq : cs) * S;
+    int rc;
+    if (chunk_rows > m->max_rows && (rc = alloc_rows(m, chunk_rows))) return rc;
+    int *h = (int *)malloc((size_t)3 * chunk_rows * sizeof(int));
+    if (!h) return LM_ERR_OOM;
+    rc = LM_OK;
+    for (int i0 = 0; i0 < nseq && rc == LM_OK; i0 += cs) {
+        const int n = nseq - i0 < cs ? nseq - i0 : cs;
+        const int R = n * S;
+        for (int i = 0; i < n; i++)
+            for (int t = 0; t < S; t++) {
+                const int r = i * S + t;
+                h[r] = tokens[(size_t)(i0 + i) * S + t];
+                h[R + r] = pos0[i0 + i] + t;
+                h[2 * R + r] = slots[i0 + i];
+            }
+        if (hipMemcpyAsync(m->d_rtok, h, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+            hipMemcpyAsync(m->d_rpos, h + R, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+            hipMemcpyAsync(m->d_rslot, h + 2 * R, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess) {
+            rc = LM_ERR_HIP;
+            break;
+        }
+        if (logits_mode == LM_LOGITS_ALL) {
+            rc = enqueue_rows(m, R, m->d_rtok, m->d_rpos, m->d_rslot, m->d_logits, 1);
+            if (rc == LM_OK && logits &&
+                hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
+                               hipMemcpyDeviceToHost, m->stream) != hipSuccess)
+                rc = LM_ERR_HIP;
+        } else {
+            rc = enqueue_rows(m, R, m->d_rtok, m->d_rpos, m->d_rslot, NULL, 0);
+            /* gather the last row of each sequence into d_attn (same row width) */
+            if (rc == LM_OK &&
+                hipMemcpy2DAsync(m->d_attn, (size_t)m->D * 4, m->d_x + (size_t)(S - 1) * m->D,
+                                 (size_t)S * m->D * 4, (size_t)m->D * 4, n,
+                                 hipMemcpyDeviceToDevice, m->stream) != hipSuccess)
+                rc = LM_ERR_HIP;
+            if (rc == LM_OK) rc = enqueue_cls_rows(m, m->d_attn, n);
+            if (rc == LM_OK && logits &&
+                hipMemcpyAsync(logits + (size_t)i0 * V, m->d_logits, (size_t)n * V * 4,
+                               hipMemcpyDeviceToHost, m->stream) != hipSuccess)
+                rc = LM_ERR_HIP;
+        }
+        if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
+    }
+    free(h);
+    return rc;
+}
+
 int lm_prefill(LMModel *m, int slot, int pos0, const int *tokens, int S, float *logits)
 {
     if (!m || !tokens || S < 1) return LM_ERR_INVALID;
     if (slot < 0 || slot >= m->max_batch || pos0 < 0 || pos0 + S > m->max_seq) return LM_ERR_RANGE;
-    if (slot != 0) {
-        fprintf(stderr, "stories_lm: lm_prefill: slot %d needs the batched path\n", slot);
-        return LM_ERR_UNSUPPORTED;
-    }
-    for (int t = 0; t < S; t++) {
-        int p = pos0 + t;
-        const float *row = lm_forward(m, tokens[t], p);
-        if (!row) return LM_ERR_HIP;
-        if (logits) memcpy(logits + (size_t)t * m->V, row, (size_t)m->V * 4);
-    }
-    return LM_OK;
+    return run_prefill(m, 1, &slot, &pos0, tokens, S, LM_LOGITS_ALL, logits);
 }
 
 int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens, int S,
                      int logits_mode, float *logits)
 {
-    (void)m; (void)nseq; (void)slots; (void)tokens; (void)S; (void)logits_mode; (void)logits;
-    return LM_ERR_UNSUPPORTED;
+    if (!m || !tokens || nseq < 1 || S < 1 ||
+        (logits_mode != LM_LOGITS_ALL && logits_mode != LM_LOGITS_LAST))
+        return LM_ERR_INVALID;
+    int *sl = (int *)malloc((size_t)nseq * 2 * sizeof(int));
+    if (!sl) return LM_ERR_OOM;
+    for (int i = 0; i < nseq; i++) {
+        sl[i] = slots ? slots[i] : i;
+        sl[nseq + i] = 0;
+    }
+    int rc = run_prefill(m, nseq, sl, sl + nseq, tokens, S, logits_mode, logits);
+    free(sl);
+    return rc;
 }
 
 int lm_read_logits(LMModel *m, int row0, int nrows, float *dst)
@@ -850,4 +1055,38 @@ int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int 
         HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
     return rc;
+}
+
+/* Diagnostics: one MFMA GEMM C = A W^T on caller data (plain store epilogue
+ * with argmax partials).  A is fp16 bits [M, K] (a_f32 == 0) or fp32 [M, K];
+ * W fp16 bits [N, K]; C fp32 [M, N]; part (may be NULL) [M, ceil(N/32)]. */
+int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16_t *W, float *C,
+                     LMArgPartHost *part)
+{
+    if (M < 1 || N < 1 || K < 32 || K % 32 || !A || !W || !C) return LM_ERR_INVALID;
+    int rc = lm_init();
+    if (rc) return rc;
+    const size_t asz = (size_t)M * K * (a_f32 ? 4 : 2), wsz = (size_t)N * K * 2;
+    const size_t csz = (size_t)M * N * 4, np = (size_t)M * ((N + 31) / 32);
+    void *dA = NULL, *dW = NULL, *dC = NULL, *dP = NULL;
+    hipError_t e = hipMalloc(&dA, asz);
+    if (e == hipSuccess) e = hipMalloc(&dW, wsz);
+    if (e == hipSuccess) e = hipMalloc(&dC, csz);
+    if (e == hipSuccess) e = hipMalloc(&dP, np * sizeof(LMArgPart));
+    if (e == hipSuccess) e = hipMemcpy(dA, A, asz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dW, W, wsz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(dC, 0xFF, csz);
+    if (e == hipSuccess) {
+        LMEpilogue ep;
+        memset(&ep, 0, sizeof(ep));
+        ep.out = (float *)dC; ep.ldc = N; ep.part = (LMArgPart *)dP;
+        e = (hipError_t)lmk_gemm(0, a_f32 ? LMK_A_F32 : LMK_A_F16, dA, K, NULL, NULL,
+                                 (const uint16_t *)dW, M, N, K, LMK_EPI_STORE, &ep);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(C, dC, csz, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && part) e = hipMemcpy(part, dP, np * sizeof(LMArgPart), hipMemcpyDeviceToHost);
+    hipFree(dA); hipFree(dW); hipFree(dC); hipFree(dP);
+    HIPCHK(e);
+    return LM_OK;
 }

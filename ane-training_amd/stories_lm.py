@@ -106,6 +106,7 @@ def lib():
         "lm_rope_table": (I, [I, I, fp, fp]),
         "lm_selftest_reduce": (I, [fp, fp]),
         "lm_profile_decode": (I, [P, I, ip, ip, I, fp, ip]),
+        "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -223,6 +224,25 @@ def selftest_reduce(x: np.ndarray) -> np.ndarray:
     rc = lib().lm_selftest_reduce(_fp(x), _fp(out))
     if rc:
         raise LMError(rc, "lm_selftest_reduce")
+    return out
+
+
+def selftest_gemm(A: np.ndarray, W16: np.ndarray, want_parts: bool = False):
+    """C = A W^T through the device MFMA GEMM.  A: fp32 [M, K] (rounded to fp16
+    on the device) or uint16 fp16 bits; W16: uint16 fp16 bits [N, K]."""
+    a_f32 = A.dtype == np.float32
+    A = np.ascontiguousarray(A)
+    W16 = np.ascontiguousarray(W16, dtype=np.uint16)
+    M, K = A.shape
+    N = W16.shape[0]
+    out = np.empty((M, N), dtype=np.float32)
+    parts = np.empty((M, (N + 31) // 32, 2), dtype=np.int32) if want_parts else None
+    rc = lib().lm_selftest_gemm(M, N, K, int(a_f32), A.ctypes.data, _u16p(W16), _fp(out),
+                                parts.ctypes.data if parts is not None else None)
+    if rc:
+        raise LMError(rc, "lm_selftest_gemm")
+    if want_parts:
+        return out, parts[..., 0].view(np.float32), parts[..., 1]
     return out
 
 

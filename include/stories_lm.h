@@ -251,6 +251,17 @@ int lm_rope_table(int max_seq, int head_dim, float *cos_out, float *sin_out);
  * 0..31, sum of lanes 32..63, wave sum (DPP), wave sum (shuffles)}. */
 int lm_selftest_reduce(const float *in64, float *out4);
 
+/* Argmax partial as the kernels write it: best value and its column. */
+typedef struct { float val; int idx; } LMArgPartHost;
+
+/* Run one MFMA GEMM C = A W^T (fp32 accumulation) on caller data through the
+ * same kernels the prefill and batched decode use (M <= 64: decode kernel,
+ * else the LDS-tiled kernel): A [M, K] fp16 bits (a_f32 = 0) or fp32 (a_f32 =
+ * 1, rounded to fp16 on load), W [N, K] fp16 bits, C [M, N] fp32, part (may be
+ * NULL) [M, ceil(N/32)] per-32-column argmax partials.  K % 32 == 0. */
+int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16_t *W,
+                     float *C, LMArgPartHost *part);
+
 /* Kernel families of a decode step (index into lm_profile_decode's output). */
 #define LM_KERN_QKV    0   /* rmsnorm + QKV GEMV + RoPE + KV append          */
 #define LM_KERN_ATTN   1   /* causal attention over the KV cache            */

@@ -1,0 +1,200 @@
+"""MFMA paths on the GPU against the CPU oracle, through the C ABI: causal
+prefill (lm_prefill / lm_prefill_batch, the training-shape forward of
+training/forward.h:104-170) and batched greedy decode above the GEMV batch
+limit (lm_forward_batch / lm_generate_greedy with B > 4).
+
+These paths round the GEMM inputs (normalised activations, attention output,
+gate) to fp16 for the MFMA units, with fp32 accumulation and an fp32 residual
+stream, so logits are held to the north-star bound atol 2e-2 + rtol 1e-2, and
+the mean absolute error must stay below 2e-3.  Greedy ids may only leave the
+oracle's trajectory at a step where the oracle's top-2 logit margin is below
+the same 2e-2 (a near tie that fp16 rounding may flip).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, TINY, TINY_GQA, TINY_HD128, cfg7
+
+pytestmark = pytest.mark.gpu
+NS = dict(rtol=1e-2, atol=2e-2)
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def close_enough(got, ref):
+    np.testing.assert_allclose(got, ref, **NS)
+    assert float(np.abs(got - ref).mean()) < 2e-3
+
+
+def make(lm, d, seed, max_batch, max_seq, kv32=False):
+    cfg = lm.make_config(**d)
+    w16 = lm.synth_weights_f16(cfg, seed, 0.02, True)
+    m = lm.Model.create(cfg, w16, True, max_batch, max_seq)
+    if kv32:
+        m.set_option(lm.LM_OPT_KV_F32, 1)
+    return m, w16
+
+
+def check_greedy(ids, ref_ids, ref_logits):
+    bad = np.where(ids != ref_ids)[0]
+    if bad.size:
+        s = bad[0]
+        top = np.sort(ref_logits[s])[::-1]
+        assert top[0] - top[1] < 2e-2, f"step {s}: ids differ, oracle margin {top[0] - top[1]}"
+
+
+@pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
+@pytest.mark.parametrize("kv", [32, 16])
+def test_prefill_matches_fixture_then_decode_continues(lm, name, d, kv):
+    _say(f"[prefill {name} kv{kv}]")
+    fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
+    m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
+    toks = fx["tokens"]
+    lg = m.prefill(toks[:30])
+    close_enough(lg, fx[f"logits_kv{kv}"][:30])
+    # the cache filled by the prefill serves the decode steps that follow
+    for p in range(30, 40):
+        row = m.forward(int(toks[p]), p)
+        close_enough(row, fx[f"logits_kv{kv}"][p])
+    m.close()
+
+
+def test_prefill_at_offset(lm, orc):
+    """Two prefill calls (positions 0..11, then 12..29) equal one of 30."""
+    _say("[prefill offset]")
+    d = TINY
+    m, w16 = make(lm, d, 41, 2, 64)
+    toks = np.random.default_rng(41).integers(0, d["vocab_size"], 30).astype(np.int32)
+    a = m.prefill(toks, slot=1)
+    b0 = m.prefill(toks[:12], slot=0)
+    b1 = m.prefill(toks[12:], slot=0, pos0=12)
+    np.testing.assert_allclose(np.concatenate([b0, b1]), a, rtol=0, atol=1e-5)
+    o = orc.Oracle(cfg7(d), lm.f16_to_f32(w16), True, 64, kv_f16=True)
+    close_enough(a, o.forward_full(toks))
+    m.close()
+
+
+@pytest.mark.parametrize("mode", ["all", "last"])
+def test_prefill_batch_matches_oracle(lm, orc, mode):
+    _say(f"[prefill batch {mode}]")
+    d = TINY_GQA
+    m, w16 = make(lm, d, 42, 5, 96)
+    rng = np.random.default_rng(42)
+    toks = rng.integers(0, d["vocab_size"], (5, 33)).astype(np.int32)
+    slots = np.array([3, 0, 4, 1, 2], np.int32)
+    md = lm.LM_LOGITS_ALL if mode == "all" else lm.LM_LOGITS_LAST
+    lg = m.prefill_batch(toks, slots=slots, mode=md)
+    w32 = lm.f16_to_f32(w16)
+    for i in range(5):
+        ref = orc.Oracle(cfg7(d), w32, True, 96, kv_f16=True).forward_full(toks[i])
+        got = lg[i * 33:(i + 1) * 33] if mode == "all" else lg[i]
+        close_enough(got, ref if mode == "all" else ref[-1])
+    # every slot's cache now continues its own sequence
+    nxt = rng.integers(0, d["vocab_size"], 5).astype(np.int32)
+    order = np.argsort(slots)
+    lgd, _ = m.forward_batch(nxt[order], np.full(5, 33, np.int32))
+    for j, i in enumerate(order):
+        o = orc.Oracle(cfg7(d), w32, True, 96, kv_f16=True)
+        ref = o.forward_full(np.concatenate([toks[i], [nxt[i]]]))[-1]
+        close_enough(lgd[j], ref)
+    m.close()
+
+
+def test_prefill_chunks_whole_sequences(lm, orc):
+    """7 sequences of 400 tokens: 5 per 2048-row chunk, so two chunks."""
+    _say("[prefill chunks]")
+    d = dict(TINY, seq_len=400)
+    m, w16 = make(lm, d, 43, 7, 400)
+    toks = np.random.default_rng(43).integers(0, d["vocab_size"], (7, 400)).astype(np.int32)
+    lg = m.prefill_batch(toks, mode=lm.LM_LOGITS_LAST)
+    w32 = lm.f16_to_f32(w16)
+    for i in (0, 4, 5, 6):
+        ref = orc.Oracle(cfg7(d), w32, True, 400, kv_f16=True).forward_full(toks[i])[-1]
+        close_enough(lg[i], ref)
+    m.close()
+
+
+@pytest.mark.parametrize("B", [5, 16, 33, 64])
+def test_batched_decode_matches_oracle(lm, orc, B):
+    """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
+    decode path) against the oracle, then greedy runs."""
+    _say(f"[batched decode B={B}]")
+    d = TINY
+    m, w16 = make(lm, d, 44 + B, B, 80)
+    w32 = lm.f16_to_f32(w16)
+    rng = np.random.default_rng(B)
+    P = 12
+    seqs = rng.integers(0, d["vocab_size"], (B, P + 6)).astype(np.int32)
+    m.prefill_batch(seqs[:, :P], mode=lm.LM_LOGITS_LAST, want_logits=False)
+    check = sorted({0, B // 2, B - 1})
+    orcs = {b: orc.Oracle(cfg7(d), w32, True, 80, kv_f16=True) for b in check}
+    for b in check:
+        orcs[b].forward_full(seqs[b, :P])           # fills the oracle's cache
+        for t in range(P):
+            orcs[b].decode_step(int(seqs[b, t]), t)
+    for t in range(P, P + 6):
+        lg, am = m.forward_batch(seqs[:, t], np.full(B, t, np.int32))
+        for b in check:
+            ref = orcs[b].decode_step(int(seqs[b, t]), t)
+            close_enough(lg[b], ref)
+    # greedy from position P+6 on every slot
+    first = rng.integers(0, d["vocab_size"], B).astype(np.int32)
+    ids = m.generate_greedy(first, np.full(B, P + 6, np.int32), 20)
+    for b in check:
+        ref_ids, ref_lg = orcs[b].greedy(int(first[b]), P + 6, 20, want_logits=True)
+        check_greedy(ids[:, b], ref_ids, ref_lg)
+    m.close()
+
+
+def test_batched_decode_graph_equals_direct(lm):
+    _say("[batched graph vs direct]")
+    d = TINY_HD128
+    m1, _ = make(lm, d, 45, 12, 48)
+    m2, _ = make(lm, d, 45, 12, 48)
+    m2.set_option(lm.LM_OPT_USE_GRAPH, 0)
+    first = np.arange(12, dtype=np.int32) * 7
+    a = m1.generate_greedy(first, np.zeros(12, np.int32), 40)
+    b = m2.generate_greedy(first, np.zeros(12, np.int32), 40)
+    assert np.array_equal(a, b)
+    m1.close()
+    m2.close()
+
+
+def test_stories_c1_prefill_logits(lm, orc):
+    """Config C1: 256 uniform prompt tokens, all 256 x 32000 logits."""
+    _say("[stories C1 prefill]")
+    d = lm.STORIES_110M
+    m, w16 = make(lm, d, 1, 1, 256)
+    toks = np.random.default_rng(2024).integers(0, 32000, 256).astype(np.int32)
+    lg = m.prefill(toks)
+    ref = orc.Oracle(cfg7(d), lm.f16_to_f32(w16), True, 256, kv_f16=True).forward_full(toks)
+    close_enough(lg, ref)
+    m.close()
+
+
+def test_stories_c2_batched_decode(lm, orc):
+    """Config C2 shape (64 slots, Stories) on short prompts: 4 sequences checked
+    against the oracle, teacher-forced and greedy."""
+    _say("[stories C2 shape]")
+    d = lm.STORIES_110M
+    m, w16 = make(lm, d, 1, 64, 64)
+    rng = np.random.default_rng(7)
+    P = 24
+    seqs = rng.integers(0, 32000, (64, P)).astype(np.int32)
+    m.prefill_batch(seqs, mode=lm.LM_LOGITS_LAST, want_logits=False)
+    first = rng.integers(0, 32000, 64).astype(np.int32)
+    ids = m.generate_greedy(first, np.full(64, P, np.int32), 8)
+    w32 = lm.f16_to_f32(w16)
+    for b in (0, 21, 42, 63):
+        o = orc.Oracle(cfg7(d), w32, True, 64, kv_f16=True)
+        for t in range(P):
+            o.decode_step(int(seqs[b, t]), t)
+        ref_ids, ref_lg = o.greedy(int(first[b]), P, 8, want_logits=True)
+        check_greedy(ids[:, b], ref_ids, ref_lg)
+    m.close()

@@ -1,0 +1,28 @@
+"""The MFMA GEMM kernels (decode and prefill tilings) against numpy on fp16
+inputs: fp32 accumulation of exactly representable products, so results agree
+with a float64 product to accumulation rounding (rtol 1e-5 of the row scale)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (30, 96, 256), (32, 768, 768), (64, 2304, 768),
+                                   (50, 200, 2048), (64, 768, 5632), (128, 128, 64), (256, 768, 768),
+                                   (200, 2304, 768), (130, 32000, 768), (512, 4096, 2048)])
+@pytest.mark.parametrize("a_f32", [False, True])
+def test_gemm_matches_numpy(lm, M, N, K, a_f32):
+    rng = np.random.default_rng(M * 7 + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float16)
+    Ain = A.astype(np.float32) if a_f32 else A.view(np.uint16)
+    C, pv, pi = lm.selftest_gemm(Ain, W.view(np.uint16), want_parts=True)
+    ref = A.astype(np.float64) @ W.astype(np.float64).T
+    scale = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64)).T
+    assert np.all(np.abs(C - ref) <= 1e-5 * scale + 1e-6)
+    # argmax partials: best of each 32-column block, lowest index on ties
+    nb = (N + 31) // 32
+    for b in range(nb):
+        blk = C[:, b * 32:min(N, b * 32 + 32)]
+        assert np.array_equal(pi[:, b], b * 32 + np.argmax(blk, axis=1))
+        assert np.array_equal(pv[:, b], blk.max(axis=1))
