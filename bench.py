@@ -73,6 +73,111 @@ def cpu_baseline(cfg7, w16, S, n_tokens):
                       f"(oracle/oracle.c restating training/forward.h), {dt:.1f} s"}, ids
 
 
+MFMA_PEAK_TFLOPS = 2500.0      # dense fp16
+
+
+def _timed(m, fn, reps):
+    """Device milliseconds per call of fn over reps calls (hipEvents on the
+    model's stream; fn's host copies of the results are excluded by design of
+    the calls used: they keep logits on the device)."""
+    fn()
+    m.sync()
+    m.timer_begin()
+    for _ in range(reps):
+        fn()
+    return m.timer_end() / reps
+
+
+def model_bytes(cfg):
+    D, F, V, L = cfg.dim, cfg.hidden_dim, abs(cfg.vocab_size), cfg.n_layers
+    hd = D // cfg.n_heads
+    NQ, NKV = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    mats = L * ((NQ + 2 * NKV) * D + D * NQ + 3 * F * D) + V * D
+    return 2 * mats, 2 * mats // 2          # bytes of fp16 matrices, matrix parameters
+
+
+def linear_flops(cfg, rows):
+    _, params = model_bytes(cfg)
+    return 2.0 * params * rows
+
+
+def attn_flops_prefill(cfg, S, nseq):
+    hd = cfg.dim // cfg.n_heads
+    return nseq * cfg.n_layers * cfg.n_heads * 2 * 2 * hd * S * (S + 1) / 2
+
+
+def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False):
+    """Configs C1-C4 of the baseline (MFMA paths), as extra entries.  direct:
+    launch decode kernels directly instead of replaying graphs."""
+    out = {}
+    cfg = S.make_config(**S.STORIES_110M)
+    wbytes, _ = model_bytes(cfg)
+    V = 32000
+    # C1: 256-token causal prefill, all 256 x 32000 fp32 logits (kept on the device)
+    m = S.Model.create(cfg, w16_stories, True, 1, 256)
+    toks = np.random.default_rng(101).integers(0, V, 256).astype(np.int32)
+    ms = _timed(m, lambda: m.prefill(toks, want_logits=False), reps_prefill)
+    fl = linear_flops(cfg, 256) + attn_flops_prefill(cfg, 256, 1)
+    by = wbytes + 256 * V * 4
+    out["c1_prefill_256"] = {"value": round(256 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
+                             "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                             "algorithmic_bytes": int(by), "flops": fl}
+    m.close()
+    # C3: 8 x 256 = 2048-token causal forward with all logits (MFMA bound)
+    m = S.Model.create(cfg, w16_stories, True, 8, 256)
+    toks = np.random.default_rng(103).integers(0, V, (8, 256)).astype(np.int32)
+    ms = _timed(m, lambda: m.prefill_batch(toks, mode=S.LM_LOGITS_ALL, want_logits=False), reps_prefill)
+    fl = linear_flops(cfg, 2048) + attn_flops_prefill(cfg, 256, 8)
+    out["c3_forward_8x256"] = {"value": round(2048 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
+                               "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                               "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "flops": fl}
+    m.close()
+    # C2: 64 sequences, 192-token prompts prefilled, then 64 greedy steps each
+    m = S.Model.create(cfg, w16_stories, True, 64, 256)
+    if direct:
+        m.set_option(S.LM_OPT_USE_GRAPH, 0)
+    rng = np.random.default_rng(102)
+    prompts = rng.integers(0, V, (64, 192)).astype(np.int32)
+    ms_pf = _timed(m, lambda: m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST, want_logits=False), 2)
+    lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
+    first = np.argmax(lg, axis=1).astype(np.int32)
+    pos = np.full(64, 192, np.int32)
+    ms = _timed(m, lambda: m.generate_greedy(first, pos, 64), reps_decode)
+    kv_step = 64 * 12 * 2 * 768 * 2 * (192 + 64 / 2 + 0.5)    # mean context 224.5
+    by_step = wbytes + kv_step + 64 * V * 0 + 64 * 2 * 12 * 768 * 2
+    t_step = ms * 1e-3 / 64
+    out["c2_decode_b64"] = {"value": round(64 * 64 / (ms * 1e-3), 1), "unit": "tok/s",
+                            "ms_per_step": round(ms / 64, 4),
+                            "hbm_frac": round(by_step / t_step / 1e9 / HBM_PEAK_GBS, 4),
+                            "algorithmic_bytes_per_step": int(by_step),
+                            "prefill_64x192_tok_s": round(64 * 192 / (ms_pf * 1e-3), 1)}
+    m.close()
+    # C4: scaled Llama-2 model, 32 sequences, 512-token contexts, 128 greedy steps
+    d4 = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
+              seq_len=640)
+    cfg4 = S.make_config(**d4)
+    w4 = S.synth_weights_f16(cfg4, 4, 0.02, True)
+    m = S.Model.create(cfg4, w4, True, 32, 640)
+    if direct:
+        m.set_option(S.LM_OPT_USE_GRAPH, 0)
+    del w4
+    prompts = np.random.default_rng(104).integers(0, V, (32, 512)).astype(np.int32)
+    lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
+    first = np.argmax(lg, axis=1).astype(np.int32)
+    pos = np.full(32, 512, np.int32)
+    ms = _timed(m, lambda: m.generate_greedy(first, pos, 128), 1)
+    wb4, _ = model_bytes(cfg4)
+    kv4 = 32 * 16 * 2 * 2048 * 2 * (512 + 128 / 2 + 0.5)
+    t4 = ms * 1e-3 / 128
+    out["c4_scaled_decode_b32"] = {"value": round(32 * 128 / (ms * 1e-3), 1), "unit": "tok/s",
+                                   "ms_per_step": round(ms / 128, 4),
+                                   "hbm_frac": round((wb4 + kv4) / t4 / 1e9 / HBM_PEAK_GBS, 4),
+                                   "algorithmic_bytes_per_step": int(wb4 + kv4)}
+    m.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,6 +188,7 @@ def main():
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
     ap.add_argument("--cpu-tokens", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs C1-C4")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one MI355X per box); "
@@ -147,6 +253,8 @@ def main():
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "kernel_us_per_launch": {k: round(v, 3) for k, v in us.items()},
     }
+    if not args.no_extra:
+        out["configs"] = bench_extra(S, w16, direct=args.direct)
     if not args.no_cpu:
         cb, cpu_ids = cpu_baseline(cfg.astuple(), w16, S, args.cpu_tokens)
         cb["ids_match_gpu"] = bool(np.array_equal(cpu_ids, ids[:args.cpu_tokens]))
