@@ -277,12 +277,13 @@ __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
  * position (8 dims per lane): K and V of the tile are loaded together, scores
  * are q.k * (1/sqrt(hd)) (forward.h:84), then an online softmax keeps the
  * running (max, sum, weighted V).  The four waves merge through LDS and the
- * normalised head output (forward.h:95-97) goes to out[b, h*HD ..]. */
+ * normalised head output (forward.h:95-97) goes to out[b, h*HD ..] (fp32), or
+ * in fp16 to out16 when that is given (the operand of the Wo GEMM). */
 template <int HD, typename KT>
 __global__ void __launch_bounds__(WG) k_attn_decode(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    float *__restrict__ out)
+    float *__restrict__ out, u16 *__restrict__ out16)
 {
     /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
      * would take 256 registers per lane */
@@ -383,7 +384,8 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
             L = fmaf(sl[w], f, L);
             acc = fmaf(so[w][d], f, acc);
         }
-        out[(size_t)b * H * HD + h * HD + d] = acc / L;
+        if (out16) out16[(size_t)b * H * HD + h * HD + d] = f2h(acc / L);
+        else out[(size_t)b * H * HD + h * HD + d] = acc / L;
     }
 }
 
@@ -662,13 +664,13 @@ extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const 
 
 extern "C" int lmk_attn_decode(hipStream_t s, const float *q, const void *kc, const void *vc,
                                int kv_f32, const int *pos, const int *slot, int B, int H, int Hkv,
-                               int hd, int max_seq, float *out)
+                               int hd, int max_seq, float *out, uint16_t *out16)
 {
     if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv) return hipErrorInvalidValue;
     dim3 grid(H, B);
 #define LAUNCH_ATTN(HD_, KT_)                                                                  \
     hipLaunchKernelGGL((k_attn_decode<HD_, KT_>), grid, dim3(WG), 0, s, q, (const KT_ *)kc,   \
-                       (const KT_ *)vc, pos, slot, H, Hkv, max_seq, out)
+                       (const KT_ *)vc, pos, slot, H, Hkv, max_seq, out, (u16 *)out16)
     if (hd == 64 && kv_f32) LAUNCH_ATTN(64, float);
     else if (hd == 64) LAUNCH_ATTN(64, u16);
     else if (hd == 128 && kv_f32) LAUNCH_ATTN(128, float);

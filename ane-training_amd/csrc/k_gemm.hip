@@ -21,17 +21,30 @@
  * accumulator i holds C[8*(i/4) + 4*(l/32) + i%4][l%32].
  *
  * Two tilings:
- *   k_gemm_tile    M >= 64 rows: work-group tile BM x BN, four waves 2 x 2, K
- *                  staged through double-buffered LDS in steps of 32
+ *   k_gemm_tile    M > 64 rows: work-group tile BM x BN, four waves 2 x 2, K
+ *                  staged through double-buffered LDS in steps of 64
  *   k_gemm_skinny  M <= 64 rows (decode batches): a work-group owns 32 columns
  *                  and all rows; its four waves split K, stream their weight
  *                  fragments straight from HBM into registers (each weight byte
  *                  read once) and add their partial tiles through LDS.
  */
+#include <type_traits>
+
 #include "k_common.h"
 #include "lm_internal.h"
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+/* Compile-time loop: f(std::integral_constant<int, i>) for i in [I, N), so
+ * register arrays are only ever indexed by constants. */
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
 #define GT 256                    /* threads per work-group */
 
@@ -195,9 +208,13 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
 
 /* ---- tiled GEMM (prefill) ------------------------------------------------- */
 
-#define BK 32
-#define LDS_PAD 8   /* halves of padding per LDS row (16 bytes) */
+#define BK 64        /* K per LDS stage */
+#define LDS_PAD 8    /* halves of padding per LDS row (16 bytes) */
 
+/* Three-stage pipeline: while the waves multiply stage k out of one LDS
+ * buffer, stage k+1 sits in registers on its way to the other buffer and
+ * stage k+2 is being fetched from memory, so a global load has two stages of
+ * MFMA work to arrive. */
 template <int BM, int BN, typename AT, bool NORM, int E>
 __global__ void __launch_bounds__(GT) k_gemm_tile(const AT *__restrict__ A, int lda,
                                                   const float *__restrict__ rstd,
@@ -207,9 +224,10 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const AT *__restrict__ A, int 
     constexpr int WM = BM / 2, WN = BN / 2;     /* wave tile */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
     constexpr int LR = BK + LDS_PAD;            /* LDS row stride (halves) */
-    constexpr int ACH = BM * BK / 8 / GT;       /* 16-byte A chunks per thread */
-    constexpr int BCH = BN * BK / 8 / GT;
-    static_assert(ACH >= 1 && BCH >= 1, "tile too small");
+    constexpr int CPR = BK / 8;                 /* 16-byte chunks per tile row */
+    constexpr int ACH = BM * CPR / GT;          /* A chunks per thread */
+    constexpr int BCH = BN * CPR / GT;
+    static_assert(ACH >= 1 && BCH >= 1 && TM >= 1 && TN >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) u16 sa[2][BM * LR];
     __shared__ __attribute__((aligned(16))) u16 sb[2][BN * LR];
 
@@ -219,47 +237,40 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const AT *__restrict__ A, int 
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int M = e.M, N = e.N;
 
-    uint4 ra[ACH], rb[BCH];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int c = 0; c < ACH; c++) {
-            const int idx = tid + c * GT;               /* chunk: row idx/4, k (idx%4)*8 */
-            const int r = min(m0 + idx / (BK / 8), M - 1);
-            ra[c] = load_a8<AT, NORM>(A, lda, r, k0 + (idx % (BK / 8)) * 8, rstd, gain);
-        }
-#pragma unroll
-        for (int c = 0; c < BCH; c++) {
-            const int idx = tid + c * GT;
-            const int r = min(n0 + idx / (BK / 8), N - 1);
-            rb[c] = *(const uint4 *)(W + (size_t)r * K + k0 + (idx % (BK / 8)) * 8);
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < ACH; c++) {
-            const int idx = tid + c * GT;
-            *(uint4 *)(&sa[buf][(idx / (BK / 8)) * LR + (idx % (BK / 8)) * 8]) = ra[c];
-        }
-#pragma unroll
-        for (int c = 0; c < BCH; c++) {
-            const int idx = tid + c * GT;
-            *(uint4 *)(&sb[buf][(idx / (BK / 8)) * LR + (idx % (BK / 8)) * 8]) = rb[c];
-        }
-    };
+    uint4 ra0[ACH], rb0[BCH], ra1[ACH], rb1[BCH];
+    /* register stages are named, not passed by pointer, so they stay in VGPRs */
+#define GLOAD(k0_, RA, RB)                                                                 \
+    do {                                                                                   \
+        const int k0v_ = (k0_);                                                            \
+        static_for<0, ACH>([&](auto c) {                                                   \
+            const int idx = tid + c * GT;                                                  \
+            const int r = min(m0 + idx / CPR, M - 1);                                      \
+            RA[c] = load_a8<AT, NORM>(A, lda, r, k0v_ + (idx % CPR) * 8, rstd, gain);      \
+        });                                                                                \
+        static_for<0, BCH>([&](auto c) {                                                   \
+            const int idx = tid + c * GT;                                                  \
+            const int r = min(n0 + idx / CPR, N - 1);                                      \
+            RB[c] = *(const uint4 *)(W + (size_t)r * K + k0v_ + (idx % CPR) * 8);          \
+        });                                                                                \
+    } while (0)
+#define SSTORE(buf_, RA, RB)                                                               \
+    do {                                                                                   \
+        static_for<0, ACH>([&](auto c) {                                                   \
+            const int idx = tid + c * GT;                                                  \
+            *(uint4 *)(&sa[buf_][(idx / CPR) * LR + (idx % CPR) * 8]) = RA[c];             \
+        });                                                                                \
+        static_for<0, BCH>([&](auto c) {                                                   \
+            const int idx = tid + c * GT;                                                  \
+            *(uint4 *)(&sb[buf_][(idx / CPR) * LR + (idx % CPR) * 8]) = RB[c];             \
+        });                                                                                \
+    } while (0)
 
     f32x16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = (f32x16){};
-
-    const int nk = K / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
             uint4 fa[TM], fb[TN];
@@ -275,11 +286,31 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const AT *__restrict__ A, int 
 #pragma unroll
                 for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
         }
+    };
+
+    const int nk = K / BK;
+    GLOAD(0, ra0, rb0);
+    SSTORE(0, ra0, rb0);
+    if (nk > 1) GLOAD(BK, ra1, rb1);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        /* stage kt from buffer 0; registers 1 hold stage kt+1 */
+        if (kt + 2 < nk) GLOAD((kt + 2) * BK, ra0, rb0);
+        compute(0);
         if (kt + 1 < nk) {
-            sstore(buf ^ 1);
+            SSTORE(1, ra1, rb1);
             __syncthreads();
+            /* stage kt+1 from buffer 1; registers 0 hold stage kt+2 */
+            if (kt + 3 < nk) GLOAD((kt + 3) * BK, ra1, rb1);
+            compute(1);
+            if (kt + 2 < nk) {
+                SSTORE(0, ra0, rb0);
+                __syncthreads();
+            }
         }
     }
+#undef GLOAD
+#undef SSTORE
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -370,49 +401,74 @@ __global__ void __launch_bounds__(GT) k_gemm_skinny(const AT *__restrict__ A, in
     }
 }
 
-/* ---- per-row RMSNorm statistics ---------------------------------------------- */
+/* ---- per-row RMSNorm ------------------------------------------------------------ */
 
-/* One wave per row: rstd[m] = 1/sqrt(mean(x[m]^2) + 1e-5) (forward.h:48-50).
- * With emb != NULL the row is first set to the fp16 embedding row emb[tok[m]]
- * (forward.h:108-110). */
-__global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int D, int M,
+/* One wave per row m (forward.h:46-53): with emb != NULL the row is first set
+ * to the fp16 embedding row emb[tok[m]] (forward.h:108-110); then
+ * xn[m, k] = fp16(x[m, k] * (1/sqrt(mean(x[m]^2) + 1e-5)) * gain[k]), the GEMM
+ * operand of the projection that follows.  The row stays in registers
+ * (D/64 values per lane). */
+template <int D>
+__global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
                                                 const u16 *__restrict__ emb,
                                                 const int *__restrict__ tok,
-                                                float *__restrict__ rstd)
+                                                const float *__restrict__ gain,
+                                                u16 *__restrict__ xn)
 {
+    constexpr int PER = D / 64;              /* values per lane, in chunks of 4 */
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * (GT / 64) + (threadIdx.x >> 6);
     if (m >= M) return;
     float *xr = x + (size_t)m * D;
-    float ss = 0.f;
+    float v[PER];
     if (emb) {
         const u16 *er = emb + (size_t)tok[m] * D;
-        for (int i = lane * 8; i < D; i += 64 * 8) {
-            float f[8];
-            unpack8(*(const uint4 *)(er + i), f);
-            *(float4 *)(xr + i) = make_float4(f[0], f[1], f[2], f[3]);
-            *(float4 *)(xr + i + 4) = make_float4(f[4], f[5], f[6], f[7]);
 #pragma unroll
-            for (int j = 0; j < 8; j++) ss = fmaf(f[j], f[j], ss);
+        for (int c = 0; c < PER / 4; c++) {
+            const uint2 h = *(const uint2 *)(er + c * 256 + lane * 4);
+            const f16x2 a = __builtin_bit_cast(f16x2, h.x), b = __builtin_bit_cast(f16x2, h.y);
+            v[4 * c] = (float)a.x; v[4 * c + 1] = (float)a.y;
+            v[4 * c + 2] = (float)b.x; v[4 * c + 3] = (float)b.y;
+            *(float4 *)(xr + c * 256 + lane * 4) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2],
+                                                               v[4 * c + 3]);
         }
     } else {
-        for (int i = lane * 4; i < D; i += 64 * 4) {
-            const float4 v = *(const float4 *)(xr + i);
-            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+#pragma unroll
+        for (int c = 0; c < PER / 4; c++) {
+            const float4 t = *(const float4 *)(xr + c * 256 + lane * 4);
+            v[4 * c] = t.x; v[4 * c + 1] = t.y; v[4 * c + 2] = t.z; v[4 * c + 3] = t.w;
         }
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) ss = fmaf(v[i], v[i], ss);
     ss = wave_sum(ss);
-    if (lane == 0) rstd[m] = 1.0f / sqrtf(ss / D + 1e-5f);
+    const float rs = 1.0f / sqrtf(ss / D + 1e-5f);
+    u16 *xo = xn + (size_t)m * D;
+#pragma unroll
+    for (int c = 0; c < PER / 4; c++) {
+        const float4 g = *(const float4 *)(gain + c * 256 + lane * 4);
+        const unsigned lo = (unsigned)f2h(v[4 * c] * rs * g.x) | ((unsigned)f2h(v[4 * c + 1] * rs * g.y) << 16);
+        const unsigned hi = (unsigned)f2h(v[4 * c + 2] * rs * g.z) | ((unsigned)f2h(v[4 * c + 3] * rs * g.w) << 16);
+        *(uint2 *)(xo + c * 256 + lane * 4) = make_uint2(lo, hi);
+    }
 }
 
 /* ============================== launchers =================================== */
 
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
-                           float *rstd)
+                           const float *gain, uint16_t *xn)
 {
-    if (M < 1 || D % 8 || (emb && !tok)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rownorm, dim3((M + 3) / 4), dim3(GT), 0, s, x, D, M, emb, tok, rstd);
+    if (M < 1 || (emb && !tok) || !gain || !xn) return hipErrorInvalidValue;
+    dim3 grid((M + 3) / 4);
+    switch (D) {
+    case 256: hipLaunchKernelGGL(k_rownorm<256>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    case 512: hipLaunchKernelGGL(k_rownorm<512>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    case 768: hipLaunchKernelGGL(k_rownorm<768>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    case 1024: hipLaunchKernelGGL(k_rownorm<1024>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    case 2048: hipLaunchKernelGGL(k_rownorm<2048>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -442,14 +498,22 @@ static int launch_gemm(hipStream_t s, const void *A, int lda, const float *rstd,
                                lda, rstd, gain, W, K, e);
         return hipGetLastError();
     }
-    /* prefill tiles: 128 x 128, or 128 x 64 when N is narrow (more work-groups) */
-    if (N >= 2048) {
+    /* prefill tiles: the largest of 128x128, 128x64, 64x64 that still gives
+     * the 256 CUs a work-group each (small M or narrow N take smaller tiles) */
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    const long t12864 = (long)((M + 127) / 128) * ((N + 63) / 64);
+    if (t128 >= 256 || (K % BK)) {
+        if (K % BK) return hipErrorInvalidValue;
         dim3 grid((M + 127) / 128, (N + 127) / 128);
         hipLaunchKernelGGL((k_gemm_tile<128, 128, AT, NORM, E>), grid, dim3(GT), 0, s,
                            (const AT *)A, lda, rstd, gain, W, K, e);
-    } else {
+    } else if (t12864 >= 256) {
         dim3 grid((M + 127) / 128, (N + 63) / 64);
         hipLaunchKernelGGL((k_gemm_tile<128, 64, AT, NORM, E>), grid, dim3(GT), 0, s,
+                           (const AT *)A, lda, rstd, gain, W, K, e);
+    } else {
+        dim3 grid((M + 63) / 64, (N + 63) / 64);
+        hipLaunchKernelGGL((k_gemm_tile<64, 64, AT, NORM, E>), grid, dim3(GT), 0, s,
                            (const AT *)A, lda, rstd, gain, W, K, e);
     }
     return hipGetLastError();

@@ -60,7 +60,7 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * NULL: slot b).  Serves decode rows and prefill rows alike. */
 int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
                     const void *vc, int kv_f32, const int *pos, const int *slot, int B, int H,
-                    int Hkv, int hd, int max_seq, float *out);
+                    int Hkv, int hd, int max_seq, float *out, uint16_t *out16);
 
 /* x[b, r] += Wo[r, :] . attn[b] */
 int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D,
@@ -87,6 +87,14 @@ int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
  * greedy loop state). */
 int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,
                      int *tok, int *pos, int *hist, int hist_stride);
+
+/* ---- prefill attention (k_attn.hip) ----------------------------------------
+ * Rows come in nseq whole sequences of S consecutive rows (consecutive
+ * positions from pos[first row], cache slot slot[first row]); every row's K/V
+ * is already in the cache.  out[r, h*hd ..] = causal attention of row r (fp16). */
+int lmk_attn_prefill(hipStream_t s, const float *q, const void *kc, const void *vc,
+                     int kv_f32, const int *pos, const int *slot, int S, int nseq,
+                     int H, int Hkv, int hd, int max_seq, uint16_t *out);
 
 /* ---- MFMA GEMMs (k_gemm.hip) ----------------------------------------------
  * C[m, n] = sum_k A[m, k] W[n, k], W fp16 [N, K], fp32 accumulation; rows M <= 64
@@ -119,10 +127,10 @@ int lmk_gemm(hipStream_t s, int a_kind, const void *A, int lda, const float *rst
              const float *gain, const uint16_t *W, int M, int N, int K, int epi,
              const LMEpilogue *ep);
 
-/* One wave per row: rstd[m] = 1/sqrt(mean(x[m]^2) + 1e-5); with emb != NULL the
- * row is first set to the embedding row emb[tok[m]]. */
+/* One wave per row: with emb != NULL x[m] is first set to the embedding row
+ * emb[tok[m]]; then xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */
 int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
-                float *rstd);
+                const float *gain, uint16_t *xn);
 
 /* ---- persistent batch-1 decode (k_persist.hip) --------------------------- */
 

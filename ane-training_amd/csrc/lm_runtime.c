@@ -55,6 +55,7 @@ struct LMModel {
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
     float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
+    uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
     int *d_rtok, *d_rpos, *d_rslot;   /* prefill rows: token, position, slot */
     /* per-slot greedy state */
@@ -259,11 +260,11 @@ static void drop_graphs(LMModel *m)
 static void free_rows(LMModel *m)
 {
     void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_g16,
-                   m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
+                   m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = NULL;
-    m->d_g16 = NULL;
+    m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
     m->d_rtok = m->d_rpos = m->d_rslot = NULL;
     m->max_rows = 0;
@@ -283,6 +284,8 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_attn, r * NQ * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_g, r * F * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_g16, r * F * 2))) return st;
+    if ((st = dev_alloc((void **)&m->d_xn16, r * D * 2))) return st;
+    if ((st = dev_alloc((void **)&m->d_a16, r * NQ * 2))) return st;
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
@@ -525,7 +528,7 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
         break;
     case LM_KERN_ATTN:
         KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
-                             m->hd, m->max_seq, m->d_attn));
+                             m->hd, m->max_seq, m->d_attn, NULL));
         break;
     case LM_KERN_WO:
         KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
@@ -574,11 +577,13 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
 
 /* Queue the layers for M rows (row r: token tok[r], position pos[r], cache slot
  * slot[r]; the K/V of every row is appended to the cache before attention, so
- * rows of one sequence attend causally to each other), then with with_cls the
+ * rows of one sequence attend causally to each other; seq_rows > 1: the rows
+ * are whole sequences of seq_rows rows, attended by the MFMA prefill kernel,
+ * else one row per slot, by the decode kernel), then with with_cls the
  * final rmsnorm + classifier of all M rows: logits to `logits` (may be NULL)
  * and argmax partials to d_amax. */
-static int enqueue_rows(LMModel *m, int M, const int *tok, const int *pos, const int *slot,
-                        float *logits, int with_cls)
+static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const int *pos,
+                        const int *slot, float *logits, int with_cls)
 {
     hipStream_t s = m->stream;
     const int D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV;
@@ -587,42 +592,47 @@ static int enqueue_rows(LMModel *m, int M, const int *tok, const int *pos, const
         const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
         const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
         void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
-        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok, m->d_rstd));
+        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok,
+                         m->d_rms_att + (size_t)l * D, m->d_xn16));
         memset(&ep, 0, sizeof(ep));
         ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
         ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
         ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
-        KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_att + (size_t)l * D, lw, M,
-                      NQ + 2 * NKV, D, LMK_EPI_QKV, &ep));
-        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
-                             m->max_seq, m->d_attn));
+        KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, lw, M, NQ + 2 * NKV, D, LMK_EPI_QKV,
+                      &ep));
+        if (seq_rows > 1)
+            KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
+                                  M / seq_rows, m->H, m->Hkv, m->hd, m->max_seq, m->d_a16));
+        else
+            KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
+                                 m->max_seq, NULL, m->d_a16));
         memset(&ep, 0, sizeof(ep));
         ep.out = m->d_x; ep.ldc = D;
-        KCHK(lmk_gemm(s, LMK_A_F32, m->d_attn, NQ, NULL, NULL, lw + m->off_wo, M, D, NQ,
+        KCHK(lmk_gemm(s, LMK_A_F16, m->d_a16, NQ, NULL, NULL, lw + m->off_wo, M, D, NQ,
                       LMK_EPI_RESID, &ep));
-        KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rstd));
+        KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_ffn + (size_t)l * D, m->d_xn16));
         memset(&ep, 0, sizeof(ep));
         ep.g = m->d_g16; ep.F = F;
-        KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_ffn + (size_t)l * D,
-                      lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
+        KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, lw + m->off_w13, M, 2 * F, D,
+                      LMK_EPI_GATE, &ep));
         memset(&ep, 0, sizeof(ep));
         ep.out = m->d_x; ep.ldc = D;
         KCHK(lmk_gemm(s, LMK_A_F16, m->d_g16, F, NULL, NULL, lw + m->off_w2, M, D, F,
                       LMK_EPI_RESID, &ep));
     }
     if (!with_cls) return LM_OK;
-    KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rstd));
+    KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
     ep.out = logits; ep.ldc = m->V; ep.part = m->d_amax;
-    KCHK(lmk_gemm(s, LMK_A_F32_NORM, m->d_x, D, m->d_rstd, m->d_rms_final, m->d_wcls, M, m->V, D,
-                  LMK_EPI_STORE, &ep));
+    KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, m->d_wcls, M, m->V, D, LMK_EPI_STORE,
+                  &ep));
     return LM_OK;
 }
 
 /* One greedy decode step of rows 0..B-1 on the MFMA path (slot b = row b). */
 static int enqueue_decode_gemm(LMModel *m, int B, float *logits)
 {
-    int rc = enqueue_rows(m, B, m->d_tok, m->d_pos, m->d_slot_id, logits, 1);
+    int rc = enqueue_rows(m, B, 1, m->d_tok, m->d_pos, m->d_slot_id, logits, 1);
     if (rc) return rc;
     KCHK(lmk_argmax_final(m->stream, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
                           m->max_seq + 1));
@@ -843,11 +853,11 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
 {
     hipStream_t s = m->stream;
     LMEpilogue ep;
-    KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, m->d_rstd));
+    KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
     ep.out = m->d_logits; ep.ldc = m->V; ep.part = m->d_amax;
-    KCHK(lmk_gemm(s, LMK_A_F32_NORM, x_rows, m->D, m->d_rstd, m->d_rms_final, m->d_wcls, M, m->V,
-                  m->D, LMK_EPI_STORE, &ep));
+    KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, m->D, NULL, NULL, m->d_wcls, M, m->V, m->D,
+                  LMK_EPI_STORE, &ep));
     return LM_OK;
 }
 
@@ -899,13 +909,13 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
             break;
         }
         if (logits_mode == LM_LOGITS_ALL) {
-            rc = enqueue_rows(m, R, m->d_rtok, m->d_rpos, m->d_rslot, m->d_logits, 1);
+            rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, m->d_logits, 1);
             if (rc == LM_OK && logits &&
                 hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
                                hipMemcpyDeviceToHost, m->stream) != hipSuccess)
                 rc = LM_ERR_HIP;
         } else {
-            rc = enqueue_rows(m, R, m->d_rtok, m->d_rpos, m->d_rslot, NULL, 0);
+            rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, NULL, 0);
             /* gather the last row of each sequence into d_attn (same row width) */
             if (rc == LM_OK &&
                 hipMemcpy2DAsync(m->d_attn, (size_t)m->D * 4, m->d_x + (size_t)(S - 1) * m->D,
