@@ -3,16 +3,23 @@
  *
  * Rows of a prefill chunk come in whole sequences of S consecutive rows with
  * consecutive positions.  Work-group (query block, head) takes 128 query rows of
- * one sequence; each of its four waves owns 32 rows.  Keys are visited in
- * tiles of 64 positions, 0 .. (last query position of the block), and for each
- * tile (forward.h:72-99, restated as an online softmax):
- *   S  = Q K^T * (1/sqrt(hd))   32x32x16 f16 MFMAs, fp32 accumulation; keys
- *                               after the query's position are masked (-inf)
- *   m' = max(m, rowmax S); P = exp(S - m'); l = l*exp(m - m') + rowsum P;
- *   O  = O*exp(m - m') + P V    P and V rounded to fp16 for the MFMA
- * and finally out = O / l, in fp16 (the operand of the Wo GEMM).  K (row-major) and V (transposed) of the tile are
- * staged in LDS once per work-group; P goes from the accumulator layout to the
- * operand layout through a per-wave LDS tile.
+ * one sequence; each of its four waves owns 32 of them.  Keys are visited in
+ * tiles of 64 positions, 0 .. (last query position of the block); for each tile
+ * (forward.h:72-99, restated as an online softmax):
+ *   S^T = K Q^T * (1/sqrt(hd))  32x32x16 f16 MFMAs, fp32 accumulation; keys after
+ *                               the query's position are masked (-inf)
+ *   m' = max(m, max_key S); P = exp(S - m'); l = l*exp(m - m') + sum_key P;
+ *   O^T = O^T*exp(m - m') + V^T P^T   P and V rounded to fp16 for the MFMA
+ * and finally out = O / l, in fp16 (the operand of the Wo GEMM).
+ *
+ * Computing the transposed scores puts one query in each accumulator column, so
+ * lane l holds 32 of the tile's 64 scores of query l % 32 (lane l ^ 32 the other
+ * 32): the softmax needs one cross-lane exchange per tile, and the accumulator
+ * already has the layout of the B operand of the V^T P^T product, up to an order
+ * of the 16 keys of each MFMA step.  That order is undone by storing V^T in LDS
+ * with bits 2 and 3 of the key index swapped.  K and V^T of tile t+1 are fetched
+ * into registers while tile t computes, and stored into the other of two LDS
+ * buffers.
  */
 #include "k_common.h"
 #include "lm_internal.h"
@@ -40,22 +47,27 @@ __device__ __forceinline__ uint4 kv8_f16(const float *p)
     return __builtin_bit_cast(uint4, h);
 }
 
+/* LDS column of key k of a tile in V^T: bits 2 and 3 swapped, so that the 8 keys
+ * lane l contributes to an MFMA step (4 from each of two groups of 8) are
+ * contiguous */
+__device__ __forceinline__ int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k >> 1) & 4); }
+
 template <int HD, typename KT>
 __global__ void __launch_bounds__(AT) k_attn_prefill(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int S, int nqb, int H, int Hkv,
     int max_seq, u16 *__restrict__ out)
 {
-    constexpr int KLD = HD + 8;          /* K tile row stride (halves)  */
+    constexpr int KLD = HD + 8;          /* K tile row stride (halves)   */
     constexpr int VLD = BKV + 8;         /* V^T tile row stride (halves) */
-    constexpr int PLD = BKV + 8;         /* P tile row stride (halves)  */
-    constexpr int KS = HD / 16;          /* MFMA k-steps over head dims */
-    constexpr int DT = HD / 32;          /* 32-wide output column tiles */
-    __shared__ __attribute__((aligned(16))) u16 sk[BKV * KLD];
-    __shared__ __attribute__((aligned(16))) u16 svt[HD * VLD];
-    __shared__ __attribute__((aligned(16))) u16 sp[4][32 * PLD];
+    constexpr int KS = HD / 16;          /* MFMA k-steps over head dims  */
+    constexpr int DT = HD / 32;          /* 32-dim row tiles of O^T      */
+    constexpr int CPT = BKV * HD / 8 / AT;   /* 16-byte chunks per thread per array */
+    static_assert(CPT >= 1 && BKV * HD / 8 % AT == 0, "staging shape");
+    __shared__ __attribute__((aligned(16))) u16 sk[2][BKV * KLD];
+    __shared__ __attribute__((aligned(16))) u16 svt[2][HD * VLD];
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int seq = blockIdx.x / nqb, qb = blockIdx.x % nqb;
     const int h = blockIdx.y;
@@ -66,111 +78,143 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     const int p0 = pos[row0];                     /* position of the block's row 0 */
     const int cs = slot[row0];
     const size_t cbase = ((size_t)cs * Hkv + kvh) * max_seq * HD;
-    const float scale = 1.0f / sqrtf((float)HD);
+    /* scores are kept in log2 units: exp(x) = exp2(x * log2 e) */
+    const float scale = 1.4426950408889634f / sqrtf((float)HD);
 
-    /* this wave's query rows: wr0 .. wr0+31 of the block */
+    const int last_pos = p0 + nrows - 1;          /* last query position of the block */
+    const int ntiles = last_pos / BKV + 1;
+
+    /* K / V chunks of one tile: chunk c = tid + i*AT is key c / (HD/8), dims
+     * (c % (HD/8))*8 .. +8; keys past the block's last position repeat it (they
+     * are masked for every query that reads them) */
+    uint4 rk[CPT], rv[CPT];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+            const size_t off = cbase + (size_t)min(kt * BKV + key, last_pos) * HD + d0;
+            rk[i] = kv8_f16(kc + off);
+            rv[i] = kv8_f16(vc + off);
+        }
+    };
+    auto stash = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < CPT; i++) {
+            const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+            *(uint4 *)(&sk[b][key * KLD + d0]) = rk[i];
+            const unsigned vw[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+            const int pk = vperm(key);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                svt[b][(d0 + j) * VLD + pk] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
+        }
+    };
+    fetch(0);
+
+    /* this wave's queries: block rows wr0 .. wr0+31; lane l takes row wr0 + l%32 */
     const int wr0 = wave * 32;
     const bool wave_active = wr0 < nrows;
-    /* Q fragments (A operand): row l%32, dims ks*16 + 8*(l/32) .. +8 */
-    uint4 qa[KS];
+    const int wave_last = p0 + min(wr0 + 31, nrows - 1);
+    const int qrow = wr0 + (lane & 31);
+    const int qp = p0 + qrow;                     /* this lane's query position */
+    /* Q^T fragments (B operand): query l%32, dims ks*16 + 8*(l/32) .. +8 */
+    uint4 qb16[KS];
     {
-        const int r = min(wr0 + (lane & 31), nrows - 1);
-        const float *qp = q + (size_t)(row0 + r) * NQ + h * HD + (lane >> 5) * 8;
+        const float *qs = q + (size_t)(row0 + min(qrow, nrows - 1)) * NQ + h * HD + g * 8;
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) qa[ks] = kv8_f16(qp + ks * 16);
+        for (int ks = 0; ks < KS; ks++) qb16[ks] = kv8_f16(qs + ks * 16);
     }
     f32x16 o[DT];
 #pragma unroll
     for (int j = 0; j < DT; j++) o[j] = (f32x16){};
-    float mrow[16], lrow[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) { mrow[i] = -INFINITY; lrow[i] = 0.f; }
+    float mrow = -INFINITY, lrow = 0.f;
 
-    const int last_pos = p0 + nrows - 1;          /* last query position of the block */
-    const int ntiles = last_pos / BKV + 1;
-    const int wave_last = p0 + min(wr0 + 31, nrows - 1);
+    stash(0);
+    __syncthreads();
     for (int kt = 0; kt < ntiles; kt++) {
+        const int b = kt & 1;
+        if (kt + 1 < ntiles) fetch(kt + 1);
         const int k0 = kt * BKV;
-        /* stage K [key][dim] and V^T [dim][key] of positions k0 .. k0+63 */
-        __syncthreads();
-        for (int c = tid; c < BKV * HD / 8; c += AT) {
-            const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-            const int p = min(k0 + key, last_pos);
-            const uint4 kk = kv8_f16(kc + cbase + (size_t)p * HD + d0);
-            const uint4 vv = kv8_f16(vc + cbase + (size_t)p * HD + d0);
-            *(uint4 *)(&sk[key * KLD + d0]) = kk;
-            const unsigned vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        if (wave_active && k0 <= wave_last) {     /* wave-uniform */
+            const u16 *K = sk[b], *VT = svt[b];
+            /* S^T tiles: rows = keys nt*32 + (0..31), columns = the wave's queries */
+            f32x16 sacc[2];
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                svt[(d0 + j) * VLD + key] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
-        }
-        __syncthreads();
-        if (!wave_active || k0 > wave_last) continue;   /* wave-uniform */
-        /* S = Q K^T for the 2 key column tiles */
-        f32x16 sacc[2];
+            for (int nt = 0; nt < 2; nt++) {
+                sacc[nt] = (f32x16){};
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            sacc[nt] = (f32x16){};
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const uint4 kb = *(const uint4 *)(&sk[(nt * 32 + (lane & 31)) * KLD + ks * 16 +
-                                                      (lane >> 5) * 8]);
-                sacc[nt] = mfma32h(qa[ks], kb, sacc[nt]);
+                for (int ks = 0; ks < KS; ks++) {
+                    const uint4 ka = *(const uint4 *)(&K[(nt * 32 + (lane & 31)) * KLD + ks * 16 + g * 8]);
+                    sacc[nt] = mfma32h(ka, qb16[ks], sacc[nt]);
+                }
             }
+            /* element i of tile nt is key k0 + nt*32 + 8*(i/4) + 4*g + i%4 */
+            float mx = -INFINITY;
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = k0 + nt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                    const float v = key > qp ? -INFINITY : sacc[nt][i] * scale;
+                    sacc[nt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(mrow, mx);
+            /* a query with every key so far masked keeps m = -inf: nothing to scale */
+            const float corr = mn == -INFINITY ? 1.f : exp2f(mrow - mn);
+            const float sub = mn == -INFINITY ? 0.f : mn;
+            float ls = 0.f;
+            uint4 pb[2][2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    f16x8 hv;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float e = exp2f(sacc[nt][8 * hh + j] - sub);
+                        ls += e;
+                        hv[j] = (_Float16)e;
+                    }
+                    pb[nt][hh] = __builtin_bit_cast(uint4, hv);
+                }
+            lrow = lrow * corr + ls;               /* per-lane partial row sum */
+            mrow = mn;
+#pragma unroll
+            for (int j = 0; j < DT; j++) o[j] *= corr;
+            /* O^T += V^T P^T over the 4 steps of 16 keys */
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int j = 0; j < DT; j++) {
+                        const uint4 va = *(const uint4 *)(&VT[(j * 32 + (lane & 31)) * VLD + nt * 32 +
+                                                              hh * 16 + g * 8]);
+                        o[j] = mfma32h(va, pb[nt][hh], o[j]);
+                    }
         }
-        /* mask, online softmax, P to LDS */
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);   /* row within wave */
-            const int qp = p0 + wr0 + r;
-            float s0 = sacc[0][i] * scale, s1 = sacc[1][i] * scale;
-            const int key0 = k0 + (lane & 31), key1 = key0 + 32;
-            if (key0 > qp) s0 = -INFINITY;
-            if (key1 > qp) s1 = -INFINITY;
-            float mx = fmaxf(s0, s1);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float mn = fmaxf(mrow[i], mx);
-            /* rows past the sequence end stay fully masked: mn = -inf */
-            const float corr = mn == -INFINITY ? 1.f : expf(mrow[i] - mn);
-            const float e0 = mn == -INFINITY ? 0.f : expf(s0 - mn);
-            const float e1 = mn == -INFINITY ? 0.f : expf(s1 - mn);
-            lrow[i] = lrow[i] * corr + e0 + e1;        /* per-lane partial row sum */
-            mrow[i] = mn;
-#pragma unroll
-            for (int j = 0; j < DT; j++) o[j][i] *= corr;
-            sp[wave][r * PLD + (lane & 31)] = f2h(e0);
-            sp[wave][r * PLD + 32 + (lane & 31)] = f2h(e1);
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   /* lgkmcnt(0): this wave's P writes landed */
-        __builtin_amdgcn_wave_barrier();
-        /* O += P V : A = P [row][key], B = V^T [dim][key] */
-#pragma unroll
-        for (int ks = 0; ks < BKV / 16; ks++) {
-            const uint4 pa = *(const uint4 *)(&sp[wave][(lane & 31) * PLD + ks * 16 + (lane >> 5) * 8]);
-#pragma unroll
-            for (int j = 0; j < DT; j++) {
-                const uint4 vb = *(const uint4 *)(&svt[(j * 32 + (lane & 31)) * VLD + ks * 16 +
-                                                       (lane >> 5) * 8]);
-                o[j] = mfma32h(pa, vb, o[j]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
+        if (kt + 1 < ntiles) stash(b ^ 1);
+        __syncthreads();
     }
     if (!wave_active) return;
-    /* finish the row sums across the 32 lanes of each half and write O / l */
+    /* finish the row sum across the lane pair and write O / l:
+     * element i of o[j] is dim j*32 + 8*(i/4) + 4*g + i%4 of query l%32 */
+    const float l = lrow + __shfl_xor(lrow, 32, 64);
+    if (qrow < nrows) {
+        const float inv = 1.0f / l;
+        u16 *op = out + (size_t)(row0 + qrow) * NQ + h * HD;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        float l = lrow[i];
+        for (int j = 0; j < DT; j++)
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
-        const int r = wr0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (r < nrows) {
-            const float inv = 1.0f / l;
-#pragma unroll
-            for (int j = 0; j < DT; j++)
-                out[(size_t)(row0 + r) * NQ + h * HD + j * 32 + (lane & 31)] = f2h(o[j][i] * inv);
-        }
+            for (int i4 = 0; i4 < 4; i4++) {
+                const unsigned lo = (unsigned)f2h(o[j][4 * i4] * inv) |
+                                    ((unsigned)f2h(o[j][4 * i4 + 1] * inv) << 16);
+                const unsigned hi = (unsigned)f2h(o[j][4 * i4 + 2] * inv) |
+                                    ((unsigned)f2h(o[j][4 * i4 + 3] * inv) << 16);
+                *(uint2 *)(op + j * 32 + 8 * i4 + 4 * g) = make_uint2(lo, hi);
+            }
     }
 }
 

@@ -4,12 +4,12 @@
  *
  *   C[m, n] = sum_k A[m, k] * W[n, k]      (y = W x per row, forward.h:36-44)
  *
- * W is an fp16 weight matrix [N, K] (row-major, K contiguous), A the
- * activations [M, lda]: fp16, or fp32 converted to fp16 while staging, with the
- * RMSNorm of forward.h:46-53 applied on the way (A * rstd[m] * gain[k]) so a
- * normalised copy of x is never written.  Epilogues (one per call site of
+ * W is an fp16 weight matrix [N, K] (row-major, K contiguous), A the fp16
+ * activations [M, lda] (normalised rows, attention output or gate, each written
+ * once by the kernel that produces it).  Epilogues (one per call site of
  * forward.h:104-170):
- *   EPI_STORE  logits [M, ldc] fp32 (optional) and per-32-column argmax partials
+ *   EPI_STORE  logits [M, ldc] fp32
+ *   EPI_ARGMAX logits (optional) and per-32-column argmax partials (greedy decode)
  *   EPI_RESID  x[m, n] += C                          (forward.h:136, 159)
  *   EPI_GATE   g[m, i] = silu(h1) * h3 in fp16; W1/W3 rows interleaved in
  *              blocks of 16, so h3 sits 16 columns right of h1 (forward.h:149-151)
@@ -22,7 +22,8 @@
  *
  * Two tilings:
  *   k_gemm_tile    M > 64 rows: work-group tile BM x BN, four waves 2 x 2, K
- *                  staged through double-buffered LDS in steps of 64
+ *                  streamed by direct global->LDS loads into a 3-deep ring of
+ *                  64-wide stages; XCD-aware tile order
  *   k_gemm_skinny  M <= 64 rows (decode batches): a work-group owns 32 columns
  *                  and all rows; its four waves split K, stream their weight
  *                  fragments straight from HBM into registers (each weight byte
@@ -50,56 +51,13 @@ __device__ __forceinline__ void static_for(F &&f)
 
 /* ---- operand staging ------------------------------------------------------- */
 
-/* 8 consecutive A elements of row m from k0 as fp16 bits (uint4). */
+/* 8 consecutive A elements of row m from k0 (fp16 bits). */
 template <typename AT, bool NORM>
 __device__ __forceinline__ uint4 load_a8(const AT *__restrict__ A, int lda, int m, int k0,
-                                         const float *__restrict__ rstd,
-                                         const float *__restrict__ gain);
-
-template <>
-__device__ __forceinline__ uint4 load_a8<u16, false>(const u16 *__restrict__ A, int lda, int m,
-                                                     int k0, const float *, const float *)
+                                         const float *__restrict__, const float *__restrict__)
 {
+    static_assert(sizeof(AT) == 2 && !NORM, "fp16 operands only");
     return *(const uint4 *)(A + (size_t)m * lda + k0);
-}
-
-template <bool NORM>
-__device__ __forceinline__ uint4 cvt_a8(const float f[8], float rs, const float *__restrict__ gain,
-                                        int k0)
-{
-    f16x8 h;
-    if (NORM) {
-        const float4 g0 = *(const float4 *)(gain + k0), g1 = *(const float4 *)(gain + k0 + 4);
-        h[0] = (_Float16)(f[0] * rs * g0.x); h[1] = (_Float16)(f[1] * rs * g0.y);
-        h[2] = (_Float16)(f[2] * rs * g0.z); h[3] = (_Float16)(f[3] * rs * g0.w);
-        h[4] = (_Float16)(f[4] * rs * g1.x); h[5] = (_Float16)(f[5] * rs * g1.y);
-        h[6] = (_Float16)(f[6] * rs * g1.z); h[7] = (_Float16)(f[7] * rs * g1.w);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) h[j] = (_Float16)f[j];
-    }
-    return __builtin_bit_cast(uint4, h);
-}
-
-template <>
-__device__ __forceinline__ uint4 load_a8<float, false>(const float *__restrict__ A, int lda, int m,
-                                                       int k0, const float *, const float *)
-{
-    const float *p = A + (size_t)m * lda + k0;
-    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
-    const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    return cvt_a8<false>(f, 1.f, nullptr, k0);
-}
-
-template <>
-__device__ __forceinline__ uint4 load_a8<float, true>(const float *__restrict__ A, int lda, int m,
-                                                      int k0, const float *__restrict__ rstd,
-                                                      const float *__restrict__ gain)
-{
-    const float *p = A + (size_t)m * lda + k0;
-    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
-    const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    return cvt_a8<true>(f, rstd[m], gain, k0);
 }
 
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c)
@@ -125,79 +83,99 @@ struct EpiArgs {
     const float *rope_cos, *rope_sin;
 };
 
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
 
-/* Apply epilogue E to one 32x32 accumulator tile at (m0, n0). */
+/* Apply epilogue E to one 32x32 accumulator tile at (m0, n0).  Every operand
+ * the epilogue reads (residual, positions, rotation angles) is loaded for the
+ * whole tile before the first store: stores the compiler cannot prove disjoint
+ * from those loads would otherwise serialise one memory round trip per element. */
 template <int E>
 __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0, const EpiArgs &e)
 {
     const int lane = threadIdx.x & 63;
     const int n = n0 + (lane & 31);
     const int rbase = m0 + 4 * (lane >> 5);
-    if (E == EPI_STORE) {
+    int rr[16];
+    bool ok[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = rbase + 8 * (i >> 2) + (i & 3);
-            float v = acc[i];
-            const bool ok = r < e.M && n < e.N;
-            if (ok && e.out) e.out[(size_t)r * e.ldc + n] = v;
-            if (e.part) {
-                /* argmax over the 32 columns of this row (lanes of one half) */
-                float bv = ok ? v : -INFINITY;
-                int bi = ok ? n : 0x7FFFFFFF;
+    for (int i = 0; i < 16; i++) {
+        rr[i] = rbase + 8 * (i >> 2) + (i & 3);
+        ok[i] = rr[i] < e.M && n < e.N;
+    }
+    if (E == EPI_STORE || E == EPI_ARGMAX) {
+        if (e.out) {
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = acc[i];
+        }
+        if (E == EPI_ARGMAX) {
+            /* argmax over the 32 columns of each row (the lanes of one half) */
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float bv = ok[i] ? acc[i] : -INFINITY;
+                int bi = ok[i] ? n : 0x7FFFFFFF;
 #pragma unroll
                 for (int off = 16; off > 0; off >>= 1) {
                     const float ov = __shfl_xor(bv, off, 64);
                     const int oi = __shfl_xor(bi, off, 64);
                     argmax_combine(bv, bi, ov, oi);
                 }
-                if ((lane & 31) == 0 && r < e.M && n0 < e.N)
-                    e.part[(size_t)r * e.nparts + n0 / 32] = LMArgPart{bv, bi};
+                if ((lane & 31) == 0 && rr[i] < e.M && n0 < e.N)
+                    e.part[(size_t)rr[i] * e.nparts + n0 / 32] = LMArgPart{bv, bi};
             }
         }
     } else if (E == EPI_RESID) {
+        float xv[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = rbase + 8 * (i >> 2) + (i & 3);
-            if (r < e.M && n < e.N) e.out[(size_t)r * e.ldc + n] += acc[i];
-        }
+        for (int i = 0; i < 16; i++) xv[i] = ok[i] ? e.out[(size_t)rr[i] * e.ldc + n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = xv[i] + acc[i];
     } else if (E == EPI_GATE) {
         /* tile columns 0..15 hold W1 rows 16j.., columns 16..31 the W3 rows */
         const int c = lane & 31;
         const int gi = (n0 / 32) * 16 + (c & 15);
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = rbase + 8 * (i >> 2) + (i & 3);
             const float h3 = __shfl_xor(acc[i], 16, 64);
-            if (c < 16 && r < e.M && n < e.N) {
+            if (c < 16 && ok[i]) {
                 const float h1 = acc[i];
                 const float silu = h1 / (1.0f + expf(-h1));        /* forward.h:101 */
-                e.g[(size_t)r * e.F + gi] = f2h(silu * h3);         /* forward.h:151 */
+                e.g[(size_t)rr[i] * e.F + gi] = f2h(silu * h3);     /* forward.h:151 */
             }
         }
     } else {  /* EPI_QKV */
         const bool odd = n & 1;
         const bool rot = n < e.NQ + e.NKV;
-        const int nn = n < e.NQ ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
+        const bool isq = n < e.NQ;
+        const int nn = isq ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
         const int h = nn / e.hd, d = nn % e.hd;
         const int half_hd = e.hd >> 1;
+        int pr[16], sr[16];
+        float cr[16], sn[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = rbase + 8 * (i >> 2) + (i & 3);
+            const int r = ok[i] ? rr[i] : 0;
+            pr[i] = e.pos[r];
+            sr[i] = isq ? 0 : e.slot[r];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int ti = pr[i] * half_hd + (d >> 1);
+            cr[i] = rot ? e.rope_cos[ti] : 1.f;
+            sn[i] = rot ? e.rope_sin[ti] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
             const float other = __shfl_xor(acc[i], 1, 64);
-            if (r >= e.M || n >= e.N) continue;
-            const int p = e.pos[r];
+            if (!ok[i]) continue;
             float v = acc[i];
-            if (rot) {
-                const int ti = p * half_hd + (d >> 1);
-                const float c = e.rope_cos[ti], s = e.rope_sin[ti];
-                /* pair (a, b) = (even column, odd column), forward.h:62-68 */
-                v = odd ? fmaf(other, s, v * c) : fmaf(v, c, -(other * s));
-            }
-            if (n < e.NQ) {
-                e.q[(size_t)r * e.NQ + n] = v;
+            if (rot)   /* pair (a, b) = (even column, odd column), forward.h:62-68 */
+                v = odd ? fmaf(other, sn[i], v * cr[i]) : fmaf(v, cr[i], -(other * sn[i]));
+            if (isq) {
+                e.q[(size_t)rr[i] * e.NQ + n] = v;
             } else {
-                const size_t off = (((size_t)e.slot[r] * e.Hkv + h) * e.max_seq + p) * e.hd + d;
+                const size_t off = (((size_t)sr[i] * e.Hkv + h) * e.max_seq + pr[i]) * e.hd + d;
                 void *dst = rot ? e.kc : e.vc;
                 if (e.kv_f32) ((float *)dst)[off] = v;
                 else ((u16 *)dst)[off] = f2h(v);
@@ -208,109 +186,129 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
 
 /* ---- tiled GEMM (prefill) ------------------------------------------------- */
 
-#define BK 64        /* K per LDS stage */
-#define LDS_PAD 8    /* halves of padding per LDS row (16 bytes) */
+#define BKH 64                 /* K (halves) per LDS stage: one 128-byte row per tile row */
+#define NSTAGE 3               /* LDS ring depth */
 
-/* Three-stage pipeline: while the waves multiply stage k out of one LDS
- * buffer, stage k+1 sits in registers on its way to the other buffer and
- * stage k+2 is being fetched from memory, so a global load has two stages of
- * MFMA work to arrive. */
-template <int BM, int BN, typename AT, bool NORM, int E>
-__global__ void __launch_bounds__(GT) k_gemm_tile(const AT *__restrict__ A, int lda,
-                                                  const float *__restrict__ rstd,
-                                                  const float *__restrict__ gain,
-                                                  const u16 *__restrict__ W, int K, EpiArgs e)
+/* vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding). */
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 0xF) | ((((n) >> 4) & 3) << 14))
+
+/* Tile rows (A rows, then W rows) live in LDS as 128-byte rows of 8 chunks of
+ * 8 halves; chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 32 rows a
+ * fragment read touches hit distinct banks.  Direct global->LDS loads write
+ * 64 lanes x 16 bytes = 8 consecutive rows per wave instruction, lane l at
+ * slot l % 8 of row l / 8: the swizzle is applied to the source address. */
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+/* 16-byte LDS read issued as inline assembly.  The compiler cannot tell which
+ * LDS buffer its own ds_reads touch relative to the direct global->LDS loads in
+ * flight, and would wait for all of those loads before every read; these reads
+ * are invisible to it, so the kernel waits explicitly: vmcnt + barrier before a
+ * stage's reads, lgkmcnt(0) before the MFMAs use them. */
+__device__ __forceinline__ uint4 lds_read16(const u16 *p)
 {
-    constexpr int WM = BM / 2, WN = BN / 2;     /* wave tile */
+    const unsigned off = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) u16 *)p;
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(off));
+    return __builtin_bit_cast(uint4, v);
+}
+
+template <int BM, int BN, int E>
+__global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
+                                                  const u16 *__restrict__ W, int K, EpiArgs e,
+                                                  int tm, int tn)
+{
+    constexpr int WM = BM / 2, WN = BN / 2;     /* wave tile, waves 2 x 2 */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
-    constexpr int LR = BK + LDS_PAD;            /* LDS row stride (halves) */
-    constexpr int CPR = BK / 8;                 /* 16-byte chunks per tile row */
-    constexpr int ACH = BM * CPR / GT;          /* A chunks per thread */
-    constexpr int BCH = BN * CPR / GT;
-    static_assert(ACH >= 1 && BCH >= 1 && TM >= 1 && TN >= 1, "tile too small");
-    __shared__ __attribute__((aligned(16))) u16 sa[2][BM * LR];
-    __shared__ __attribute__((aligned(16))) u16 sb[2][BN * LR];
+    constexpr int ROWS = BM + BN;               /* tile rows per stage */
+    constexpr int STAGE = ROWS * 64;            /* halves per stage (128 B per row) */
+    constexpr int LDW = ROWS / 8 / 4;           /* load instructions per wave per stage */
+    static_assert(TM >= 1 && TN >= 1 && LDW >= 1 && ROWS % 32 == 0, "tile shape");
+    /* three separate arrays (not one indexed ring) so that the compiler can
+     * tell a stage's LDS reads from the direct loads in flight into the others
+     * and does not wait for those loads */
+    __shared__ __attribute__((aligned(1024))) u16 lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) u16 lds1[STAGE];
+    __shared__ __attribute__((aligned(1024))) u16 lds2[STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    /* XCD-aware tile order: work-group id goes to XCD id % 8; give each XCD a
+     * contiguous run of tiles (M fastest), i.e. a slice of N, so the W rows of
+     * its tiles stay in its own L2. */
+    const int T = tm * tn, id = blockIdx.x;
+    const int g = (T % 8 == 0) ? (id % 8) * (T / 8) + id / 8 : id;
+    const int m0 = (g % tm) * BM, n0 = (g / tm) * BN;
     const int M = e.M, N = e.N;
 
-    uint4 ra0[ACH], rb0[BCH], ra1[ACH], rb1[BCH];
-    /* register stages are named, not passed by pointer, so they stay in VGPRs */
-#define GLOAD(k0_, RA, RB)                                                                 \
-    do {                                                                                   \
-        const int k0v_ = (k0_);                                                            \
-        static_for<0, ACH>([&](auto c) {                                                   \
-            const int idx = tid + c * GT;                                                  \
-            const int r = min(m0 + idx / CPR, M - 1);                                      \
-            RA[c] = load_a8<AT, NORM>(A, lda, r, k0v_ + (idx % CPR) * 8, rstd, gain);      \
-        });                                                                                \
-        static_for<0, BCH>([&](auto c) {                                                   \
-            const int idx = tid + c * GT;                                                  \
-            const int r = min(n0 + idx / CPR, N - 1);                                      \
-            RB[c] = *(const uint4 *)(W + (size_t)r * K + k0v_ + (idx % CPR) * 8);          \
-        });                                                                                \
-    } while (0)
-#define SSTORE(buf_, RA, RB)                                                               \
-    do {                                                                                   \
-        static_for<0, ACH>([&](auto c) {                                                   \
-            const int idx = tid + c * GT;                                                  \
-            *(uint4 *)(&sa[buf_][(idx / CPR) * LR + (idx % CPR) * 8]) = RA[c];             \
-        });                                                                                \
-        static_for<0, BCH>([&](auto c) {                                                   \
-            const int idx = tid + c * GT;                                                  \
-            *(uint4 *)(&sb[buf_][(idx / CPR) * LR + (idx % CPR) * 8]) = RB[c];             \
-        });                                                                                \
-    } while (0)
+    /* per-lane source rows of this wave's load instructions (fixed over k) */
+    const u16 *src[LDW];
+#pragma unroll
+    for (int i = 0; i < LDW; i++) {
+        const int row = (wave * LDW + i) * 8 + lane / 8;
+        const int chunk = swz(row, lane % 8);
+        if (row < BM)
+            src[i] = A + (size_t)min(m0 + row, M - 1) * lda + chunk * 8;
+        else
+            src[i] = W + (size_t)min(n0 + row - BM, N - 1) * K + chunk * 8;
+    }
+    auto issue = [&](u16 *buf, int kt) {
+        u16 *dst = buf + wave * LDW * 8 * 64;
+#pragma unroll
+        for (int i = 0; i < LDW; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * BKH),
+                                             (__attribute__((address_space(3))) void *)(dst + i * 8 * 64),
+                                             16, 0, 0);
+    };
 
     f32x16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = (f32x16){};
-    auto compute = [&](int buf) {
+
+    auto compute = [&](const u16 *st) {
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ks++) {
+        for (int ks = 0; ks < BKH / 16; ks++) {
+            const int c = ks * 2 + (lane >> 5);
             uint4 fa[TM], fb[TN];
-            const int kk = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-            for (int i = 0; i < TM; i++)
-                fa[i] = *(const uint4 *)(&sa[buf][(wm * WM + i * 32 + (lane & 31)) * LR + kk]);
+            for (int i = 0; i < TM; i++) {
+                const int row = wm * WM + i * 32 + (lane & 31);
+                fa[i] = lds_read16(st + row * 64 + swz(row, c) * 8);
+            }
 #pragma unroll
-            for (int j = 0; j < TN; j++)
-                fb[j] = *(const uint4 *)(&sb[buf][(wn * WN + j * 32 + (lane & 31)) * LR + kk]);
+            for (int j = 0; j < TN; j++) {
+                const int row = BM + wn * WN + j * 32 + (lane & 31);
+                fb[j] = lds_read16(st + row * 64 + swz(row, c) * 8);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
         }
     };
-
-    const int nk = K / BK;
-    GLOAD(0, ra0, rb0);
-    SSTORE(0, ra0, rb0);
-    if (nk > 1) GLOAD(BK, ra1, rb1);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-        /* stage kt from buffer 0; registers 1 hold stage kt+1 */
-        if (kt + 2 < nk) GLOAD((kt + 2) * BK, ra0, rb0);
-        compute(0);
-        if (kt + 1 < nk) {
-            SSTORE(1, ra1, rb1);
-            __syncthreads();
-            /* stage kt+1 from buffer 1; registers 0 hold stage kt+2 */
-            if (kt + 3 < nk) GLOAD((kt + 3) * BK, ra1, rb1);
-            compute(1);
-            if (kt + 2 < nk) {
-                SSTORE(0, ra0, rb0);
-                __syncthreads();
-            }
-        }
+    /* one k-stage: wait for this wave's loads of stage kt (at most the next
+     * stage's may still be outstanding), then a bare barrier (a fenced
+     * __syncthreads would wait for every outstanding load) so all waves' loads
+     * of stage kt have landed and stage kt-1's buffer is free for stage kt+2 */
+    const int nk = K / BKH;
+    auto step = [&](int kt, const u16 *cur, u16 *ahead) {
+        if (kt + 1 < nk) WAIT_VMCNT(LDW); else WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        if (kt + 2 < nk) issue(ahead, kt + 2);
+        compute(cur);
+    };
+    issue(lds0, 0);
+    if (nk > 1) issue(lds1, 1);
+    for (int kt = 0; kt < nk; kt += NSTAGE) {
+        step(kt, lds0, lds2);
+        if (kt + 1 < nk) step(kt + 1, lds1, lds0);
+        if (kt + 2 < nk) step(kt + 2, lds2, lds1);
     }
-#undef GLOAD
-#undef SSTORE
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -454,6 +452,49 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
     }
 }
 
+/* ---- RoPE + K/V append of stored QKV rows --------------------------------------- */
+
+/* qkv [M, NQ+2*NKV] fp32 rows (plain GEMM output): q pairs rotated to q [M, NQ];
+ * k pairs rotated and v pairs appended to the cache at (slot[m], pos[m])
+ * (forward.h:55-70, 118-128).  One thread per column pair, rows on blockIdx.y. */
+template <typename KT>
+__global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, int NQ, int NKV,
+                                                 int hd, int Hkv, int max_seq,
+                                                 const int *__restrict__ pos,
+                                                 const int *__restrict__ slot,
+                                                 const float *__restrict__ rc,
+                                                 const float *__restrict__ rs,
+                                                 float *__restrict__ q, KT *__restrict__ kc,
+                                                 KT *__restrict__ vc)
+{
+    const int m = blockIdx.y;
+    const int pr = blockIdx.x * GT + threadIdx.x;          /* column pair */
+    const int W = NQ + 2 * NKV;
+    if (2 * pr >= W) return;
+    const int n = 2 * pr;
+    const float2 v = *(const float2 *)(qkv + (size_t)m * W + n);
+    const int p = pos[m];
+    if (n < NQ + NKV) {
+        const int nn = n < NQ ? n : n - NQ;
+        const int ti = p * (hd >> 1) + ((nn % hd) >> 1);
+        const float c = rc[ti], sn = rs[ti];
+        const float o0 = fmaf(v.x, c, -(v.y * sn));   /* forward.h:64 */
+        const float o1 = fmaf(v.x, sn, v.y * c);      /* forward.h:65 */
+        if (n < NQ) {
+            *(float2 *)(q + (size_t)m * NQ + n) = make_float2(o0, o1);
+        } else {
+            const size_t off = (((size_t)slot[m] * Hkv + nn / hd) * max_seq + p) * hd + nn % hd;
+            kc[off] = kv_pack<KT>(o0);
+            kc[off + 1] = kv_pack<KT>(o1);
+        }
+    } else {
+        const int nn = n - NQ - NKV;
+        const size_t off = (((size_t)slot[m] * Hkv + nn / hd) * max_seq + p) * hd + nn % hd;
+        vc[off] = kv_pack<KT>(v.x);
+        vc[off + 1] = kv_pack<KT>(v.y);
+    }
+}
+
 /* ============================== launchers =================================== */
 
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
@@ -484,67 +525,76 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     return e;
 }
 
-template <typename AT, bool NORM, int E>
-static int launch_gemm(hipStream_t s, const void *A, int lda, const float *rstd, const float *gain,
-                       const uint16_t *W, int M, int N, int K, const EpiArgs &e)
+template <int BM, int BN, int E>
+static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
+                        int K, const EpiArgs &e)
+{
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm_tile<BM, BN, E>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A, lda,
+                       (const u16 *)W, K, e, tm, tn);
+}
+
+template <int E>
+static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
+                       int K, const EpiArgs &e)
 {
     if (M <= 64) {
         dim3 grid((N + 31) / 32);
         if (M <= 32)
-            hipLaunchKernelGGL((k_gemm_skinny<1, AT, NORM, E>), grid, dim3(GT), 0, s, (const AT *)A,
-                               lda, rstd, gain, W, K, e);
+            hipLaunchKernelGGL((k_gemm_skinny<1, u16, false, E>), grid, dim3(GT), 0, s,
+                               (const u16 *)A, lda, nullptr, nullptr, W, K, e);
         else
-            hipLaunchKernelGGL((k_gemm_skinny<2, AT, NORM, E>), grid, dim3(GT), 0, s, (const AT *)A,
-                               lda, rstd, gain, W, K, e);
+            hipLaunchKernelGGL((k_gemm_skinny<2, u16, false, E>), grid, dim3(GT), 0, s,
+                               (const u16 *)A, lda, nullptr, nullptr, W, K, e);
         return hipGetLastError();
     }
-    /* prefill tiles: the largest of 128x128, 128x64, 64x64 that still gives
-     * the 256 CUs a work-group each (small M or narrow N take smaller tiles) */
-    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    const long t12864 = (long)((M + 127) / 128) * ((N + 63) / 64);
-    if (t128 >= 256 || (K % BK)) {
-        if (K % BK) return hipErrorInvalidValue;
-        dim3 grid((M + 127) / 128, (N + 127) / 128);
-        hipLaunchKernelGGL((k_gemm_tile<128, 128, AT, NORM, E>), grid, dim3(GT), 0, s,
-                           (const AT *)A, lda, rstd, gain, W, K, e);
-    } else if (t12864 >= 256) {
-        dim3 grid((M + 127) / 128, (N + 63) / 64);
-        hipLaunchKernelGGL((k_gemm_tile<128, 64, AT, NORM, E>), grid, dim3(GT), 0, s,
-                           (const AT *)A, lda, rstd, gain, W, K, e);
-    } else {
-        dim3 grid((M + 63) / 64, (N + 63) / 64);
-        hipLaunchKernelGGL((k_gemm_tile<64, 64, AT, NORM, E>), grid, dim3(GT), 0, s,
-                           (const AT *)A, lda, rstd, gain, W, K, e);
-    }
+    if (K % BKH) return hipErrorInvalidValue;
+    /* the largest tile that still gives the 256 CUs about a work-group each */
+    auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(256, 128) >= 240)
+        launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
+    else if (tiles(128, 128) >= 240)
+        launch_tile<128, 128, E>(s, A, lda, W, M, N, K, e);
+    else if (tiles(128, 64) >= 240)
+        launch_tile<128, 64, E>(s, A, lda, W, M, N, K, e);
+    else
+        launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
     return hipGetLastError();
 }
 
-extern "C" int lmk_gemm(hipStream_t s, int a_kind, const void *A, int lda, const float *rstd,
-                        const float *gain, const uint16_t *W, int M, int N, int K, int epi,
-                        const LMEpilogue *ep)
+extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
+                        int K, int epi, const LMEpilogue *ep)
 {
     if (M < 1 || N < 1 || K < 32 || K % 32 || lda < K || !A || !W || !ep) return hipErrorInvalidValue;
-    if (a_kind == LMK_A_F32_NORM && (!rstd || !gain)) return hipErrorInvalidValue;
     if (epi == EPI_GATE && (N % 32 || !ep->g)) return hipErrorInvalidValue;
     if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || (ep->hd & 1) ||
                            N != ep->NQ + 2 * ep->NKV))
         return hipErrorInvalidValue;
     if (epi == EPI_RESID && (!ep->out || ep->ldc < N)) return hipErrorInvalidValue;
-    if (epi == EPI_STORE && ep->out && ep->ldc < N) return hipErrorInvalidValue;
+    if ((epi == EPI_STORE || epi == EPI_ARGMAX) && ep->out && ep->ldc < N) return hipErrorInvalidValue;
+    if (epi == EPI_ARGMAX && !ep->part) return hipErrorInvalidValue;
     const EpiArgs e = to_epi(ep, M, N);
-#define BY_EPI(AT_, NORM_)                                                                        \
-    switch (epi) {                                                                                \
-    case EPI_STORE: return launch_gemm<AT_, NORM_, EPI_STORE>(s, A, lda, rstd, gain, W, M, N, K, e); \
-    case EPI_RESID: return launch_gemm<AT_, NORM_, EPI_RESID>(s, A, lda, rstd, gain, W, M, N, K, e); \
-    case EPI_GATE: return launch_gemm<AT_, NORM_, EPI_GATE>(s, A, lda, rstd, gain, W, M, N, K, e);   \
-    case EPI_QKV: return launch_gemm<AT_, NORM_, EPI_QKV>(s, A, lda, rstd, gain, W, M, N, K, e);     \
-    default: return hipErrorInvalidValue;                                                         \
-    }
-    switch (a_kind) {
-    case LMK_A_F16: BY_EPI(u16, false);
-    case LMK_A_F32: BY_EPI(float, false);
-    case LMK_A_F32_NORM: BY_EPI(float, true);
+    switch (epi) {
+    case EPI_STORE: return launch_gemm<EPI_STORE>(s, A, lda, W, M, N, K, e);
+    case EPI_RESID: return launch_gemm<EPI_RESID>(s, A, lda, W, M, N, K, e);
+    case EPI_GATE: return launch_gemm<EPI_GATE>(s, A, lda, W, M, N, K, e);
+    case EPI_QKV: return launch_gemm<EPI_QKV>(s, A, lda, W, M, N, K, e);
+    case EPI_ARGMAX: return launch_gemm<EPI_ARGMAX>(s, A, lda, W, M, N, K, e);
     default: return hipErrorInvalidValue;
     }
-#undef BY_EPI
+}
+
+extern "C" int lmk_qkv_post(hipStream_t s, const float *qkv, int M, int NQ, int NKV, int hd, int Hkv,
+                            int max_seq, const int *pos, const int *slot, const float *rope_cos,
+                            const float *rope_sin, float *q, void *kc, void *vc, int kv_f32)
+{
+    if (M < 1 || M > 65535 || (hd & 1) || NQ % hd || NKV % hd) return hipErrorInvalidValue;
+    dim3 grid(((NQ + 2 * NKV) / 2 + GT - 1) / GT, M);
+    if (kv_f32)
+        hipLaunchKernelGGL(k_qkv_post<float>, grid, dim3(GT), 0, s, qkv, NQ, NKV, hd, Hkv, max_seq, pos,
+                           slot, rope_cos, rope_sin, q, (float *)kc, (float *)vc);
+    else
+        hipLaunchKernelGGL(k_qkv_post<u16>, grid, dim3(GT), 0, s, qkv, NQ, NKV, hd, Hkv, max_seq, pos,
+                           slot, rope_cos, rope_sin, q, (u16 *)kc, (u16 *)vc);
+    return hipGetLastError();
 }

@@ -97,23 +97,20 @@ int lmk_attn_prefill(hipStream_t s, const float *q, const void *kc, const void *
                      int H, int Hkv, int hd, int max_seq, uint16_t *out);
 
 /* ---- MFMA GEMMs (k_gemm.hip) ----------------------------------------------
- * C[m, n] = sum_k A[m, k] W[n, k], W fp16 [N, K], fp32 accumulation; rows M <= 64
- * take the skinny (decode) kernel, larger M the LDS-tiled (prefill) kernel.
- * K must be a multiple of 32. */
+ * C[m, n] = sum_k A[m, k] W[n, k], A fp16 [M, lda], W fp16 [N, K], fp32
+ * accumulation; rows M <= 64 take the skinny (decode) kernel (K % 32 == 0),
+ * larger M the LDS-tiled (prefill) kernel (K % 64 == 0). */
 
-#define LMK_A_F16       0   /* A fp16 [M, lda]                                   */
-#define LMK_A_F32       1   /* A fp32 [M, lda], rounded to fp16                   */
-#define LMK_A_F32_NORM  2   /* A fp32, times rstd[m] * gain[k], rounded to fp16   */
-
-#define LMK_EPI_STORE   0   /* out (fp32 [M, ldc], may be NULL) + argmax partials  */
+#define LMK_EPI_STORE   0   /* out fp32 [M, ldc]                                   */
 #define LMK_EPI_RESID   1   /* out[m, n] += C (fp32 residual stream)               */
 #define LMK_EPI_GATE    2   /* g[m, i] = fp16(silu(h1) * h3), W1/W3 interleaved    */
 #define LMK_EPI_QKV     3   /* RoPE; q -> fp32 [M, NQ]; k, v -> cache(slot, pos)   */
+#define LMK_EPI_ARGMAX  4   /* out (may be NULL) + [M, ceil(N/32)] argmax partials */
 
 typedef struct {
     float *out;              /* STORE / RESID                                      */
     int ldc;
-    LMArgPart *part;         /* STORE: [M, ceil(N/32)] argmax partials, or NULL    */
+    LMArgPart *part;         /* ARGMAX: [M, ceil(N/32)] argmax partials            */
     uint16_t *g;             /* GATE: [M, F] fp16                                  */
     int F;
     float *q;                /* QKV                                                 */
@@ -123,9 +120,14 @@ typedef struct {
     const float *rope_cos, *rope_sin;
 } LMEpilogue;
 
-int lmk_gemm(hipStream_t s, int a_kind, const void *A, int lda, const float *rstd,
-             const float *gain, const uint16_t *W, int M, int N, int K, int epi,
-             const LMEpilogue *ep);
+int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
+             int K, int epi, const LMEpilogue *ep);
+
+/* qkv [M, NQ+2*NKV] fp32 rows -> RoPE'd q [M, NQ], RoPE'd k and v appended to the
+ * cache at (slot[m], pos[m]). */
+int lmk_qkv_post(hipStream_t s, const float *qkv, int M, int NQ, int NKV, int hd, int Hkv,
+                 int max_seq, const int *pos, const int *slot, const float *rope_cos,
+                 const float *rope_sin, float *q, void *kc, void *vc, int kv_f32);
 
 /* One wave per row: with emb != NULL x[m] is first set to the embedding row
  * emb[tok[m]]; then xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */

@@ -53,7 +53,7 @@ struct LMModel {
     size_t kv_layer_elems;
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
-    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
+    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd, *d_qkv;
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
@@ -259,11 +259,11 @@ static void drop_graphs(LMModel *m)
 
 static void free_rows(LMModel *m)
 {
-    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_g16,
+    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_qkv, m->d_g16,
                    m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
-    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = NULL;
+    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_qkv = NULL;
     m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
     m->d_rtok = m->d_rpos = m->d_rslot = NULL;
@@ -288,6 +288,7 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_a16, r * NQ * 2))) return st;
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_qkv, r * (NQ + 2 * (size_t)m->NKV) * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
     if ((st = dev_alloc((void **)&m->d_rtok, r * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rpos, r * 4))) return st;
@@ -580,8 +581,9 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
  * rows of one sequence attend causally to each other; seq_rows > 1: the rows
  * are whole sequences of seq_rows rows, attended by the MFMA prefill kernel,
  * else one row per slot, by the decode kernel), then with with_cls the
- * final rmsnorm + classifier of all M rows: logits to `logits` (may be NULL)
- * and argmax partials to d_amax. */
+ * final rmsnorm + classifier of all M rows: logits to `logits` (prefill: only
+ * when non-NULL; decode: may be NULL) and, for decode rows, the argmax partials
+ * to d_amax. */
 static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const int *pos,
                         const int *slot, float *logits, int with_cls)
 {
@@ -595,11 +597,19 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok,
                          m->d_rms_att + (size_t)l * D, m->d_xn16));
         memset(&ep, 0, sizeof(ep));
-        ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
-        ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
-        ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
-        KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, lw, M, NQ + 2 * NKV, D, LMK_EPI_QKV,
-                      &ep));
+        if (M > 64) {
+            /* prefill rows: plain fp32 QKV rows, then a coalesced RoPE + append pass */
+            ep.out = m->d_qkv; ep.ldc = NQ + 2 * NKV;
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQ + 2 * NKV, D, LMK_EPI_STORE, &ep));
+            KCHK(lmk_qkv_post(s, m->d_qkv, M, NQ, NKV, m->hd, m->Hkv, m->max_seq, pos, slot,
+                              m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc, m->kv_f32));
+        } else {
+            /* decode rows: RoPE and the append fused into the GEMM epilogue */
+            ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
+            ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
+            ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQ + 2 * NKV, D, LMK_EPI_QKV, &ep));
+        }
         if (seq_rows > 1)
             KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
                                   M / seq_rows, m->H, m->Hkv, m->hd, m->max_seq, m->d_a16));
@@ -608,24 +618,28 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                                  m->max_seq, NULL, m->d_a16));
         memset(&ep, 0, sizeof(ep));
         ep.out = m->d_x; ep.ldc = D;
-        KCHK(lmk_gemm(s, LMK_A_F16, m->d_a16, NQ, NULL, NULL, lw + m->off_wo, M, D, NQ,
+        KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ,
                       LMK_EPI_RESID, &ep));
         KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_ffn + (size_t)l * D, m->d_xn16));
         memset(&ep, 0, sizeof(ep));
         ep.g = m->d_g16; ep.F = F;
-        KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, lw + m->off_w13, M, 2 * F, D,
+        KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D,
                       LMK_EPI_GATE, &ep));
         memset(&ep, 0, sizeof(ep));
         ep.out = m->d_x; ep.ldc = D;
-        KCHK(lmk_gemm(s, LMK_A_F16, m->d_g16, F, NULL, NULL, lw + m->off_w2, M, D, F,
+        KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F,
                       LMK_EPI_RESID, &ep));
     }
     if (!with_cls) return LM_OK;
     KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
-    ep.out = logits; ep.ldc = m->V; ep.part = m->d_amax;
-    KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, D, NULL, NULL, m->d_wcls, M, m->V, D, LMK_EPI_STORE,
-                  &ep));
+    ep.out = logits; ep.ldc = m->V;
+    if (seq_rows > 1) {   /* prefill: logits only */
+        if (logits) KCHK(lmk_gemm(s, m->d_xn16, D, m->d_wcls, M, m->V, D, LMK_EPI_STORE, &ep));
+    } else {              /* decode: argmax partials for the greedy step (+ logits) */
+        ep.part = m->d_amax;
+        KCHK(lmk_gemm(s, m->d_xn16, D, m->d_wcls, M, m->V, D, LMK_EPI_ARGMAX, &ep));
+    }
     return LM_OK;
 }
 
@@ -848,16 +862,15 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
 }
 
 /* Final rmsnorm + classifier of M rows held in x_rows (fp32 [M, D]): logits to
- * d_logits, argmax partials to d_amax. */
+ * d_logits. */
 static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
 {
     hipStream_t s = m->stream;
     LMEpilogue ep;
     KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
-    ep.out = m->d_logits; ep.ldc = m->V; ep.part = m->d_amax;
-    KCHK(lmk_gemm(s, LMK_A_F16, m->d_xn16, m->D, NULL, NULL, m->d_wcls, M, m->V, m->D,
-                  LMK_EPI_STORE, &ep));
+    ep.out = m->d_logits; ep.ldc = m->V;
+    KCHK(lmk_gemm(s, m->d_xn16, m->D, m->d_wcls, M, m->V, m->D, LMK_EPI_STORE, &ep));
     return LM_OK;
 }
 
@@ -1076,8 +1089,15 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
     if (M < 1 || N < 1 || K < 32 || K % 32 || !A || !W || !C) return LM_ERR_INVALID;
     int rc = lm_init();
     if (rc) return rc;
-    const size_t asz = (size_t)M * K * (a_f32 ? 4 : 2), wsz = (size_t)N * K * 2;
+    const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2;
     const size_t csz = (size_t)M * N * 4, np = (size_t)M * ((N + 31) / 32);
+    uint16_t *a16 = NULL;
+    if (a_f32) {   /* the kernels take fp16 operands: round on the host (RNE) */
+        a16 = (uint16_t *)malloc(asz);
+        if (!a16) return LM_ERR_OOM;
+        lm_f32_to_f16((const float *)A, a16, (size_t)M * K);
+        A = a16;
+    }
     void *dA = NULL, *dW = NULL, *dC = NULL, *dP = NULL;
     hipError_t e = hipMalloc(&dA, asz);
     if (e == hipSuccess) e = hipMalloc(&dW, wsz);
@@ -1090,13 +1110,14 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
         LMEpilogue ep;
         memset(&ep, 0, sizeof(ep));
         ep.out = (float *)dC; ep.ldc = N; ep.part = (LMArgPart *)dP;
-        e = (hipError_t)lmk_gemm(0, a_f32 ? LMK_A_F32 : LMK_A_F16, dA, K, NULL, NULL,
-                                 (const uint16_t *)dW, M, N, K, LMK_EPI_STORE, &ep);
+        e = (hipError_t)lmk_gemm(0, (const uint16_t *)dA, K, (const uint16_t *)dW, M, N, K,
+                                 LMK_EPI_ARGMAX, &ep);
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemcpy(C, dC, csz, hipMemcpyDeviceToHost);
     if (e == hipSuccess && part) e = hipMemcpy(part, dP, np * sizeof(LMArgPart), hipMemcpyDeviceToHost);
     hipFree(dA); hipFree(dW); hipFree(dC); hipFree(dP);
+    free(a16);
     HIPCHK(e);
     return LM_OK;
 }
