@@ -25,9 +25,13 @@
  *                  streamed by direct global->LDS loads into a 3-deep ring of
  *                  64-wide stages; XCD-aware tile order
  *   k_gemm_skinny  M <= 64 rows (decode batches): a work-group owns 32 columns
- *                  and all rows; its four waves split K, stream their weight
+ *                  and all rows of one K-chunk (all of K, or 1/ns of it for a
+ *                  K-split GEMM, whose fp32 partials the next row kernel sums);
+ *                  its four waves split the chunk, stream their weight
  *                  fragments straight from HBM into registers (each weight byte
  *                  read once) and add their partial tiles through LDS.
+ * A classifier over decode rows (N >= 16384) takes the tiled kernel with a
+ * 64-row tile instead.
  */
 #include <type_traits>
 
@@ -48,17 +52,6 @@ __device__ __forceinline__ void static_for(F &&f)
 }
 
 #define GT 256                    /* threads per work-group */
-
-/* ---- operand staging ------------------------------------------------------- */
-
-/* 8 consecutive A elements of row m from k0 (fp16 bits). */
-template <typename AT, bool NORM>
-__device__ __forceinline__ uint4 load_a8(const AT *__restrict__ A, int lda, int m, int k0,
-                                         const float *__restrict__, const float *__restrict__)
-{
-    static_assert(sizeof(AT) == 2 && !NORM, "fp16 operands only");
-    return *(const uint4 *)(A + (size_t)m * lda + k0);
-}
 
 __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c)
 {
@@ -81,6 +74,7 @@ struct EpiArgs {
     int kv_f32, NQ, NKV, hd, Hkv, max_seq;
     const int *slot, *pos;
     const float *rope_cos, *rope_sin;
+    size_t sstride;         /* STORE of a K-split GEMM: out of split s is out + s*sstride */
 };
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
@@ -199,19 +193,51 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
  * slot l % 8 of row l / 8: the swizzle is applied to the source address. */
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
+/* 16-byte LDS reads issued as inline assembly, together with the wait for
+ * them in the same statement.  The compiler cannot tell which LDS buffer its
+ * own ds_reads touch relative to the direct global->LDS loads in flight, and
+ * would wait for all of those loads before every read; these reads are
+ * invisible to it, so the kernel orders them explicitly (vmcnt + barrier before
+ * a stage's reads).  The lgkmcnt(0) wait sits inside the statement: were it a
+ * statement of its own, the compiler could schedule a use of a read's result
+ * (an MFMA, a register copy) between the read and the wait. */
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-/* 16-byte LDS read issued as inline assembly.  The compiler cannot tell which
- * LDS buffer its own ds_reads touch relative to the direct global->LDS loads in
- * flight, and would wait for all of those loads before every read; these reads
- * are invisible to it, so the kernel waits explicitly: vmcnt + barrier before a
- * stage's reads, lgkmcnt(0) before the MFMAs use them. */
-__device__ __forceinline__ uint4 lds_read16(const u16 *p)
+__device__ __forceinline__ unsigned lds_off(const u16 *p)
 {
-    const unsigned off = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) u16 *)p;
-    u32x4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(off));
-    return __builtin_bit_cast(uint4, v);
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) u16 *)p;
+}
+__device__ __forceinline__ void lds_read_wait(u32x4 (&v)[2], const unsigned (&a)[2])
+{
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1])
+                 : "v"(a[0]), "v"(a[1])
+                 : "memory");
+}
+__device__ __forceinline__ void lds_read_wait(u32x4 (&v)[3], const unsigned (&a)[3])
+{
+    asm volatile("ds_read_b128 %0, %3\n\tds_read_b128 %1, %4\n\tds_read_b128 %2, %5\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2])
+                 : "memory");
+}
+__device__ __forceinline__ void lds_read_wait(u32x4 (&v)[4], const unsigned (&a)[4])
+{
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\t"
+                 "ds_read_b128 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+                 : "memory");
+}
+__device__ __forceinline__ void lds_read_wait(u32x4 (&v)[6], const unsigned (&a)[6])
+{
+    asm volatile("ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\tds_read_b128 %2, %8\n\t"
+                 "ds_read_b128 %3, %9\n\tds_read_b128 %4, %10\n\tds_read_b128 %5, %11\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5])
+                 : "memory");
 }
 
 template <int BM, int BN, int E>
@@ -269,26 +295,39 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = (f32x16){};
 
+    /* fragments of k-step ks: A rows (TM), then W rows (TN); the reads of step
+     * ks+1 are issued after the MFMAs of step ks, into the other register set */
+    constexpr int NF = TM + TN;
+    auto frag_addr = [&](const u16 *st, int ks, unsigned (&ad)[NF]) {
+        const int c = ks * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int row = wm * WM + i * 32 + (lane & 31);
+            ad[i] = lds_off(st + row * 64 + swz(row, c) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int row = BM + wn * WN + j * 32 + (lane & 31);
+            ad[TM + j] = lds_off(st + row * 64 + swz(row, c) * 8);
+        }
+    };
     auto compute = [&](const u16 *st) {
+        u32x4 f[2][NF];
+        unsigned ad[NF];
+        frag_addr(st, 0, ad);
+        lds_read_wait(f[0], ad);
 #pragma unroll
         for (int ks = 0; ks < BKH / 16; ks++) {
-            const int c = ks * 2 + (lane >> 5);
-            uint4 fa[TM], fb[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int row = wm * WM + i * 32 + (lane & 31);
-                fa[i] = lds_read16(st + row * 64 + swz(row, c) * 8);
-            }
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int row = BM + wn * WN + j * 32 + (lane & 31);
-                fb[j] = lds_read16(st + row * 64 + swz(row, c) * 8);
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = mfma32(__builtin_bit_cast(uint4, f[ks & 1][i]),
+                                       __builtin_bit_cast(uint4, f[ks & 1][TM + j]), acc[i][j]);
+            if (ks + 1 < BKH / 16) {
+                frag_addr(st, ks + 1, ad);
+                lds_read_wait(f[(ks + 1) & 1], ad);
+            }
         }
     };
     /* one k-stage: wait for this wave's loads of stage kt (at most the next
@@ -318,13 +357,19 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
 
 /* ---- skinny GEMM (decode batches, M <= 64) ---------------------------------- */
 
-#define SK_STEPS 8   /* k-steps of 16 fetched per pipeline stage */
-
-template <int MT, typename AT, bool NORM, int E>
-__global__ void __launch_bounds__(GT) k_gemm_skinny(const AT *__restrict__ A, int lda,
-                                                    const float *__restrict__ rstd,
-                                                    const float *__restrict__ gain,
-                                                    const u16 *__restrict__ W, int K, EpiArgs e)
+/* Work-group (32-column block x, K-split y): columns 32x .. 32x+31, k-steps of
+ * 16 of its chunk cut between the four waves.  A wave fetches SK k-steps at a
+ * time (one weight fragment and MT activation fragments per step, straight into
+ * registers) one stage ahead of the MFMAs.  Every fetch is unconditional: steps
+ * past the wave's range load the last valid step again and are zeroed, so the
+ * loads form straight-line code whose outstanding count the compiler tracks
+ * exactly (a load behind a branch would make it wait for every load in flight,
+ * the next stage's included).  SK matches the wave's step count for short
+ * chunks. */
+template <int MT, int SK, int E>
+__global__ void __launch_bounds__(GT) k_gemm_skinny(const u16 *__restrict__ A, int lda,
+                                                    const u16 *__restrict__ W, int K, int kc,
+                                                    EpiArgs e)
 {
     __shared__ float red[3][MT * 16][64];
     /* MFMA instructions execute whatever the EXEC mask says, so every branch
@@ -334,49 +379,50 @@ __global__ void __launch_bounds__(GT) k_gemm_skinny(const AT *__restrict__ A, in
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n0 = blockIdx.x * 32;
     const int M = e.M, N = e.N;
-    const int nsteps = K / 16;                    /* k-steps of the whole row      */
+    const int nsteps = kc / 16;                   /* k-steps of this work-group    */
+    const int sb = blockIdx.y * nsteps;           /* its first k-step              */
     const int per = (nsteps + 3) / 4;             /* k-steps of this wave's slice  */
-    const int s0 = wave * per, s1 = min(nsteps, s0 + per);
+    const int s0 = sb + wave * per, s1 = min(sb + nsteps, s0 + per);
+    const int nstage = s1 > s0 ? (s1 - s0 + SK - 1) / SK : 0;
     const int wrow = min(n0 + (lane & 31), N - 1);
     const int koff = (lane >> 5) * 8;
     const u16 *wp = W + (size_t)wrow * K + koff;
-    int arow[MT];
+    const u16 *ap[MT];
 #pragma unroll
-    for (int i = 0; i < MT; i++) arow[i] = min(i * 32 + (lane & 31), M - 1);
+    for (int i = 0; i < MT; i++) ap[i] = A + (size_t)min(i * 32 + (lane & 31), M - 1) * lda + koff;
 
     f32x16 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; i++) acc[i] = (f32x16){};
 
-    uint4 fb[2][SK_STEPS], fa[2][SK_STEPS][MT];
+    uint4 fb[2][SK], fa[2][SK][MT];
     auto fetch = [&](int st, int b) {
 #pragma unroll
-        for (int j = 0; j < SK_STEPS; j++) {
-            const int s = st + j;
-            if (s < s1) {
-                fb[b][j] = *(const uint4 *)(wp + s * 16);
+        for (int j = 0; j < SK; j++) {
+            const int sv = s0 + st * SK + j;
+            const int sc = min(sv, s1 - 1);
+            const uint4 w = *(const uint4 *)(wp + sc * 16);
+            fb[b][j] = sv < s1 ? w : make_uint4(0, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < MT; i++)
-                    fa[b][j][i] = load_a8<AT, NORM>(A, lda, arow[i], s * 16 + koff, rstd, gain);
-            }
+            for (int i = 0; i < MT; i++) fa[b][j][i] = *(const uint4 *)(ap[i] + sc * 16);
         }
     };
-    auto consume = [&](int st, int b) {
+    auto consume = [&](int b) {
 #pragma unroll
-        for (int j = 0; j < SK_STEPS; j++)
-            if (st + j < s1)
+        for (int j = 0; j < SK; j++)
 #pragma unroll
-                for (int i = 0; i < MT; i++) acc[i] = mfma32(fa[b][j][i], fb[b][j], acc[i]);
+            for (int i = 0; i < MT; i++) acc[i] = mfma32(fa[b][j][i], fb[b][j], acc[i]);
     };
-    if (s0 < s1) {
-        fetch(s0, 0);
-        for (int st = s0; st < s1; st += 2 * SK_STEPS) {
-            if (st + SK_STEPS < s1) fetch(st + SK_STEPS, 1);
-            consume(st, 0);
-            if (st + SK_STEPS < s1) {
-                if (st + 2 * SK_STEPS < s1) fetch(st + 2 * SK_STEPS, 0);
-                consume(st + SK_STEPS, 1);
-            }
+    if (nstage == 1) {
+        fetch(0, 0);
+        consume(0);
+    } else if (nstage > 1) {
+        fetch(0, 0);
+        for (int st = 0; st < nstage; st += 2) {
+            fetch(st + 1, 1);
+            consume(0);
+            fetch(st + 2, 0);
+            consume(1);
         }
     }
     /* sum the four waves' partial tiles */
@@ -388,6 +434,7 @@ __global__ void __launch_bounds__(GT) k_gemm_skinny(const AT *__restrict__ A, in
     }
     __syncthreads();
     if (wave == 0) {
+        if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
 #pragma unroll
         for (int i = 0; i < MT; i++) {
 #pragma unroll
@@ -399,56 +446,130 @@ __global__ void __launch_bounds__(GT) k_gemm_skinny(const AT *__restrict__ A, in
     }
 }
 
+/* Launch the skinny kernel over grid (N/32, ns) with k-chunk kc = K/ns. */
+template <int E>
+static void launch_skinny(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
+                          int N, int K, int ns, const EpiArgs &e)
+{
+    const int kc = K / ns;
+    const int per = (kc / 16 + 3) / 4;            /* k-steps per wave */
+    dim3 grid((N + 31) / 32, ns);
+#define SKL(MT_, SK_)                                                                            \
+    hipLaunchKernelGGL((k_gemm_skinny<MT_, SK_, E>), grid, dim3(GT), 0, s, (const u16 *)A, lda,   \
+                       (const u16 *)W, K, kc, e)
+#define SKL_MT(SK_)            \
+    if (M <= 32) SKL(1, SK_);  \
+    else SKL(2, SK_);
+    if (per <= 1) { SKL_MT(1) }
+    else if (per <= 2) { SKL_MT(2) }
+    else if (per <= 4) { SKL_MT(4) }
+    else { SKL_MT(8) }
+#undef SKL_MT
+#undef SKL
+}
+
 /* ---- per-row RMSNorm ------------------------------------------------------------ */
 
-/* One wave per row m (forward.h:46-53): with emb != NULL the row is first set
- * to the fp16 embedding row emb[tok[m]] (forward.h:108-110); then
+/* One work-group per row m (forward.h:46-53): with emb != NULL the row is first
+ * set to the fp16 embedding row emb[tok[m]] (forward.h:108-110); with ns > 0 the
+ * ns partials of a K-split projection are added to it first, in split order (the
+ * residual add, forward.h:134-136, 157-159); then
  * xn[m, k] = fp16(x[m, k] * (1/sqrt(mean(x[m]^2) + 1e-5)) * gain[k]), the GEMM
- * operand of the projection that follows.  The row stays in registers
- * (D/64 values per lane). */
+ * operand of the projection that follows.  Thread t owns the D/256 values
+ * 4t .. 4t+3 (+1024 ...), so every load of the row is issued at once. */
 template <int D>
 __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
                                                 const u16 *__restrict__ emb,
                                                 const int *__restrict__ tok,
+                                                const float *__restrict__ sp, int ns,
+                                                size_t sstride,
                                                 const float *__restrict__ gain,
                                                 u16 *__restrict__ xn)
 {
-    constexpr int PER = D / 64;              /* values per lane, in chunks of 4 */
-    const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * (GT / 64) + (threadIdx.x >> 6);
-    if (m >= M) return;
+    constexpr int PER = D / GT;              /* values per thread */
+    constexpr int C4 = (PER + 3) / 4;        /* float4 groups per thread */
+    static_assert(D % GT == 0, "row width");
+    __shared__ float red[GT / 64];
+    const int t = threadIdx.x;
+    const int m = blockIdx.x;
     float *xr = x + (size_t)m * D;
-    float v[PER];
+    /* value i of this thread is column col(i) = (i/4)*1024 + 4t + i%4 (D >= 1024),
+     * or t*PER + i (D < 1024) */
+    auto col = [&](int c) { return PER >= 4 ? c * (4 * GT) + 4 * t : t * PER; };
+    float v[C4 * 4];
     if (emb) {
         const u16 *er = emb + (size_t)tok[m] * D;
 #pragma unroll
-        for (int c = 0; c < PER / 4; c++) {
-            const uint2 h = *(const uint2 *)(er + c * 256 + lane * 4);
-            const f16x2 a = __builtin_bit_cast(f16x2, h.x), b = __builtin_bit_cast(f16x2, h.y);
-            v[4 * c] = (float)a.x; v[4 * c + 1] = (float)a.y;
-            v[4 * c + 2] = (float)b.x; v[4 * c + 3] = (float)b.y;
-            *(float4 *)(xr + c * 256 + lane * 4) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2],
-                                                               v[4 * c + 3]);
+        for (int c = 0; c < C4; c++) {
+            if (PER >= 4) {
+                const uint2 h = *(const uint2 *)(er + col(c));
+                const f16x2 a = __builtin_bit_cast(f16x2, h.x), b = __builtin_bit_cast(f16x2, h.y);
+                v[4 * c] = (float)a.x; v[4 * c + 1] = (float)a.y;
+                v[4 * c + 2] = (float)b.x; v[4 * c + 3] = (float)b.y;
+            } else {
+#pragma unroll
+                for (int i = 0; i < PER; i++) v[i] = h2f(er[col(0) + i]);
+            }
         }
     } else {
 #pragma unroll
-        for (int c = 0; c < PER / 4; c++) {
-            const float4 t = *(const float4 *)(xr + c * 256 + lane * 4);
-            v[4 * c] = t.x; v[4 * c + 1] = t.y; v[4 * c + 2] = t.z; v[4 * c + 3] = t.w;
+        for (int c = 0; c < C4; c++) {
+            if (PER >= 4) {
+                const float4 q4 = *(const float4 *)(xr + col(c));
+                v[4 * c] = q4.x; v[4 * c + 1] = q4.y; v[4 * c + 2] = q4.z; v[4 * c + 3] = q4.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < PER; i++) v[i] = xr[col(0) + i];
+            }
+        }
+        if (ns > 0) {
+            for (int q = 0; q < ns; q++) {
+                const float *pr = sp + q * sstride + (size_t)m * D;
+#pragma unroll
+                for (int c = 0; c < C4; c++) {
+                    if (PER >= 4) {
+                        const float4 q4 = *(const float4 *)(pr + col(c));
+                        v[4 * c] += q4.x; v[4 * c + 1] += q4.y; v[4 * c + 2] += q4.z; v[4 * c + 3] += q4.w;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < PER; i++) v[i] += pr[col(0) + i];
+                    }
+                }
+            }
+        }
+    }
+    if (emb || ns > 0) {
+#pragma unroll
+        for (int c = 0; c < C4; c++) {
+            if (PER >= 4)
+                *(float4 *)(xr + col(c)) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+            else
+#pragma unroll
+                for (int i = 0; i < PER; i++) xr[col(0) + i] = v[i];
         }
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; i++) ss = fmaf(v[i], v[i], ss);
     ss = wave_sum(ss);
-    const float rs = 1.0f / sqrtf(ss / D + 1e-5f);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < GT / 64; w++) tot += red[w];
+    const float rs = 1.0f / sqrtf(tot / D + 1e-5f);
     u16 *xo = xn + (size_t)m * D;
 #pragma unroll
-    for (int c = 0; c < PER / 4; c++) {
-        const float4 g = *(const float4 *)(gain + c * 256 + lane * 4);
-        const unsigned lo = (unsigned)f2h(v[4 * c] * rs * g.x) | ((unsigned)f2h(v[4 * c + 1] * rs * g.y) << 16);
-        const unsigned hi = (unsigned)f2h(v[4 * c + 2] * rs * g.z) | ((unsigned)f2h(v[4 * c + 3] * rs * g.w) << 16);
-        *(uint2 *)(xo + c * 256 + lane * 4) = make_uint2(lo, hi);
+    for (int c = 0; c < C4; c++) {
+        if (PER >= 4) {
+            const float4 g = *(const float4 *)(gain + col(c));
+            const unsigned lo = (unsigned)f2h(v[4 * c] * rs * g.x) | ((unsigned)f2h(v[4 * c + 1] * rs * g.y) << 16);
+            const unsigned hi = (unsigned)f2h(v[4 * c + 2] * rs * g.z) | ((unsigned)f2h(v[4 * c + 3] * rs * g.w) << 16);
+            *(uint2 *)(xo + col(c)) = make_uint2(lo, hi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; i++) xo[col(0) + i] = f2h(v[i] * rs * gain[col(0) + i]);
+        }
     }
 }
 
@@ -456,9 +577,12 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
 
 /* qkv [M, NQ+2*NKV] fp32 rows (plain GEMM output): q pairs rotated to q [M, NQ];
  * k pairs rotated and v pairs appended to the cache at (slot[m], pos[m])
- * (forward.h:55-70, 118-128).  One thread per column pair, rows on blockIdx.y. */
+ * (forward.h:55-70, 118-128); with ns > 1, qkv holds the ns partials of a K-split
+ * GEMM, ns x [M, NQ+2*NKV] sstride floats apart, summed first.  One thread per
+ * column pair, rows on blockIdx.y. */
 template <typename KT>
-__global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, int NQ, int NKV,
+__global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, int ns,
+                                                 size_t sstride, int NQ, int NKV,
                                                  int hd, int Hkv, int max_seq,
                                                  const int *__restrict__ pos,
                                                  const int *__restrict__ slot,
@@ -472,7 +596,12 @@ __global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, 
     const int W = NQ + 2 * NKV;
     if (2 * pr >= W) return;
     const int n = 2 * pr;
-    const float2 v = *(const float2 *)(qkv + (size_t)m * W + n);
+    float2 v = *(const float2 *)(qkv + (size_t)m * W + n);
+    for (int q = 1; q < ns; q++) {          /* partials of a K-split GEMM, in split order */
+        const float2 t = *(const float2 *)(qkv + q * sstride + (size_t)m * W + n);
+        v.x += t.x;
+        v.y += t.y;
+    }
     const int p = pos[m];
     if (n < NQ + NKV) {
         const int nn = n < NQ ? n : n - NQ;
@@ -498,16 +627,17 @@ __global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, 
 /* ============================== launchers =================================== */
 
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
-                           const float *gain, uint16_t *xn)
+                           const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn)
 {
-    if (M < 1 || (emb && !tok) || !gain || !xn) return hipErrorInvalidValue;
-    dim3 grid((M + 3) / 4);
+    if (M < 1 || (emb && !tok) || !gain || !xn || ns < 0 || (ns && (!sp || emb)))
+        return hipErrorInvalidValue;
+    dim3 grid(M);
     switch (D) {
-    case 256: hipLaunchKernelGGL(k_rownorm<256>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
-    case 512: hipLaunchKernelGGL(k_rownorm<512>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
-    case 768: hipLaunchKernelGGL(k_rownorm<768>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
-    case 1024: hipLaunchKernelGGL(k_rownorm<1024>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
-    case 2048: hipLaunchKernelGGL(k_rownorm<2048>, grid, dim3(GT), 0, s, x, M, emb, tok, gain, xn); break;
+    case 256: hipLaunchKernelGGL(k_rownorm<256>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 512: hipLaunchKernelGGL(k_rownorm<512>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 768: hipLaunchKernelGGL(k_rownorm<768>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 1024: hipLaunchKernelGGL(k_rownorm<1024>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 2048: hipLaunchKernelGGL(k_rownorm<2048>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -522,6 +652,7 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     e.q = p->q; e.kc = p->kc; e.vc = p->vc; e.kv_f32 = p->kv_f32;
     e.NQ = p->NQ; e.NKV = p->NKV; e.hd = p->hd; e.Hkv = p->Hkv; e.max_seq = p->max_seq;
     e.slot = p->slot; e.pos = p->pos; e.rope_cos = p->rope_cos; e.rope_sin = p->rope_sin;
+    e.sstride = 0;
     return e;
 }
 
@@ -538,14 +669,14 @@ template <int E>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
 {
+    if (M <= 64 && N >= 16384 && K % BKH == 0) {
+        /* a classifier over decode rows: a 64-row MFMA tile stages the rows in
+         * LDS once per 128 columns instead of once per 32 */
+        launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
+        return hipGetLastError();
+    }
     if (M <= 64) {
-        dim3 grid((N + 31) / 32);
-        if (M <= 32)
-            hipLaunchKernelGGL((k_gemm_skinny<1, u16, false, E>), grid, dim3(GT), 0, s,
-                               (const u16 *)A, lda, nullptr, nullptr, W, K, e);
-        else
-            hipLaunchKernelGGL((k_gemm_skinny<2, u16, false, E>), grid, dim3(GT), 0, s,
-                               (const u16 *)A, lda, nullptr, nullptr, W, K, e);
+        launch_skinny<E>(s, A, lda, W, M, N, K, 1, e);
         return hipGetLastError();
     }
     if (K % BKH) return hipErrorInvalidValue;
@@ -584,17 +715,47 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
     }
 }
 
-extern "C" int lmk_qkv_post(hipStream_t s, const float *qkv, int M, int NQ, int NKV, int hd, int Hkv,
-                            int max_seq, const int *pos, const int *slot, const float *rope_cos,
-                            const float *rope_sin, float *q, void *kc, void *vc, int kv_f32)
+extern "C" int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstride, int M, int NQ,
+                            int NKV, int hd, int Hkv, int max_seq, const int *pos, const int *slot,
+                            const float *rope_cos, const float *rope_sin, float *q, void *kc,
+                            void *vc, int kv_f32)
 {
-    if (M < 1 || M > 65535 || (hd & 1) || NQ % hd || NKV % hd) return hipErrorInvalidValue;
+    if (M < 1 || M > 65535 || ns < 1 || (hd & 1) || NQ % hd || NKV % hd) return hipErrorInvalidValue;
     dim3 grid(((NQ + 2 * NKV) / 2 + GT - 1) / GT, M);
     if (kv_f32)
-        hipLaunchKernelGGL(k_qkv_post<float>, grid, dim3(GT), 0, s, qkv, NQ, NKV, hd, Hkv, max_seq, pos,
+        hipLaunchKernelGGL(k_qkv_post<float>, grid, dim3(GT), 0, s, qkv, ns, sstride, NQ, NKV, hd, Hkv, max_seq, pos,
                            slot, rope_cos, rope_sin, q, (float *)kc, (float *)vc);
     else
-        hipLaunchKernelGGL(k_qkv_post<u16>, grid, dim3(GT), 0, s, qkv, NQ, NKV, hd, Hkv, max_seq, pos,
+        hipLaunchKernelGGL(k_qkv_post<u16>, grid, dim3(GT), 0, s, qkv, ns, sstride, NQ, NKV, hd, Hkv, max_seq, pos,
                            slot, rope_cos, rope_sin, q, (u16 *)kc, (u16 *)vc);
+    return hipGetLastError();
+}
+
+/* K-split count for a decode-row GEMM (M <= 64): with one work-group per 32
+ * columns a narrow N leaves most CUs idle, so K is cut into the fewest splits
+ * (k-chunks a multiple of 64) that give about one work-group per CU. */
+extern "C" int lmk_pick_split(int M, int N, int K)
+{
+    const int nb = (N + 31) / 32;
+    if (M > 64 || nb >= 192) return 1;
+    int best = 1;
+    for (int ns = 2; ns <= LMK_MAX_SPLIT; ns++) {
+        if (K % (64 * ns)) continue;
+        best = ns;
+        if (nb * ns >= 256) break;
+    }
+    return best;
+}
+
+extern "C" int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
+                              int N, int K, int ns, float *part)
+{
+    if (M < 1 || M > 64 || N < 1 || ns < 1 || ns > LMK_MAX_SPLIT || K % (16 * ns) || lda < K ||
+        !A || !W || !part)
+        return hipErrorInvalidValue;
+    EpiArgs e = {};
+    e.M = M; e.N = N; e.out = part; e.ldc = N; e.nparts = (N + 31) / 32;
+    e.sstride = (size_t)M * N;
+    launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
     return hipGetLastError();
 }

@@ -123,16 +123,26 @@ typedef struct {
 int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
              int K, int epi, const LMEpilogue *ep);
 
-/* qkv [M, NQ+2*NKV] fp32 rows -> RoPE'd q [M, NQ], RoPE'd k and v appended to the
- * cache at (slot[m], pos[m]). */
-int lmk_qkv_post(hipStream_t s, const float *qkv, int M, int NQ, int NKV, int hd, int Hkv,
-                 int max_seq, const int *pos, const int *slot, const float *rope_cos,
-                 const float *rope_sin, float *q, void *kc, void *vc, int kv_f32);
+/* qkv [M, NQ+2*NKV] fp32 rows (the sum of ns partials sstride floats apart) ->
+ * RoPE'd q [M, NQ], RoPE'd k and v appended to the cache at (slot[m], pos[m]). */
+int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstride, int M, int NQ, int NKV,
+                 int hd, int Hkv, int max_seq, const int *pos, const int *slot,
+                 const float *rope_cos, const float *rope_sin, float *q, void *kc, void *vc,
+                 int kv_f32);
+
+/* Decode-row GEMM (M <= 64) with K cut into ns splits: part[s][M][N] (fp32) is
+ * split s's partial of A W^T; lmk_pick_split chooses ns for a shape. */
+#define LMK_MAX_SPLIT 16
+int lmk_pick_split(int M, int N, int K);
+int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
+                   int K, int ns, float *part);
 
 /* One wave per row: with emb != NULL x[m] is first set to the embedding row
- * emb[tok[m]]; then xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */
+ * emb[tok[m]]; with ns > 0 the ns partials sp[s][m] (sstride floats apart) of a
+ * K-split projection are added to x[m] first (the residual add); then
+ * xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */
 int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
-                const float *gain, uint16_t *xn);
+                const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn);
 
 /* ---- persistent batch-1 decode (k_persist.hip) --------------------------- */
 

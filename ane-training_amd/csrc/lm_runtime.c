@@ -54,6 +54,7 @@ struct LMModel {
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
     float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd, *d_qkv;
+    float *d_part;              /* partials of K-split decode-row GEMMs       */
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
@@ -259,11 +260,11 @@ static void drop_graphs(LMModel *m)
 
 static void free_rows(LMModel *m)
 {
-    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_qkv, m->d_g16,
+    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_qkv, m->d_part, m->d_g16,
                    m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
-    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_qkv = NULL;
+    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_qkv = m->d_part = NULL;
     m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
     m->d_rtok = m->d_rpos = m->d_rslot = NULL;
@@ -289,6 +290,11 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_qkv, r * (NQ + 2 * (size_t)m->NKV) * 4))) return st;
+    {
+        const size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
+        const size_t rd = r < 64 ? r : 64;
+        if ((st = dev_alloc((void **)&m->d_part, LMK_MAX_SPLIT * rd * w * 4))) return st;
+    }
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
     if ((st = dev_alloc((void **)&m->d_rtok, r * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rpos, r * 4))) return st;
@@ -588,27 +594,43 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                         const int *slot, float *logits, int with_cls)
 {
     hipStream_t s = m->stream;
-    const int D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV;
+    const int D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, NQKV = NQ + 2 * NKV;
+    const size_t sx = (size_t)M * D;   /* split stride of a [M, D] partial */
+    /* decode rows (M <= 64) run narrow projections K-split: the partials land in
+     * d_part and the kernel that next reads x adds them (the residual add) */
+    const int dec = M <= 64;
+    const int ns_qkv = dec ? lmk_pick_split(M, NQKV, D) : 1;
+    const int ns_wo = dec ? lmk_pick_split(M, D, NQ) : 1;
+    const int ns_w2 = dec ? lmk_pick_split(M, D, F) : 1;
+    const float *pend = NULL;          /* W2 partials not yet added to x */
+    int pend_ns = 0;
     LMEpilogue ep;
     for (int l = 0; l < m->L; l++) {
         const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
         const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
         void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
-        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok,
+        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok, pend, pend_ns, sx,
                          m->d_rms_att + (size_t)l * D, m->d_xn16));
+        pend = NULL;
+        pend_ns = 0;
         memset(&ep, 0, sizeof(ep));
-        if (M > 64) {
+        if (!dec) {
             /* prefill rows: plain fp32 QKV rows, then a coalesced RoPE + append pass */
-            ep.out = m->d_qkv; ep.ldc = NQ + 2 * NKV;
-            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQ + 2 * NKV, D, LMK_EPI_STORE, &ep));
-            KCHK(lmk_qkv_post(s, m->d_qkv, M, NQ, NKV, m->hd, m->Hkv, m->max_seq, pos, slot,
+            ep.out = m->d_qkv; ep.ldc = NQKV;
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_STORE, &ep));
+            KCHK(lmk_qkv_post(s, m->d_qkv, 1, 0, M, NQ, NKV, m->hd, m->Hkv, m->max_seq, pos, slot,
                               m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc, m->kv_f32));
+        } else if (ns_qkv > 1) {
+            KCHK(lmk_gemm_split(s, m->d_xn16, D, lw, M, NQKV, D, ns_qkv, m->d_part));
+            KCHK(lmk_qkv_post(s, m->d_part, ns_qkv, (size_t)M * NQKV, M, NQ, NKV, m->hd, m->Hkv,
+                              m->max_seq, pos, slot, m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc,
+                              m->kv_f32));
         } else {
-            /* decode rows: RoPE and the append fused into the GEMM epilogue */
+            /* wide enough unsplit: RoPE and the append fused into the GEMM epilogue */
             ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
             ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
             ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
-            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQ + 2 * NKV, D, LMK_EPI_QKV, &ep));
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
         }
         if (seq_rows > 1)
             KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
@@ -616,22 +638,38 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         else
             KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
                                  m->max_seq, NULL, m->d_a16));
-        memset(&ep, 0, sizeof(ep));
-        ep.out = m->d_x; ep.ldc = D;
-        KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ,
-                      LMK_EPI_RESID, &ep));
-        KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_ffn + (size_t)l * D, m->d_xn16));
+        if (ns_wo > 1) {
+            KCHK(lmk_gemm_split(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, ns_wo, m->d_part));
+            KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_part, ns_wo, sx,
+                             m->d_rms_ffn + (size_t)l * D, m->d_xn16));
+        } else {
+            memset(&ep, 0, sizeof(ep));
+            ep.out = m->d_x; ep.ldc = D;
+            KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, LMK_EPI_RESID, &ep));
+            KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, NULL, 0, 0,
+                             m->d_rms_ffn + (size_t)l * D, m->d_xn16));
+        }
         memset(&ep, 0, sizeof(ep));
         ep.g = m->d_g16; ep.F = F;
-        KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D,
-                      LMK_EPI_GATE, &ep));
-        memset(&ep, 0, sizeof(ep));
-        ep.out = m->d_x; ep.ldc = D;
-        KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F,
-                      LMK_EPI_RESID, &ep));
+        KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
+        if (ns_w2 > 1) {
+            KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));
+            pend = m->d_part;
+            pend_ns = ns_w2;
+        } else {
+            memset(&ep, 0, sizeof(ep));
+            ep.out = m->d_x; ep.ldc = D;
+            KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F, LMK_EPI_RESID, &ep));
+        }
     }
-    if (!with_cls) return LM_OK;
-    KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
+    if (!with_cls) {
+        /* x must hold the final residual for the caller: add pending partials */
+        if (pend_ns)
+            KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, pend, pend_ns, sx, m->d_rms_final,
+                             m->d_xn16));
+        return LM_OK;
+    }
+    KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, pend, pend_ns, sx, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
     ep.out = logits; ep.ldc = m->V;
     if (seq_rows > 1) {   /* prefill: logits only */
@@ -867,7 +905,7 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
 {
     hipStream_t s = m->stream;
     LMEpilogue ep;
-    KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, m->d_rms_final, m->d_xn16));
+    KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, NULL, 0, 0, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
     ep.out = m->d_logits; ep.ldc = m->V;
     KCHK(lmk_gemm(s, m->d_xn16, m->D, m->d_wcls, M, m->V, m->D, LMK_EPI_STORE, &ep));
@@ -1120,4 +1158,37 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
     free(a16);
     HIPCHK(e);
     return LM_OK;
+}
+
+int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, const uint16_t *W,
+                           float *parts)
+{
+    if (M < 1 || M > 64 || N < 1 || K < 32 || K % 32 || !A || !W || !parts) return LM_ERR_INVALID;
+    if (nsplit == 0) nsplit = lmk_pick_split(M, N, K);
+    if (nsplit < 1 || nsplit > LMK_MAX_SPLIT || K % (16 * nsplit)) return LM_ERR_INVALID;
+    int rc = lm_init();
+    if (rc) return rc;
+    const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2;
+    const size_t psz = (size_t)nsplit * M * N * 4;
+    void *dA = NULL, *dW = NULL, *dP = NULL;
+    hipError_t e = hipMalloc(&dA, asz);
+    if (e == hipSuccess) e = hipMalloc(&dW, wsz);
+    if (e == hipSuccess) e = hipMalloc(&dP, psz);
+    if (e == hipSuccess) e = hipMemcpy(dA, A, asz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dW, W, wsz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(dP, 0xFF, psz);
+    if (e == hipSuccess)
+        e = (hipError_t)lmk_gemm_split(0, (const uint16_t *)dA, K, (const uint16_t *)dW, M, N, K,
+                                       nsplit, (float *)dP);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(parts, dP, psz, hipMemcpyDeviceToHost);
+    hipFree(dA); hipFree(dW); hipFree(dP);
+    HIPCHK(e);
+    return nsplit;
+}
+
+int lm_gemm_split_count(int M, int N, int K)
+{
+    if (M < 1 || N < 1 || K < 32 || K % 32) return LM_ERR_INVALID;
+    return lmk_pick_split(M, N, K);
 }

@@ -107,6 +107,8 @@ def lib():
         "lm_selftest_reduce": (I, [fp, fp]),
         "lm_profile_decode": (I, [P, I, ip, ip, I, fp, ip]),
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
+        "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
+        "lm_gemm_split_count": (I, [I, I, I]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -243,6 +245,30 @@ def selftest_gemm(A: np.ndarray, W16: np.ndarray, want_parts: bool = False):
         raise LMError(rc, "lm_selftest_gemm")
     if want_parts:
         return out, parts[..., 0].view(np.float32), parts[..., 1]
+    return out
+
+
+def gemm_split_count(M: int, N: int, K: int) -> int:
+    """K-split count the runtime uses for a decode-row [M, K] x [N, K]^T GEMM."""
+    n = lib().lm_gemm_split_count(M, N, K)
+    if n < 0:
+        raise LMError(n, "lm_gemm_split_count")
+    return n
+
+
+def selftest_gemm_split(A16: np.ndarray, W16: np.ndarray, nsplit: int = 0) -> np.ndarray:
+    """Partials [n, M, N] of the K-split decode-row GEMM (M <= 64); A16, W16 are
+    uint16 fp16 bits [M, K], [N, K]; nsplit 0 = the runtime's choice."""
+    A16 = np.ascontiguousarray(A16, dtype=np.uint16)
+    W16 = np.ascontiguousarray(W16, dtype=np.uint16)
+    M, K = A16.shape
+    N = W16.shape[0]
+    n = nsplit or gemm_split_count(M, N, K)
+    out = np.empty((n, M, N), dtype=np.float32)
+    rc = lib().lm_selftest_gemm_split(M, N, K, nsplit, _u16p(A16), _u16p(W16), _fp(out))
+    if rc < 0:
+        raise LMError(rc, "lm_selftest_gemm_split")
+    assert rc == n
     return out
 
 

@@ -9,7 +9,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 32), (30, 96, 256), (32, 768, 768), (64, 2304, 768),
                                    (50, 200, 2048), (64, 768, 5632), (128, 128, 64), (256, 768, 768),
-                                   (200, 2304, 768), (130, 32000, 768), (512, 4096, 2048)])
+                                   (200, 2304, 768), (130, 32000, 768), (512, 4096, 2048),
+                                   (64, 32000, 768), (5, 20000, 256)])
 @pytest.mark.parametrize("a_f32", [False, True])
 def test_gemm_matches_numpy(lm, M, N, K, a_f32):
     rng = np.random.default_rng(M * 7 + N + K)
@@ -26,3 +27,22 @@ def test_gemm_matches_numpy(lm, M, N, K, a_f32):
         blk = C[:, b * 32:min(N, b * 32 + 32)]
         assert np.array_equal(pi[:, b], b * 32 + np.argmax(blk, axis=1))
         assert np.array_equal(pv[:, b], blk.max(axis=1))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 768, 768), (64, 768, 2048), (64, 2304, 768), (7, 768, 768),
+                                   (32, 2048, 5632), (33, 200, 512)])
+@pytest.mark.parametrize("nsplit", [0, 2])
+def test_gemm_split_partials(lm, M, N, K, nsplit):
+    """Each K-split partial is the product over its own K-chunk."""
+    rng = np.random.default_rng(M + 3 * N + 5 * K + nsplit)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float16)
+    P = lm.selftest_gemm_split(A.view(np.uint16), W.view(np.uint16), nsplit)
+    n = P.shape[0]
+    assert n == (nsplit or lm.gemm_split_count(M, N, K)) and K % n == 0
+    kc = K // n
+    for s in range(n):
+        a = A[:, s * kc:(s + 1) * kc].astype(np.float64)
+        w = W[:, s * kc:(s + 1) * kc].astype(np.float64)
+        scale = np.abs(a) @ np.abs(w).T
+        assert np.all(np.abs(P[s] - a @ w.T) <= 1e-5 * scale + 1e-6), s
