@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
                     sacc[nt][i] = v;
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = fmaxf(mx, xor32_f(mx));
             const float mn = fmaxf(mrow, mx);
             /* a query with every key so far masked keeps m = -inf: nothing to scale */
             const float corr = mn == -INFINITY ? 1.f : exp2f(mrow - mn);
@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     if (!wave_active) return;
     /* finish the row sum across the lane pair and write O / l:
      * element i of o[j] is dim j*32 + 8*(i/4) + 4*g + i%4 of query l%32 */
-    const float l = lrow + __shfl_xor(lrow, 32, 64);
+    const float l = lrow + xor32_f(lrow);
     if (qrow < nrows) {
         const float inv = 1.0f / l;
         u16 *op = out + (size_t)(row0 + qrow) * NQ + h * HD;

@@ -71,6 +71,30 @@ __device__ __forceinline__ float half_wave_sum(float v)
     return v;
 }
 
+/* Value of lane l ^ 16 (l ^ 32): v_permlane16_swap (v_permlane32_swap), a VALU
+ * exchange.  Swapping v with itself gives (v[l & ~16], v[l | 16]) in every lane
+ * (checked on the device), so the partner is the element the lane's own bit does
+ * not name. */
+__device__ __forceinline__ float xor16_f(float v)
+{
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_f(float v)
+{
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+/* DPP move of an int that leaves lanes outside row_mask unchanged. */
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_keep_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
+}
+
 /* Sum over the wave, returned uniformly (scalar). */
 __device__ __forceinline__ float wave_sum(float v)
 {
@@ -102,6 +126,26 @@ __device__ __forceinline__ float wave_sum_shfl(float v)
 __device__ __forceinline__ void argmax_combine(float &bv, int &bi, float v, int i)
 {
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ void argmax_dpp_step(float &bv, int &bi)
+{
+    const float ov = __builtin_bit_cast(float, dpp_keep_i<CTRL, ROW_MASK>(__builtin_bit_cast(int, bv)));
+    const int oi = dpp_keep_i<CTRL, ROW_MASK>(bi);
+    argmax_combine(bv, bi, ov, oi);
+}
+
+/* (max, index) over each 32-lane half with DPP moves (VALU only): afterwards
+ * lanes 16..31 hold the result of lanes 0..31 and lanes 48..63 that of lanes
+ * 32..63 (read lanes 31 and 63).  Lowest index on ties. */
+__device__ __forceinline__ void half_wave_argmax(float &bv, int &bi)
+{
+    argmax_dpp_step<DPP_QUAD_XOR1>(bv, bi);
+    argmax_dpp_step<DPP_QUAD_XOR2>(bv, bi);
+    argmax_dpp_step<DPP_ROW_HALF_MIRROR>(bv, bi);
+    argmax_dpp_step<DPP_ROW_MIRROR>(bv, bi);
+    argmax_dpp_step<DPP_ROW_BCAST15, 0xA>(bv, bi);
 }
 
 #endif /* K_COMMON_H */

@@ -97,24 +97,20 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         ok[i] = rr[i] < e.M && n < e.N;
     }
     if (E == EPI_STORE || E == EPI_ARGMAX) {
-        if (e.out) {
+        if (e.out) {   /* streamed out: a later kernel or the host reads them */
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = acc[i];
+                if (ok[i]) __builtin_nontemporal_store(acc[i], &e.out[(size_t)rr[i] * e.ldc + n]);
         }
         if (E == EPI_ARGMAX) {
-            /* argmax over the 32 columns of each row (the lanes of one half) */
+            /* argmax over the 32 columns of each row (the lanes of one half),
+             * with DPP moves: lanes 31 and 63 end up with their half's result */
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 float bv = ok[i] ? acc[i] : -INFINITY;
                 int bi = ok[i] ? n : 0x7FFFFFFF;
-#pragma unroll
-                for (int off = 16; off > 0; off >>= 1) {
-                    const float ov = __shfl_xor(bv, off, 64);
-                    const int oi = __shfl_xor(bi, off, 64);
-                    argmax_combine(bv, bi, ov, oi);
-                }
-                if ((lane & 31) == 0 && rr[i] < e.M && n0 < e.N)
+                half_wave_argmax(bv, bi);
+                if ((lane & 31) == 31 && rr[i] < e.M && n0 < e.N)
                     e.part[(size_t)rr[i] * e.nparts + n0 / 32] = LMArgPart{bv, bi};
             }
         }
@@ -127,16 +123,24 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
             if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = xv[i] + acc[i];
     } else if (E == EPI_GATE) {
         /* tile columns 0..15 hold W1 rows 16j.., columns 16..31 the W3 rows */
+        /* rows rr[i], rr[i+1] (i even) of gate index gi: lane c < 16 takes row
+         * rr[i] (h1 its own, h3 from lane c + 16), lane c + 16 takes row rr[i+1]
+         * (h3 its own, h1 from lane c), so every lane evaluates one gate per pair.
+         * sigmoid(h1) = 1/(1 + e^-h1) with the hardware exp2 and reciprocal
+         * (about 1 ulp each in fp32); the gate is rounded to fp16 afterwards. */
         const int c = lane & 31;
+        const bool lo = c < 16;
         const int gi = (n0 / 32) * 16 + (c & 15);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float h3 = __shfl_xor(acc[i], 16, 64);
-            if (c < 16 && ok[i]) {
-                const float h1 = acc[i];
-                const float silu = h1 / (1.0f + expf(-h1));        /* forward.h:101 */
-                e.g[(size_t)rr[i] * e.F + gi] = f2h(silu * h3);     /* forward.h:151 */
-            }
+        for (int i = 0; i < 16; i += 2) {
+            const float other = xor16_f(lo ? acc[i + 1] : acc[i]);
+            const float h1 = lo ? acc[i] : other;
+            const float h3 = lo ? other : acc[i + 1];
+            const int r = lo ? rr[i] : rr[i + 1];
+            const bool okr = lo ? ok[i] : ok[i + 1];
+            const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
+            const float silu = h1 * __builtin_amdgcn_rcpf(1.0f + ex);   /* forward.h:101 */
+            if (okr) e.g[(size_t)r * e.F + gi] = f2h(silu * h3);        /* forward.h:151 */
         }
     } else {  /* EPI_QKV */
         const bool odd = n & 1;
@@ -161,7 +165,7 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float other = __shfl_xor(acc[i], 1, 64);
+            const float other = dpp_f<DPP_QUAD_XOR1>(acc[i]);   /* column n ^ 1 */
             if (!ok[i]) continue;
             float v = acc[i];
             if (rot)   /* pair (a, b) = (even column, odd column), forward.h:62-68 */
@@ -240,6 +244,37 @@ __device__ __forceinline__ void lds_read_wait(u32x4 (&v)[6], const unsigned (&a)
                  : "memory");
 }
 
+/* Split form for software pipelining: lds_read_issue starts the reads, and
+ * lds_wait_regs waits for them while naming their destination registers as
+ * in/out operands, so no use of the results can be scheduled before the wait.
+ * (A register copy of a pending result between the two statements would still
+ * be wrong; the build checks the generated code for that.) */
+template <int N>
+__device__ __forceinline__ void lds_read_issue(u32x4 (&v)[N], const unsigned (&a)[N])
+{
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("ds_read_b128 %0, %1" : "=&v"(v[i]) : "v"(a[i]) : "memory");
+}
+__device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[2])
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]) : : "memory");
+}
+__device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[3])
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]) : : "memory");
+}
+__device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[4])
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : : "memory");
+}
+__device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
+{
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5])
+                 :
+                 : "memory");
+}
+
 template <int BM, int BN, int E>
 __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                   const u16 *__restrict__ W, int K, EpiArgs e,
@@ -280,13 +315,17 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         else
             src[i] = W + (size_t)min(n0 + row - BM, N - 1) * K + chunk * 8;
     }
-    auto issue = [&](u16 *buf, int kt) {
+    /* load instructions [I0, I1) of this wave's share of stage kt into buf */
+    auto issue_range = [&](u16 *buf, int kt, auto I0, auto I1) {
         u16 *dst = buf + wave * LDW * 8 * 64;
-#pragma unroll
-        for (int i = 0; i < LDW; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * BKH),
-                                             (__attribute__((address_space(3))) void *)(dst + i * 8 * 64),
+        static_for<decltype(I0)::value, decltype(I1)::value>([&](auto I) {
+            __builtin_amdgcn_global_load_lds((const void *)(src[I] + kt * BKH),
+                                             (__attribute__((address_space(3))) void *)(dst + I * 8 * 64),
                                              16, 0, 0);
+        });
+    };
+    auto issue = [&](u16 *buf, int kt) {
+        issue_range(buf, kt, std::integral_constant<int, 0>{}, std::integral_constant<int, LDW>{});
     };
 
     f32x16 acc[TM][TN];
@@ -311,24 +350,31 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
             ad[TM + j] = lds_off(st + row * 64 + swz(row, c) * 8);
         }
     };
-    auto compute = [&](const u16 *st) {
+    /* k-steps of one stage; the loads of stage kt2 (when ld) are issued a
+     * quarter before each step's MFMAs, so they queue behind the matrix work
+     * instead of holding the wave after the barrier */
+    auto compute = [&](const u16 *st, u16 *ahead, int kt2, bool ld) {
         u32x4 f[2][NF];
         unsigned ad[NF];
         frag_addr(st, 0, ad);
         lds_read_wait(f[0], ad);
-#pragma unroll
-        for (int ks = 0; ks < BKH / 16; ks++) {
+        static_for<0, BKH / 16>([&](auto KS) {
+            constexpr int ks = decltype(KS)::value;
+            if (ks + 1 < BKH / 16) {      /* next step's reads run under this step's MFMAs */
+                frag_addr(st, ks + 1, ad);
+                lds_read_issue<NF>(f[(ks + 1) & 1], ad);
+            }
+            if (ld)
+                issue_range(ahead, kt2, std::integral_constant<int, ks * LDW / 4>{},
+                            std::integral_constant<int, (ks + 1) * LDW / 4>{});
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = mfma32(__builtin_bit_cast(uint4, f[ks & 1][i]),
                                        __builtin_bit_cast(uint4, f[ks & 1][TM + j]), acc[i][j]);
-            if (ks + 1 < BKH / 16) {
-                frag_addr(st, ks + 1, ad);
-                lds_read_wait(f[(ks + 1) & 1], ad);
-            }
-        }
+            if (ks + 1 < BKH / 16) lds_wait_regs(f[(ks + 1) & 1]);
+        });
     };
     /* one k-stage: wait for this wave's loads of stage kt (at most the next
      * stage's may still be outstanding), then a bare barrier (a fenced
@@ -338,8 +384,7 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
     auto step = [&](int kt, const u16 *cur, u16 *ahead) {
         if (kt + 1 < nk) WAIT_VMCNT(LDW); else WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
-        if (kt + 2 < nk) issue(ahead, kt + 2);
-        compute(cur);
+        compute(cur, ahead, kt + 2, kt + 2 < nk);
     };
     issue(lds0, 0);
     if (nk > 1) issue(lds1, 1);

@@ -291,9 +291,12 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_qkv, r * (NQ + 2 * (size_t)m->NKV) * 4))) return st;
     {
+        /* K-split partials of decode rows, or one [R, D] product of prefill rows */
         const size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
         const size_t rd = r < 64 ? r : 64;
-        if ((st = dev_alloc((void **)&m->d_part, LMK_MAX_SPLIT * rd * w * 4))) return st;
+        size_t n = LMK_MAX_SPLIT * rd * w;
+        if (r * D > n) n = r * D;
+        if ((st = dev_alloc((void **)&m->d_part, n * 4))) return st;
     }
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
     if ((st = dev_alloc((void **)&m->d_rtok, r * 4))) return st;
@@ -596,12 +599,15 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
     hipStream_t s = m->stream;
     const int D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, NQKV = NQ + 2 * NKV;
     const size_t sx = (size_t)M * D;   /* split stride of a [M, D] partial */
-    /* decode rows (M <= 64) run narrow projections K-split: the partials land in
-     * d_part and the kernel that next reads x adds them (the residual add) */
+    /* Wo and W2 write their product, not x: into d_part as fp32 (decode rows
+     * (M <= 64) run these narrow projections K-split, one partial per split),
+     * and the row norm that next reads x adds it (the residual add).  Only
+     * unsplit decode rows keep the residual add in the GEMM epilogue. */
     const int dec = M <= 64;
     const int ns_qkv = dec ? lmk_pick_split(M, NQKV, D) : 1;
     const int ns_wo = dec ? lmk_pick_split(M, D, NQ) : 1;
     const int ns_w2 = dec ? lmk_pick_split(M, D, F) : 1;
+    const int sep_wo = !dec || ns_wo > 1, sep_w2 = !dec || ns_w2 > 1;
     const float *pend = NULL;          /* W2 partials not yet added to x */
     int pend_ns = 0;
     LMEpilogue ep;
@@ -638,8 +644,14 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         else
             KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
                                  m->max_seq, NULL, m->d_a16));
-        if (ns_wo > 1) {
-            KCHK(lmk_gemm_split(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, ns_wo, m->d_part));
+        if (sep_wo) {
+            if (ns_wo > 1) {
+                KCHK(lmk_gemm_split(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, ns_wo, m->d_part));
+            } else {
+                memset(&ep, 0, sizeof(ep));
+                ep.out = m->d_part; ep.ldc = D;
+                KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, LMK_EPI_STORE, &ep));
+            }
             KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, m->d_part, ns_wo, sx,
                              m->d_rms_ffn + (size_t)l * D, m->d_xn16));
         } else {
@@ -652,8 +664,14 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         memset(&ep, 0, sizeof(ep));
         ep.g = m->d_g16; ep.F = F;
         KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
-        if (ns_w2 > 1) {
-            KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));
+        if (sep_w2) {
+            if (ns_w2 > 1) {
+                KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));
+            } else {
+                memset(&ep, 0, sizeof(ep));
+                ep.out = m->d_part; ep.ldc = D;
+                KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F, LMK_EPI_STORE, &ep));
+            }
             pend = m->d_part;
             pend_ns = ns_w2;
         } else {
