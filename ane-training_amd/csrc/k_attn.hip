@@ -17,9 +17,9 @@
  * 32): the softmax needs one cross-lane exchange per tile, and the accumulator
  * already has the layout of the B operand of the V^T P^T product, up to an order
  * of the 16 keys of each MFMA step.  That order is undone by storing V^T in LDS
- * with bits 2 and 3 of the key index swapped.  K and V^T of tile t+1 are fetched
- * into registers while tile t computes, and stored into the other of two LDS
- * buffers.
+ * with bits 2 and 3 of the key index swapped.  K and V^T of tile t+2 are fetched
+ * into registers while tile t computes, and tile t+1 is stored into the other of
+ * two LDS buffers.
  */
 #include "k_common.h"
 #include "lm_internal.h"
@@ -87,8 +87,10 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     /* K / V chunks of one tile: chunk c = tid + i*AT is key c / (HD/8), dims
      * (c % (HD/8))*8 .. +8; keys past the block's last position repeat it (they
      * are masked for every query that reads them) */
-    uint4 rk[CPT], rv[CPT];
-    auto fetch = [&](int kt) {
+    /* two register sets: tile t sits in set t % 2 from its fetch (two tiles
+     * ahead of its use) until it is stored to LDS (one tile ahead) */
+    uint4 rk0[CPT], rv0[CPT], rk1[CPT], rv1[CPT];
+    auto fetch = [&](int kt, uint4 (&rk)[CPT], uint4 (&rv)[CPT]) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
@@ -97,7 +99,7 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
             rv[i] = kv8_f16(vc + off);
         }
     };
-    auto stash = [&](int b) {
+    auto stash = [&](int b, const uint4 (&rk)[CPT], const uint4 (&rv)[CPT]) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
@@ -109,7 +111,8 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
                 svt[b][(d0 + j) * VLD + pk] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
         }
     };
-    fetch(0);
+    fetch(0, rk0, rv0);
+    fetch(1, rk1, rv1);   /* past the last tile: the last position again, unused */
 
     /* this wave's queries: block rows wr0 .. wr0+31; lane l takes row wr0 + l%32 */
     const int wr0 = wave * 32;
@@ -129,11 +132,14 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     for (int j = 0; j < DT; j++) o[j] = (f32x16){};
     float mrow = -INFINITY, lrow = 0.f;
 
-    stash(0);
+    stash(0, rk0, rv0);
     __syncthreads();
-    for (int kt = 0; kt < ntiles; kt++) {
+    /* tile kt: fetch tile kt+2 into the set tile kt left (unconditionally, so
+     * the compiler waits only for the older set), compute kt, store kt+1 */
+    auto body = [&](int kt, uint4 (&rka)[CPT], uint4 (&rva)[CPT], const uint4 (&rkb)[CPT],
+                    const uint4 (&rvb)[CPT]) {
         const int b = kt & 1;
-        if (kt + 1 < ntiles) fetch(kt + 1);
+        fetch(kt + 2, rka, rva);
         const int k0 = kt * BKV;
         if (wave_active && k0 <= wave_last) {     /* wave-uniform */
             const u16 *K = sk[b], *VT = svt[b];
@@ -195,8 +201,12 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
                         o[j] = mfma32h(va, pb[nt][hh], o[j]);
                     }
         }
-        if (kt + 1 < ntiles) stash(b ^ 1);
+        if (kt + 1 < ntiles) stash(b ^ 1, rkb, rvb);
         __syncthreads();
+    };
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        body(kt, rk0, rv0, rk1, rv1);
+        if (kt + 1 < ntiles) body(kt + 1, rk1, rv1, rk0, rv0);
     }
     if (!wave_active) return;
     /* finish the row sum across the lane pair and write O / l:

@@ -314,17 +314,28 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
     float m = -INFINITY, l = 0.f, o[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) o[j] = 0.f;
-    for (int t = wv; t < ntiles; t += NWAVE) {
-        Raw kr[NP], vr[NP];
+    /* the wave's first tile is loaded before pos[b] has arrived (positions
+     * clamped into the cache, masked below), so the K/V fetch does not wait for
+     * it; later tiles load positions < ctx only */
+    Raw kr[NP], vr[NP];
 #pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const int p = t * TILE + pp + PP * i;
-            if (p < ctx) {
-                kv_raw_load(K + (size_t)p * HD, kr[i]);
-                kv_raw_load(V + (size_t)p * HD, vr[i]);
-            } else {
-                kv_raw_zero(kr[i]);
-                kv_raw_zero(vr[i]);
+    for (int i = 0; i < NP; i++) {
+        const int p = min(wv * TILE + pp + PP * i, max_seq - 1);
+        kv_raw_load(K + (size_t)p * HD, kr[i]);
+        kv_raw_load(V + (size_t)p * HD, vr[i]);
+    }
+    for (int t = wv; t < ntiles; t += NWAVE) {
+        if (t != wv) {
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                const int p = t * TILE + pp + PP * i;
+                if (p < ctx) {
+                    kv_raw_load(K + (size_t)p * HD, kr[i]);
+                    kv_raw_load(V + (size_t)p * HD, vr[i]);
+                } else {
+                    kv_raw_zero(kr[i]);
+                    kv_raw_zero(vr[i]);
+                }
             }
         }
         float s[NP];

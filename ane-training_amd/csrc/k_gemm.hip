@@ -75,6 +75,7 @@ struct EpiArgs {
     const int *slot, *pos;
     const float *rope_cos, *rope_sin;
     size_t sstride;         /* STORE of a K-split GEMM: out of split s is out + s*sstride */
+    int nt;                 /* STORE / ARGMAX: non-temporal stores of out */
 };
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
@@ -97,10 +98,14 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         ok[i] = rr[i] < e.M && n < e.N;
     }
     if (E == EPI_STORE || E == EPI_ARGMAX) {
-        if (e.out) {   /* streamed out: a later kernel or the host reads them */
+        if (e.out && e.nt) {   /* logits: streamed past the caches */
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 if (ok[i]) __builtin_nontemporal_store(acc[i], &e.out[(size_t)rr[i] * e.ldc + n]);
+        } else if (e.out) {
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = acc[i];
         }
         if (E == EPI_ARGMAX) {
             /* argmax over the 32 columns of each row (the lanes of one half),
@@ -568,18 +573,35 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
             }
         }
         if (ns > 0) {
-            for (int q = 0; q < ns; q++) {
+            /* partials in groups of four: the group's loads are all issued before
+             * its adds (the adds stay in split order) */
+            auto add_part = [&](const float (&t)[C4 * 4]) {
+#pragma unroll
+                for (int i = 0; i < PER; i++) v[i] += t[i];
+            };
+            auto load_part = [&](int q, float (&t)[C4 * 4]) {
                 const float *pr = sp + q * sstride + (size_t)m * D;
 #pragma unroll
                 for (int c = 0; c < C4; c++) {
                     if (PER >= 4) {
                         const float4 q4 = *(const float4 *)(pr + col(c));
-                        v[4 * c] += q4.x; v[4 * c + 1] += q4.y; v[4 * c + 2] += q4.z; v[4 * c + 3] += q4.w;
+                        t[4 * c] = q4.x; t[4 * c + 1] = q4.y; t[4 * c + 2] = q4.z; t[4 * c + 3] = q4.w;
                     } else {
 #pragma unroll
-                        for (int i = 0; i < PER; i++) v[i] += pr[col(0) + i];
+                        for (int i = 0; i < PER; i++) t[i] = pr[col(0) + i];
                     }
                 }
+            };
+            int q = 0;
+            for (; q + 4 <= ns; q += 4) {
+                float t0[C4 * 4], t1[C4 * 4], t2[C4 * 4], t3[C4 * 4];
+                load_part(q, t0); load_part(q + 1, t1); load_part(q + 2, t2); load_part(q + 3, t3);
+                add_part(t0); add_part(t1); add_part(t2); add_part(t3);
+            }
+            for (; q < ns; q++) {
+                float t0[C4 * 4];
+                load_part(q, t0);
+                add_part(t0);
             }
         }
     }
@@ -698,6 +720,7 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     e.NQ = p->NQ; e.NKV = p->NKV; e.hd = p->hd; e.Hkv = p->Hkv; e.max_seq = p->max_seq;
     e.slot = p->slot; e.pos = p->pos; e.rope_cos = p->rope_cos; e.rope_sin = p->rope_sin;
     e.sstride = 0;
+    e.nt = p->stream_out;
     return e;
 }
 

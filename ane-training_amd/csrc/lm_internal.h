@@ -110,6 +110,8 @@ int lmk_attn_prefill(hipStream_t s, const float *q, const void *kc, const void *
 typedef struct {
     float *out;              /* STORE / RESID                                      */
     int ldc;
+    int stream_out;          /* STORE / ARGMAX: out is not read again on the device
+                                soon (logits): non-temporal stores                  */
     LMArgPart *part;         /* ARGMAX: [M, ceil(N/32)] argmax partials            */
     uint16_t *g;             /* GATE: [M, F] fp16                                  */
     int F;
@@ -137,7 +139,7 @@ int lmk_pick_split(int M, int N, int K);
 int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                    int K, int ns, float *part);
 
-/* One wave per row: with emb != NULL x[m] is first set to the embedding row
+/* One work-group per row: with emb != NULL x[m] is first set to the embedding row
  * emb[tok[m]]; with ns > 0 the ns partials sp[s][m] (sstride floats apart) of a
  * K-split projection are added to x[m] first (the residual add); then
  * xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */

@@ -689,7 +689,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
     }
     KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, pend, pend_ns, sx, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
-    ep.out = logits; ep.ldc = m->V;
+    ep.out = logits; ep.ldc = m->V; ep.stream_out = 1;
     if (seq_rows > 1) {   /* prefill: logits only */
         if (logits) KCHK(lmk_gemm(s, m->d_xn16, D, m->d_wcls, M, m->V, D, LMK_EPI_STORE, &ep));
     } else {              /* decode: argmax partials for the greedy step (+ logits) */
@@ -925,7 +925,7 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
     LMEpilogue ep;
     KCHK(lmk_rownorm(s, x_rows, m->D, M, NULL, NULL, NULL, 0, 0, m->d_rms_final, m->d_xn16));
     memset(&ep, 0, sizeof(ep));
-    ep.out = m->d_logits; ep.ldc = m->V;
+    ep.out = m->d_logits; ep.ldc = m->V; ep.stream_out = 1;
     KCHK(lmk_gemm(s, m->d_xn16, m->D, m->d_wcls, M, m->V, m->D, LMK_EPI_STORE, &ep));
     return LM_OK;
 }
