@@ -314,18 +314,22 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
     float m = -INFINITY, l = 0.f, o[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) o[j] = 0.f;
-    /* the wave's first tile is loaded before pos[b] has arrived (positions
-     * clamped into the cache, masked below), so the K/V fetch does not wait for
-     * it; later tiles load positions < ctx only */
+    /* hd 64: the wave's first tile is loaded before pos[b] has arrived
+     * (positions clamped into the cache, masked below), so the K/V fetch does
+     * not wait for it; later tiles, and every tile at hd 128 (where holding a
+     * tile across the loop would halve occupancy), load positions < ctx only */
+    constexpr bool EARLY = HD == 64;
     Raw kr[NP], vr[NP];
+    if (EARLY) {
 #pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const int p = min(wv * TILE + pp + PP * i, max_seq - 1);
-        kv_raw_load(K + (size_t)p * HD, kr[i]);
-        kv_raw_load(V + (size_t)p * HD, vr[i]);
+        for (int i = 0; i < NP; i++) {
+            const int p = min(wv * TILE + pp + PP * i, max_seq - 1);
+            kv_raw_load(K + (size_t)p * HD, kr[i]);
+            kv_raw_load(V + (size_t)p * HD, vr[i]);
+        }
     }
     for (int t = wv; t < ntiles; t += NWAVE) {
-        if (t != wv) {
+        if (!EARLY || t != wv) {
 #pragma unroll
             for (int i = 0; i < NP; i++) {
                 const int p = t * TILE + pp + PP * i;

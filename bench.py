@@ -106,75 +106,83 @@ def attn_flops_prefill(cfg, S, nseq):
     return nseq * cfg.n_layers * cfg.n_heads * 2 * 2 * hd * S * (S + 1) / 2
 
 
-def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False):
+def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, only=None):
     """Configs C1-C4 of the baseline (MFMA paths), as extra entries.  direct:
-    launch decode kernels directly instead of replaying graphs."""
+    launch decode kernels directly instead of replaying graphs; only: run just
+    these configs ("c1" .. "c4")."""
     out = {}
+
+    def want(c):
+        return only is None or c in only
     cfg = S.make_config(**S.STORIES_110M)
     wbytes, _ = model_bytes(cfg)
     V = 32000
     # C1: 256-token causal prefill, all 256 x 32000 fp32 logits (kept on the device)
-    m = S.Model.create(cfg, w16_stories, True, 1, 256)
-    toks = np.random.default_rng(101).integers(0, V, 256).astype(np.int32)
-    ms = _timed(m, lambda: m.prefill(toks, want_logits=False), reps_prefill)
-    fl = linear_flops(cfg, 256) + attn_flops_prefill(cfg, 256, 1)
-    by = wbytes + 256 * V * 4
-    out["c1_prefill_256"] = {"value": round(256 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
-                             "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                             "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                             "algorithmic_bytes": int(by), "flops": fl}
-    m.close()
+    if want("c1"):
+        m = S.Model.create(cfg, w16_stories, True, 1, 256)
+        toks = np.random.default_rng(101).integers(0, V, 256).astype(np.int32)
+        ms = _timed(m, lambda: m.prefill(toks, want_logits=False), reps_prefill)
+        fl = linear_flops(cfg, 256) + attn_flops_prefill(cfg, 256, 1)
+        by = wbytes + 256 * V * 4
+        out["c1_prefill_256"] = {"value": round(256 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
+                                 "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                                 "algorithmic_bytes": int(by), "flops": fl}
+        m.close()
     # C3: 8 x 256 = 2048-token causal forward with all logits (MFMA bound)
-    m = S.Model.create(cfg, w16_stories, True, 8, 256)
-    toks = np.random.default_rng(103).integers(0, V, (8, 256)).astype(np.int32)
-    ms = _timed(m, lambda: m.prefill_batch(toks, mode=S.LM_LOGITS_ALL, want_logits=False), reps_prefill)
-    fl = linear_flops(cfg, 2048) + attn_flops_prefill(cfg, 256, 8)
-    out["c3_forward_8x256"] = {"value": round(2048 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
-                               "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                               "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "flops": fl}
-    m.close()
+    if want("c3"):
+        m = S.Model.create(cfg, w16_stories, True, 8, 256)
+        toks = np.random.default_rng(103).integers(0, V, (8, 256)).astype(np.int32)
+        ms = _timed(m, lambda: m.prefill_batch(toks, mode=S.LM_LOGITS_ALL, want_logits=False), reps_prefill)
+        fl = linear_flops(cfg, 2048) + attn_flops_prefill(cfg, 256, 8)
+        out["c3_forward_8x256"] = {"value": round(2048 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
+                                   "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                                   "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "flops": fl}
+        m.close()
     # C2: 64 sequences, 192-token prompts prefilled, then 64 greedy steps each
-    m = S.Model.create(cfg, w16_stories, True, 64, 256)
-    if direct:
-        m.set_option(S.LM_OPT_USE_GRAPH, 0)
-    rng = np.random.default_rng(102)
-    prompts = rng.integers(0, V, (64, 192)).astype(np.int32)
-    ms_pf = _timed(m, lambda: m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST, want_logits=False), 2)
-    lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
-    first = np.argmax(lg, axis=1).astype(np.int32)
-    pos = np.full(64, 192, np.int32)
-    ms = _timed(m, lambda: m.generate_greedy(first, pos, 64), reps_decode)
-    kv_step = 64 * 12 * 2 * 768 * 2 * (192 + 64 / 2 + 0.5)    # mean context 224.5
-    by_step = wbytes + kv_step + 64 * V * 0 + 64 * 2 * 12 * 768 * 2
-    t_step = ms * 1e-3 / 64
-    out["c2_decode_b64"] = {"value": round(64 * 64 / (ms * 1e-3), 1), "unit": "tok/s",
-                            "ms_per_step": round(ms / 64, 4),
-                            "hbm_frac": round(by_step / t_step / 1e9 / HBM_PEAK_GBS, 4),
-                            "algorithmic_bytes_per_step": int(by_step),
-                            "prefill_64x192_tok_s": round(64 * 192 / (ms_pf * 1e-3), 1)}
-    m.close()
+    if want("c2"):
+        m = S.Model.create(cfg, w16_stories, True, 64, 256)
+        if direct:
+            m.set_option(S.LM_OPT_USE_GRAPH, 0)
+        rng = np.random.default_rng(102)
+        prompts = rng.integers(0, V, (64, 192)).astype(np.int32)
+        ms_pf = _timed(m, lambda: m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST, want_logits=False), 2)
+        lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
+        first = np.argmax(lg, axis=1).astype(np.int32)
+        pos = np.full(64, 192, np.int32)
+        ms = _timed(m, lambda: m.generate_greedy(first, pos, 64), reps_decode)
+        kv_step = 64 * 12 * 2 * 768 * 2 * (192 + 64 / 2 + 0.5)    # mean context 224.5
+        by_step = wbytes + kv_step + 64 * V * 0 + 64 * 2 * 12 * 768 * 2
+        t_step = ms * 1e-3 / 64
+        out["c2_decode_b64"] = {"value": round(64 * 64 / (ms * 1e-3), 1), "unit": "tok/s",
+                                "ms_per_step": round(ms / 64, 4),
+                                "hbm_frac": round(by_step / t_step / 1e9 / HBM_PEAK_GBS, 4),
+                                "algorithmic_bytes_per_step": int(by_step),
+                                "prefill_64x192_tok_s": round(64 * 192 / (ms_pf * 1e-3), 1)}
+        m.close()
     # C4: scaled Llama-2 model, 32 sequences, 512-token contexts, 128 greedy steps
-    d4 = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
-              seq_len=640)
-    cfg4 = S.make_config(**d4)
-    w4 = S.synth_weights_f16(cfg4, 4, 0.02, True)
-    m = S.Model.create(cfg4, w4, True, 32, 640)
-    if direct:
-        m.set_option(S.LM_OPT_USE_GRAPH, 0)
-    del w4
-    prompts = np.random.default_rng(104).integers(0, V, (32, 512)).astype(np.int32)
-    lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
-    first = np.argmax(lg, axis=1).astype(np.int32)
-    pos = np.full(32, 512, np.int32)
-    ms = _timed(m, lambda: m.generate_greedy(first, pos, 128), 1)
-    wb4, _ = model_bytes(cfg4)
-    kv4 = 32 * 16 * 2 * 2048 * 2 * (512 + 128 / 2 + 0.5)
-    t4 = ms * 1e-3 / 128
-    out["c4_scaled_decode_b32"] = {"value": round(32 * 128 / (ms * 1e-3), 1), "unit": "tok/s",
-                                   "ms_per_step": round(ms / 128, 4),
-                                   "hbm_frac": round((wb4 + kv4) / t4 / 1e9 / HBM_PEAK_GBS, 4),
-                                   "algorithmic_bytes_per_step": int(wb4 + kv4)}
-    m.close()
+    if want("c4"):
+        d4 = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
+                  seq_len=640)
+        cfg4 = S.make_config(**d4)
+        w4 = S.synth_weights_f16(cfg4, 4, 0.02, True)
+        m = S.Model.create(cfg4, w4, True, 32, 640)
+        if direct:
+            m.set_option(S.LM_OPT_USE_GRAPH, 0)
+        del w4
+        prompts = np.random.default_rng(104).integers(0, V, (32, 512)).astype(np.int32)
+        lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
+        first = np.argmax(lg, axis=1).astype(np.int32)
+        pos = np.full(32, 512, np.int32)
+        ms = _timed(m, lambda: m.generate_greedy(first, pos, 128), 1)
+        wb4, _ = model_bytes(cfg4)
+        kv4 = 32 * 16 * 2 * 2048 * 2 * (512 + 128 / 2 + 0.5)
+        t4 = ms * 1e-3 / 128
+        out["c4_scaled_decode_b32"] = {"value": round(32 * 128 / (ms * 1e-3), 1), "unit": "tok/s",
+                                       "ms_per_step": round(ms / 128, 4),
+                                       "hbm_frac": round((wb4 + kv4) / t4 / 1e9 / HBM_PEAK_GBS, 4),
+                                       "algorithmic_bytes_per_step": int(wb4 + kv4)}
+        m.close()
     return out
 
 
@@ -189,11 +197,22 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip configs C1-C4")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"],
+                    help="run just this config of C1-C4 (for profiling) and print its entry")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one MI355X per box); "
               "--gpus must be 1", file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        import stories_lm as S
+        rc = S.init()
+        if rc:
+            raise SystemExit(f"lm_init: {S.strerror(rc)}")
+        cfg = S.make_config(**S.STORIES_110M)
+        w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
+        print(json.dumps(bench_extra(S, w16, direct=args.direct, only={args.only})), flush=True)
+        return
     steps = max(SEQ, (args.steps + SEQ - 1) // SEQ * SEQ)
     warm = (args.warmup + SEQ - 1) // SEQ * SEQ
     import stories_lm as S
