@@ -282,8 +282,8 @@ __device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
 
 template <int BM, int BN, int E>
 __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
-                                                  const u16 *__restrict__ W, int K, EpiArgs e,
-                                                  int tm, int tn)
+                                                  const u16 *__restrict__ W, int K, int kc,
+                                                  EpiArgs e, int tm, int tn)
 {
     constexpr int WM = BM / 2, WN = BN / 2;     /* wave tile, waves 2 x 2 */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
@@ -309,16 +309,18 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
     const int m0 = (g % tm) * BM, n0 = (g / tm) * BN;
     const int M = e.M, N = e.N;
 
-    /* per-lane source rows of this wave's load instructions (fixed over k) */
+    /* per-lane source rows of this wave's load instructions (fixed over k);
+     * work-group split y takes k = y*kc .. y*kc + kc - 1 (kc = K unsplit) */
+    const int k0 = blockIdx.y * kc;
     const u16 *src[LDW];
 #pragma unroll
     for (int i = 0; i < LDW; i++) {
         const int row = (wave * LDW + i) * 8 + lane / 8;
         const int chunk = swz(row, lane % 8);
         if (row < BM)
-            src[i] = A + (size_t)min(m0 + row, M - 1) * lda + chunk * 8;
+            src[i] = A + (size_t)min(m0 + row, M - 1) * lda + k0 + chunk * 8;
         else
-            src[i] = W + (size_t)min(n0 + row - BM, N - 1) * K + chunk * 8;
+            src[i] = W + (size_t)min(n0 + row - BM, N - 1) * K + k0 + chunk * 8;
     }
     /* load instructions [I0, I1) of this wave's share of stage kt into buf */
     auto issue_range = [&](u16 *buf, int kt, auto I0, auto I1) {
@@ -385,7 +387,7 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
      * stage's may still be outstanding), then a bare barrier (a fenced
      * __syncthreads would wait for every outstanding load) so all waves' loads
      * of stage kt have landed and stage kt-1's buffer is free for stage kt+2 */
-    const int nk = K / BKH;
+    const int nk = kc / BKH;
     auto step = [&](int kt, const u16 *cur, u16 *ahead) {
         if (kt + 1 < nk) WAIT_VMCNT(LDW); else WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
@@ -398,6 +400,7 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         if (kt + 1 < nk) step(kt + 1, lds1, lds0);
         if (kt + 2 < nk) step(kt + 2, lds2, lds1);
     }
+    if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -730,7 +733,17 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
     hipLaunchKernelGGL((k_gemm_tile<BM, BN, E>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A, lda,
-                       (const u16 *)W, K, e, tm, tn);
+                       (const u16 *)W, K, K, e, tm, tn);
+}
+
+/* The tiled kernel over grid (tiles, ns), split y taking k-chunk y*K/ns. */
+template <int BM, int BN>
+static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
+                              int N, int K, int ns, const EpiArgs &e)
+{
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE>), dim3(tm * tn, ns), dim3(GT), 0, s,
+                       (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
 }
 
 template <int E>

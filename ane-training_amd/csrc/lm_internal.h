@@ -66,13 +66,24 @@ int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
 int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D,
                     int B, float *x);
 
-/* xn = rmsnorm(x[b]) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
+/* xn = rmsnorm(x[b] (+ the nh Wo shares part[b][h], in head order, when part
+ * != NULL)) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
 int lmk_ffn13(hipStream_t s, float *x, const float *rms_w,
-              const uint16_t *w13, int D, int F, int B, float *g);
+              const uint16_t *w13, int D, int F, int B, float *g, const float *part, int nh);
 
-/* x[b, r] += W2[r, :] . g[b, :] */
+/* x[b, r] += (the nh Wo shares part[b][h][r], in head order, when part !=
+ * NULL) + W2[r, :] . g[b, :] */
 int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
-                    int F, int B, float *x);
+                    int F, int B, float *x, const float *part, int nh);
+
+/* Attention of head h, row b, fused with that head's share of Wo:
+ * part[(b*H + h)*D + r] = Wo[r, h*hd .. +hd] . attn(b, h) (D = H*hd, slot b =
+ * row b).  Only for shapes lmk_attn_wo_supported accepts (the Wo head block
+ * must fit in LDS). */
+int lmk_attn_wo_supported(int D, int hd);
+int lmk_attn_wo(hipStream_t s, const float *q, const void *kc, const void *vc, int kv_f32,
+                const int *pos, int B, int H, int Hkv, int hd, int max_seq, int D,
+                const uint16_t *wo, float *part);
 
 /* xn = rmsnorm(x[b]) * w; logits[b, v] = Wcls[v] . xn (logits may be NULL);
  * argmax partials (lowest index on ties) to part[b * nblk + blk], nblk =

@@ -55,6 +55,8 @@ struct LMModel {
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
     float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd, *d_qkv;
     float *d_part;              /* partials of K-split decode-row GEMMs       */
+    float *d_opart;             /* batch 1-4 chain: per-head Wo shares [4][H][D] */
+    int fuse_wo;                /* attention + Wo fused in the batch 1-4 chain  */
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
@@ -386,6 +388,8 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_tok, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
+    m->fuse_wo = lmk_attn_wo_supported(m->D, m->hd);
+    if ((st = dev_alloc((void **)&m->d_opart, (size_t)MAX_GEMV_B * m->H * D * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
     m->pl_grid = lmk_persist_grid();
     m->pl_ok = m->pl_grid > 0 && lmk_persist_supported(m->D, m->F, m->hd, m->H);
@@ -465,7 +469,7 @@ void lm_free(LMModel *m)
     free_rows(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_ll, m->d_ptok,
+                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_opart, m->d_ll, m->d_ptok,
                    m->d_err};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
@@ -495,6 +499,13 @@ int lm_set_option(LMModel *m, int option, int value)
         return LM_OK;
     case LM_OPT_USE_GRAPH:
         m->use_graph = value ? 1 : 0;
+        return LM_OK;
+    case LM_OPT_FUSE_ATTN_WO:
+        if (value && !lmk_attn_wo_supported(m->D, m->hd)) return LM_ERR_UNSUPPORTED;
+        if ((value ? 1 : 0) == m->fuse_wo) return LM_OK;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        drop_graphs(m);
+        m->fuse_wo = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_KV_F32:
         if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
@@ -537,17 +548,23 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
                           m->max_seq));
         break;
     case LM_KERN_ATTN:
-        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
-                             m->hd, m->max_seq, m->d_attn, NULL));
+        if (m->fuse_wo)
+            KCHK(lmk_attn_wo(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
+                             m->max_seq, D, lw + m->off_wo, m->d_opart));
+        else
+            KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
+                                 m->hd, m->max_seq, m->d_attn, NULL));
         break;
-    case LM_KERN_WO:
-        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
+    case LM_KERN_WO:   /* fused: the attention kernel wrote the per-head shares */
+        if (!m->fuse_wo) KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
         break;
     case LM_KERN_W13:
-        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
+        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g,
+                       m->fuse_wo ? m->d_opart : NULL, m->H));
         break;
     case LM_KERN_W2:
-        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
+        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x,
+                             m->fuse_wo ? m->d_opart : NULL, m->H));
         break;
     case LM_KERN_CLS:
         KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
@@ -1099,6 +1116,11 @@ int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int 
     HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
     for (int f = 0; f < LM_KERN_COUNT && rc == LM_OK; f++) {
         const int per_step = (f == LM_KERN_CLS || f == LM_KERN_ARGMAX) ? 1 : m->L;
+        if (f == LM_KERN_WO && m->fuse_wo) {   /* part of the attention kernel */
+            if (launches_per_step) launches_per_step[f] = 0;
+            us_per_launch[f] = 0.f;
+            continue;
+        }
         if (launches_per_step) launches_per_step[f] = per_step;
         hipGraph_t g = NULL;
         hipGraphExec_t ge = NULL;

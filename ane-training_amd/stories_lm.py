@@ -34,6 +34,7 @@ LM_DTYPE_F16 = 1
 LM_OPT_DECODE_PATH = 1
 LM_OPT_USE_GRAPH = 2
 LM_OPT_KV_F32 = 3
+LM_OPT_FUSE_ATTN_WO = 4
 # kernel families of a decode step (LM_KERN_* in stories_lm.h)
 KERN_NAMES = ("qkv", "attn", "wo", "w13", "w2", "cls", "argmax")
 
@@ -58,6 +59,72 @@ class LMWeights(C.Structure):
 class LMDeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32), ("compute_units", C.c_int),
                 ("clock_khz", C.c_int), ("l2_bytes", C.c_int), ("total_mem", C.c_size_t)]
+
+
+class Rng(C.Structure):
+    """drand48-recurrence random stream (LMRng)."""
+    _fields_ = [("x", C.c_uint64)]
+
+    def __init__(self, seed: int = 0):
+        super().__init__()
+        lib().lm_rng_seed(C.byref(self), seed)
+
+    def next(self) -> float:
+        return lib().lm_rng_next(C.byref(self))
+
+
+class Tokenizer:
+    """llama2.c tokenizer (LMTokenizer)."""
+
+    def __init__(self, path: str, vocab_size: int):
+        st = C.c_int(0)
+        self._h = lib().lm_tokenizer_load(path.encode(), vocab_size, C.byref(st))
+        if not self._h:
+            raise LMError(st.value, "lm_tokenizer_load")
+
+    def close(self):
+        if self._h:
+            lib().lm_tokenizer_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def vocab_size(self) -> int:
+        return lib().lm_tokenizer_vocab_size(self._h)
+
+    def decode(self, token: int) -> bytes:
+        return lib().lm_tokenizer_decode(self._h, token)
+
+    def encode(self, text, max_tokens: int = 1024) -> list:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        out = np.zeros(max(max_tokens, 1), dtype=np.int32)
+        n = lib().lm_tokenizer_encode(self._h, raw, _ip(out), max_tokens)
+        if n < 0:
+            raise LMError(n, "lm_tokenizer_encode")
+        return out[:n].tolist()
+
+
+def sample_argmax(logits) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    return lib().lm_sample_argmax(_fp(x), x.size)
+
+
+def sample_temperature(logits, temp: float, rng: Rng) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = lib().lm_sample_temperature(_fp(x), x.size, temp, C.byref(rng))
+    if r < 0:
+        raise LMError(r, "lm_sample_temperature")
+    return r
+
+
+def sample_topp(logits, temp: float, topp: float, rng: Rng) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = lib().lm_sample_topp(_fp(x), x.size, temp, topp, C.byref(rng))
+    if r < 0:
+        raise LMError(r, "lm_sample_topp")
+    return r
 
 
 class LMError(RuntimeError):
@@ -109,6 +176,16 @@ def lib():
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
         "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
         "lm_gemm_split_count": (I, [I, I, I]),
+        "lm_tokenizer_load": (P, [C.c_char_p, I, ip]),
+        "lm_tokenizer_free": (None, [P]),
+        "lm_tokenizer_vocab_size": (I, [P]),
+        "lm_tokenizer_decode": (C.c_char_p, [P, I]),
+        "lm_tokenizer_encode": (I, [P, C.c_char_p, ip, I]),
+        "lm_rng_seed": (None, [C.POINTER(Rng), C.c_uint64]),
+        "lm_rng_next": (C.c_double, [C.POINTER(Rng)]),
+        "lm_sample_argmax": (I, [fp, I]),
+        "lm_sample_temperature": (I, [fp, I, F, C.POINTER(Rng)]),
+        "lm_sample_topp": (I, [fp, I, F, F, C.POINTER(Rng)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -246,6 +246,9 @@ def main():
     mean_ctx = (SEQ + 1) / 2
     kvb = 2 if args.kv16 else 4
     algo = algorithmic_bytes(cfg, 1, mean_ctx, kvb)
+    if launches["wo"] == 0:   # Wo runs inside the attention kernel (per-head shares)
+        algo["attn"] += algo.pop("wo")
+        del us["wo"], launches["wo"]
     dom = max(us, key=lambda k: us[k] * launches[k])
     dur_us = us[dom]
     achieved = algo[dom] / (dur_us * 1e-6) / 1e9

@@ -206,6 +206,11 @@ int lm_timer_end(LMModel *m, float *ms);
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
+/* LM_OPT_FUSE_ATTN_WO: 1 (default where the shape allows it: D = H*hd with a
+ * Wo head block of D x hd fp16 that fits in LDS, e.g. Stories) runs the batch
+ * 1-4 chain's attention and Wo as one kernel per layer, each head adding its
+ * share of the Wo product to the residual; 0 keeps two kernels. */
+#define LM_OPT_FUSE_ATTN_WO 4
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------
@@ -275,8 +280,9 @@ int lm_gemm_split_count(int M, int N, int K);
 
 /* Kernel families of a decode step (index into lm_profile_decode's output). */
 #define LM_KERN_QKV    0   /* rmsnorm + QKV GEMV + RoPE + KV append          */
-#define LM_KERN_ATTN   1   /* causal attention over the KV cache            */
-#define LM_KERN_WO     2   /* Wo GEMV + residual                            */
+#define LM_KERN_ATTN   1   /* causal attention over the KV cache (+ per-head
+                              Wo shares when LM_OPT_FUSE_ATTN_WO is on)      */
+#define LM_KERN_WO     2   /* Wo GEMV + residual (no launches when fused)   */
 #define LM_KERN_W13    3   /* rmsnorm + W1/W3 GEMV + SiLU gate              */
 #define LM_KERN_W2     4   /* W2 GEMV + residual                            */
 #define LM_KERN_CLS    5   /* final rmsnorm + classifier + argmax partials  */
@@ -291,6 +297,41 @@ int lm_gemm_split_count(int M, int N, int K);
  * entries at pos[b] and the activations overwritten. */
 int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
                       float *us_per_launch, int *launches_per_step);
+
+/* ---------------------------------------------------------------------------
+ * Text: tokenizer, random stream, samplers (host only, no device needed)
+ * ------------------------------------------------------------------------- */
+
+/* llama2.c tokenizer.bin: int max_token_length, then per token {float score,
+ * int len, len bytes} (replaces tokenizer_load, generate.m:37-56).  NULL on
+ * failure with *status = LM_ERR_IO / LM_ERR_FORMAT / LM_ERR_OOM. */
+typedef struct LMTokenizer LMTokenizer;
+LMTokenizer *lm_tokenizer_load(const char *path, int vocab_size, int *status);
+void lm_tokenizer_free(LMTokenizer *t);
+int lm_tokenizer_vocab_size(const LMTokenizer *t);
+
+/* The token's string, "" when out of range (tokenizer_decode, generate.m:58-65). */
+const char *lm_tokenizer_decode(const LMTokenizer *t, int token);
+
+/* Greedy BPE of text into at most max_tokens ids, returned count (or a
+ * negative status): every byte becomes its single-byte token (bytes without
+ * one are skipped), then the adjacent pair whose concatenation is the
+ * highest-scoring token is merged until none is (tokenizer_encode,
+ * generate.m:68-126; no BOS, no leading space). */
+int lm_tokenizer_encode(const LMTokenizer *t, const char *text, int *tokens, int max_tokens);
+
+/* Random stream with the drand48 recurrence and srand48 seeding (the
+ * reference's sampler draws, generate.m:153,197), with explicit state. */
+typedef struct { uint64_t x; } LMRng;
+void lm_rng_seed(LMRng *r, uint64_t seed);
+double lm_rng_next(LMRng *r);
+
+/* Samplers over n host logits (generate.m:129-209): argmax (lowest index on
+ * ties); temperature softmax then one draw; nucleus (top-p) over the
+ * temperature softmax.  Return the token, or a negative status. */
+int lm_sample_argmax(const float *logits, int n);
+int lm_sample_temperature(const float *logits, int n, float temp, LMRng *r);
+int lm_sample_topp(const float *logits, int n, float temp, float topp, LMRng *r);
 
 #ifdef __cplusplus
 }

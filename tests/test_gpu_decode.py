@@ -46,10 +46,13 @@ def test_dpp_wave_reductions(lm):
 
 @pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-def test_tiny_decode_steps_match_oracle(lm, name, d, kv):
-    _say(f"[tiny decode {name} kv{kv}]")
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_tiny_decode_steps_match_oracle(lm, name, d, kv, fuse):
+    """fuse: attention and Wo in one kernel (per-head Wo shares) or two."""
+    _say(f"[tiny decode {name} kv{kv} fuse{fuse}]")
     fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
+    m.set_option(lm.LM_OPT_FUSE_ATTN_WO, fuse)
     got = np.stack([m.forward(int(t), p) for p, t in enumerate(fx["tokens"])])
     np.testing.assert_allclose(got, fx[f"logits_kv{kv}"], **TIGHT)
     np.testing.assert_allclose(got, fx["logits_kv32"], **NORTH_STAR)
@@ -59,13 +62,15 @@ def test_tiny_decode_steps_match_oracle(lm, name, d, kv):
 
 
 @pytest.mark.parametrize("B", [2, 3, 4])
-def test_tiny_batch_decode_matches_oracle(lm, orc, B):
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_tiny_batch_decode_matches_oracle(lm, orc, B, fuse):
     """B slots in one batched step, first in lock-step, then at different
     positions (slot b advances every b+1 steps; a repeated (token, pos) step
     rewrites the same cache entry)."""
-    _say(f"[tiny batch decode B={B}]")
+    _say(f"[tiny batch decode B={B} fuse{fuse}]")
     d = TINY
     m, w16 = make(lm, d, 21, B, 64, True)
+    m.set_option(lm.LM_OPT_FUSE_ATTN_WO, fuse)
     w32 = lm.f16_to_f32(w16)
     seqs = np.random.default_rng(B).integers(0, d["vocab_size"], (B, 40)).astype(np.int32)
     orcs = [orc.Oracle(cfg7(d), w32, True, 64) for _ in range(B)]
