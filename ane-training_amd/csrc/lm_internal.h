@@ -32,6 +32,7 @@ void lmh_tensor_sizes(const Config *c, int untied, size_t sz[LMH_NTENSORS]);
 const void *lmh_weights_ptr(const LMWeights *w, int t);
 int lmh_weights_untied(const LMWeights *w);
 int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data);
+int lmh_read_blzt(const char *path, Config *cfg, float **data);
 
 /* Rows of W1 and W3 are stored interleaved in blocks of LMK_GATE_BLOCK rows:
  * block j = [W1 rows j*G .. j*G+G-1, W3 rows j*G .. j*G+G-1], so any 2G-wide

@@ -460,6 +460,26 @@ LMModel *lm_load_llama2c(const char *path, int max_batch, int max_seq, int *stat
     return m;
 }
 
+LMModel *lm_load_blzt(const char *path, int max_batch, int max_seq, int *status)
+{
+    if (!path) {
+        if (status) *status = LM_ERR_INVALID;
+        return NULL;
+    }
+    Config cfg;
+    float *data = NULL;
+    int rc = lmh_read_blzt(path, &cfg, &data);
+    if (rc) {
+        if (status) *status = rc;
+        return NULL;
+    }
+    LMWeights w;
+    lm_weights_view(&cfg, LM_DTYPE_F32, data, 0, &w);
+    LMModel *m = lm_create(&cfg, &w, max_batch, max_seq, status);
+    free(data);
+    return m;
+}
+
 void lm_free(LMModel *m)
 {
     if (!m) return;

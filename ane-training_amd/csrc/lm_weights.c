@@ -334,6 +334,127 @@ int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data)
 }
 
 /* ------------------------------------------------------------------------- */
+/* BLZT v4 checkpoints (the reference's training checkpoints)                 */
+/* ------------------------------------------------------------------------- */
+
+/* Header of a BLZT checkpoint, 96 bytes (training/training_dynamic/config.h:78-86,
+ * read by generate.m:212-248): magic 'BLZT', version 4, training counters,
+ * model shape (with the GQA fields kv_heads, head_dim, q_dim in version 4). */
+typedef struct {
+    int32_t magic, version, step, total_steps;
+    int32_t n_layers, vocab_size, dim, hidden_dim, n_heads, seq_len;
+    float lr, loss;
+    double cum_compile, cum_train, cum_wall;
+    int32_t cum_steps, cum_batches, adam_t;
+    int32_t kv_heads, head_dim, q_dim;
+} BlztHeader;
+
+#define BLZT_MAGIC 0x424C5A54
+
+static int read_f32(FILE *f, float *dst, size_t n)
+{
+    return fread(dst, sizeof(float), n, f) == n ? LM_OK : LM_ERR_FORMAT;
+}
+
+static int skip_f32(FILE *f, size_t n)
+{
+    /* long is 64-bit on the LP64 hosts this builds for */
+    return fseek(f, (long)(n * sizeof(float)), SEEK_CUR) == 0 ? LM_OK : LM_ERR_FORMAT;
+}
+
+/* Weights of a BLZT v4 file into a llama2.c-ordered fp32 buffer (tied
+ * classifier: the embedding).  Per layer the file holds Wq, Wk, Wv, Wo, W1,
+ * W2, W3, rms_att, rms_ffn followed by the Adam m and v of each; then
+ * rms_final (+ Adam) and the embedding (generate.m:228-246). */
+int lmh_read_blzt(const char *path, Config *cfg, float **data)
+{
+    *data = NULL;
+    FILE *f = fopen(path, "rb");
+    if (!f) {
+        fprintf(stderr, "lm_load_blzt: cannot open %s\n", path);
+        return LM_ERR_IO;
+    }
+    BlztHeader h;
+    if (fread(&h, sizeof(h), 1, f) != 1 || h.magic != BLZT_MAGIC || h.version != 4) {
+        fprintf(stderr, "lm_load_blzt: %s is not a BLZT version 4 checkpoint\n", path);
+        fclose(f);
+        return LM_ERR_FORMAT;
+    }
+    Config c;
+    c.dim = h.dim;
+    c.hidden_dim = h.hidden_dim;
+    c.n_layers = h.n_layers;
+    c.n_heads = h.n_heads;
+    c.n_kv_heads = h.kv_heads > 0 ? h.kv_heads : h.n_heads;
+    c.vocab_size = h.vocab_size;
+    c.seq_len = h.seq_len;
+    const int hd = h.head_dim > 0 ? h.head_dim : (h.n_heads > 0 ? h.dim / h.n_heads : 0);
+    const int qd = h.q_dim > 0 ? h.q_dim : h.n_heads * hd;
+    if (lmh_check_config(&c) || c.vocab_size < 1 || qd != c.dim || hd * c.n_heads != c.dim) {
+        fprintf(stderr, "lm_load_blzt: unsupported shape in %s (dim=%d heads=%d head_dim=%d "
+                "q_dim=%d kv_heads=%d vocab=%d): this loop needs q_dim == dim\n",
+                path, h.dim, h.n_heads, hd, qd, c.n_kv_heads, h.vocab_size);
+        fclose(f);
+        return LM_ERR_FORMAT;
+    }
+    size_t sz[LMH_NTENSORS];
+    lmh_tensor_sizes(&c, 0, sz);
+    const size_t L = (size_t)c.n_layers, D = (size_t)c.dim;
+    const size_t wq = sz[LMH_T_WQ] / L, wk = sz[LMH_T_WK] / L, wv = sz[LMH_T_WV] / L;
+    const size_t wo = sz[LMH_T_WO] / L, w1 = sz[LMH_T_W1] / L, w2 = sz[LMH_T_W2] / L;
+    const size_t w3 = sz[LMH_T_W3] / L;
+    float *buf = (float *)malloc(lm_weights_numel(&c, 0) * sizeof(float));
+    if (!buf) {
+        fclose(f);
+        return LM_ERR_OOM;
+    }
+    LMWeights w;
+    lm_weights_view(&c, LM_DTYPE_F32, buf, 0, &w);
+    float *emb = (float *)w.token_embedding, *ra = (float *)w.rms_att_w, *rf = (float *)w.rms_ffn_w;
+    float *q = (float *)w.wq, *k = (float *)w.wk, *v = (float *)w.wv, *o = (float *)w.wo;
+    float *p1 = (float *)w.w1, *p2 = (float *)w.w2, *p3 = (float *)w.w3, *fin = (float *)w.rms_final_w;
+    int rc = LM_OK;
+    for (size_t l = 0; l < L && rc == LM_OK; l++) {
+        rc = read_f32(f, q + l * wq, wq);
+        if (!rc) rc = read_f32(f, k + l * wk, wk);
+        if (!rc) rc = read_f32(f, v + l * wv, wv);
+        if (!rc) rc = read_f32(f, o + l * wo, wo);
+        if (!rc) rc = read_f32(f, p1 + l * w1, w1);
+        if (!rc) rc = read_f32(f, p2 + l * w2, w2);
+        if (!rc) rc = read_f32(f, p3 + l * w3, w3);
+        if (!rc) rc = read_f32(f, ra + l * D, D);
+        if (!rc) rc = read_f32(f, rf + l * D, D);
+        if (!rc) rc = skip_f32(f, 2 * (wq + wk + wv + wo + w1 + w2 + w3 + 2 * D));
+    }
+    if (!rc) rc = read_f32(f, fin, D);
+    if (!rc) rc = skip_f32(f, 2 * D);
+    if (!rc) rc = read_f32(f, emb, (size_t)c.vocab_size * D);
+    fclose(f);
+    if (rc) {
+        fprintf(stderr, "lm_load_blzt: %s is truncated\n", path);
+        free(buf);
+        return rc;
+    }
+    *cfg = c;
+    *data = buf;
+    return LM_OK;
+}
+
+int lm_blzt_to_llama2c(const char *blzt_path, const char *out_path)
+{
+    if (!blzt_path || !out_path) return LM_ERR_INVALID;
+    Config c;
+    float *data = NULL;
+    int rc = lmh_read_blzt(blzt_path, &c, &data);
+    if (rc) return rc;
+    LMWeights w;
+    lm_weights_view(&c, LM_DTYPE_F32, data, 0, &w);
+    rc = lm_write_llama2c(out_path, &c, &w);
+    free(data);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------- */
 /* RoPE table                                                                 */
 /* ------------------------------------------------------------------------- */
 

@@ -61,6 +61,71 @@ class LMDeviceInfo(C.Structure):
                 ("clock_khz", C.c_int), ("l2_bytes", C.c_int), ("total_mem", C.c_size_t)]
 
 
+class GenConfig(C.Structure):
+    """ANEGenConfig (ane_gen.h)."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("max_tokens", C.c_int),
+                ("seed", C.c_uint64)]
+
+
+class GenResult(C.Structure):
+    """ANEGenResult (ane_gen.h)."""
+    _fields_ = [("text", C.c_void_p), ("tokens_generated", C.c_int), ("total_ms", C.c_double),
+                ("ms_per_token", C.c_double), ("stop_reason", C.c_int)]
+
+
+GenTokenFn = C.CFUNCTYPE(C.c_bool, C.c_char_p, C.c_int, C.c_void_p)
+GEN_STOP_EOS, GEN_STOP_MAX, GEN_STOP_CALLBACK, GEN_STOP_ERROR = 0, 1, 2, 3
+
+
+class GenSession:
+    """ANEGenSession: text generation from a checkpoint (BLZT v4 or llama2.c)
+    and a llama2.c tokenizer."""
+
+    def __init__(self, checkpoint: str, tokenizer: str):
+        err = C.c_int(0)
+        self._h = lib().ane_gen_create(checkpoint.encode(), tokenizer.encode(), C.byref(err))
+        if not self._h:
+            raise LMError(-err.value - 100,
+                          "ane_gen_create: " + lib().ane_train_error_str(err.value).decode())
+
+    def run(self, prompt, temperature=0.8, top_p=0.9, max_tokens=256, seed=0, on_token=None):
+        """Returns (text bytes, tokens_generated, stop_reason, ms_per_token, ids
+        seen by the callback)."""
+        cfg = GenConfig(temperature, top_p, max_tokens, seed)
+        ids = []
+
+        def cb(piece, tok, ctx):
+            ids.append(tok)
+            return bool(on_token(piece, tok)) if on_token else True
+
+        fn = GenTokenFn(cb)
+        res = lib().ane_gen_run(self._h, prompt.encode() if isinstance(prompt, str) else prompt,
+                                C.byref(cfg), fn, None)
+        text = C.string_at(res.text) if res.text else b""
+        out = (text, res.tokens_generated, res.stop_reason, res.ms_per_token, ids)
+        lib().ane_gen_result_free(C.byref(res))
+        return out
+
+    def close(self):
+        if self._h:
+            lib().ane_gen_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+def gen_default_config():
+    c = lib().ane_gen_default_config()
+    return dict(temperature=c.temperature, top_p=c.top_p, max_tokens=c.max_tokens, seed=c.seed)
+
+
+def blzt_to_llama2c(blzt_path: str, out_path: str):
+    rc = lib().lm_blzt_to_llama2c(blzt_path.encode(), out_path.encode())
+    if rc:
+        raise LMError(rc, "lm_blzt_to_llama2c")
+
+
 class Rng(C.Structure):
     """drand48-recurrence random stream (LMRng)."""
     _fields_ = [("x", C.c_uint64)]
@@ -186,6 +251,14 @@ def lib():
         "lm_sample_argmax": (I, [fp, I]),
         "lm_sample_temperature": (I, [fp, I, F, C.POINTER(Rng)]),
         "lm_sample_topp": (I, [fp, I, F, F, C.POINTER(Rng)]),
+        "lm_load_blzt": (P, [C.c_char_p, I, I, ip]),
+        "lm_blzt_to_llama2c": (I, [C.c_char_p, C.c_char_p]),
+        "ane_train_error_str": (C.c_char_p, [I]),
+        "ane_gen_default_config": (GenConfig, []),
+        "ane_gen_create": (P, [C.c_char_p, C.c_char_p, ip]),
+        "ane_gen_run": (GenResult, [P, C.c_char_p, C.POINTER(GenConfig), GenTokenFn, P]),
+        "ane_gen_result_free": (None, [C.POINTER(GenResult)]),
+        "ane_gen_destroy": (None, [P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -356,6 +429,16 @@ class Model:
         self._h = handle
         self.cfg = cfg
         self.vocab = abs(cfg.vocab_size)
+
+    @classmethod
+    def load_blzt(cls, path: str, max_batch: int, max_seq: int):
+        st = C.c_int(0)
+        h = lib().lm_load_blzt(path.encode(), max_batch, max_seq, C.byref(st))
+        if not h:
+            raise LMError(st.value, "lm_load_blzt")
+        cfg = Config()
+        lib().lm_get_config(h, C.byref(cfg))
+        return cls(h, cfg)
 
     @classmethod
     def create(cls, cfg: Config, weights: np.ndarray, untied: bool, max_batch: int, max_seq: int):

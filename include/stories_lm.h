@@ -124,6 +124,17 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch,
 LMModel *lm_load_llama2c(const char *path, int max_batch, int max_seq,
                          int *status);
 
+/* Read a BLZT version 4 training checkpoint (the reference's format:
+ * load_gen_checkpoint, training/training_dynamic/generate.m:212-248; header
+ * config.h:78-86) and lm_create it: the weights are read, the Adam state is
+ * skipped, the classifier is the embedding.  Shapes with q_dim != dim fail
+ * with LM_ERR_FORMAT. */
+LMModel *lm_load_blzt(const char *path, int max_batch, int max_seq, int *status);
+
+/* Host only: rewrite a BLZT v4 checkpoint's weights as a llama2.c file (tied
+ * classifier). */
+int lm_blzt_to_llama2c(const char *blzt_path, const char *out_path);
+
 /* Release every host and device resource of the handle.  NULL is a no-op. */
 void lm_free(LMModel *m);
 
