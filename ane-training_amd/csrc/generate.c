@@ -10,13 +10,20 @@
  *
  *   stories_generate [--ckpt model.bin | --synth SEED] [--steps N]
  *                    [--first TOKEN] [--stepwise] [--print]
+ *   stories_generate --ckpt model --tokenizer tokenizer.bin [--prompt TEXT]
+ *                    [--temp T] [--topp P] [--seed S] [--steps N]
  *
- * --ckpt     llama2.c model file (training/model.h:78-164 layout)
- * --synth    seeded N(0, 0.02) fp16 Stories-110M weights (untied classifier)
- * --stepwise one lm_forward call per token with the argmax taken on the host
- *            (the loop shape of generate.m); default: lm_generate_greedy, which
- *            keeps the argmax feedback on the device
+ * --ckpt      llama2.c model file (training/model.h:78-164 layout), or with
+ *             --tokenizer also a BLZT v4 checkpoint
+ * --synth     seeded N(0, 0.02) fp16 Stories-110M weights (untied classifier)
+ * --stepwise  one lm_forward call per token with the argmax taken on the host
+ *             (the loop shape of generate.m); default: lm_generate_greedy, which
+ *             keeps the argmax feedback on the device
+ * --tokenizer text mode through the generation session (ane_gen.h): prompt,
+ *             sampling (temperature / top-p, generate.m:488-497) and streamed
+ *             text, as generate.m prints it
  */
+#include "ane_gen.h"
 #include "stories_lm.h"
 
 #include <stdint.h>
@@ -40,25 +47,74 @@ static int argmax_first(const float *v, int n)
     return best;
 }
 
+static bool print_piece(const char *piece, int id, void *ctx)
+{
+    (void)id;
+    (void)ctx;
+    fputs(piece, stdout);
+    fflush(stdout);
+    return true;
+}
+
+static int run_text(const char *ckpt, const char *tokenizer, const char *prompt, float temp,
+                    float topp, unsigned long long seed, int steps)
+{
+    ANETrainError err;
+    ANEGenSession *g = ane_gen_create(ckpt, tokenizer, &err);
+    if (!g) {
+        fprintf(stderr, "ane_gen_create: %s\n", ane_train_error_str(err));
+        return 1;
+    }
+    ANEGenConfig cfg = ane_gen_default_config();
+    cfg.temperature = temp;
+    cfg.top_p = topp;
+    cfg.max_tokens = steps;
+    cfg.seed = seed;
+    if (prompt) fputs(prompt, stdout);
+    ANEGenResult r = ane_gen_run(g, prompt, &cfg, print_piece, NULL);
+    static const char *why[] = {"EOS", "max tokens", "callback", "error"};
+    printf("\n%d tokens, %.3f ms/token, %.1f tok/s (stop: %s)\n", r.tokens_generated, r.ms_per_token,
+           r.ms_per_token > 0 ? 1e3 / r.ms_per_token : 0.0, why[r.stop_reason & 3]);
+    const int rc = r.stop_reason == ANE_GEN_STOP_ERROR;
+    ane_gen_result_free(&r);
+    ane_gen_destroy(g);
+    return rc;
+}
+
 int main(int argc, char **argv)
 {
-    const char *ckpt = NULL;
+    const char *ckpt = NULL, *tokenizer = NULL, *prompt = NULL;
     unsigned long long seed = 1;
     int steps = 256, first = 1, stepwise = 0, print = 0;
+    float temp = 0.8f, topp = 0.9f;
     for (int i = 1; i < argc; i++) {
         if (!strcmp(argv[i], "--ckpt") && i + 1 < argc) ckpt = argv[++i];
         else if (!strcmp(argv[i], "--synth") && i + 1 < argc) seed = strtoull(argv[++i], NULL, 10);
+        else if (!strcmp(argv[i], "--seed") && i + 1 < argc) seed = strtoull(argv[++i], NULL, 10);
         else if (!strcmp(argv[i], "--steps") && i + 1 < argc) steps = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--first") && i + 1 < argc) first = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--tokenizer") && i + 1 < argc) tokenizer = argv[++i];
+        else if (!strcmp(argv[i], "--prompt") && i + 1 < argc) prompt = argv[++i];
+        else if (!strcmp(argv[i], "--temp") && i + 1 < argc) temp = (float)atof(argv[++i]);
+        else if (!strcmp(argv[i], "--topp") && i + 1 < argc) topp = (float)atof(argv[++i]);
         else if (!strcmp(argv[i], "--stepwise")) stepwise = 1;
         else if (!strcmp(argv[i], "--print")) print = 1;
         else {
             fprintf(stderr, "usage: %s [--ckpt model.bin | --synth SEED] [--steps N] "
-                            "[--first TOKEN] [--stepwise] [--print]\n", argv[0]);
+                            "[--first TOKEN] [--stepwise] [--print]\n"
+                            "       %s --ckpt model --tokenizer tokenizer.bin [--prompt TEXT] "
+                            "[--temp T] [--topp P] [--seed S] [--steps N]\n", argv[0], argv[0]);
             return 2;
         }
     }
     if (steps < 1) return 2;
+    if (tokenizer) {
+        if (!ckpt) {
+            fprintf(stderr, "--tokenizer needs --ckpt\n");
+            return 2;
+        }
+        return run_text(ckpt, tokenizer, prompt, temp, topp, seed, steps);
+    }
     int rc = lm_init();
     if (rc) {
         fprintf(stderr, "lm_init: %s\n", lm_strerror(rc));
