@@ -10,6 +10,7 @@ PKG = os.path.join(ROOT, "ane-training_amd")
 sys.path.insert(0, PKG)
 
 import check_lds_asm  # noqa: E402
+import pytest  # noqa: E402
 
 HEAD = "_Z11k_gemm_tileILi64ELi64ELi0EEvPKtiS1_i7EpiArgsii:\n"
 TAIL = ".Lfunc_end0:\n"
@@ -39,6 +40,9 @@ def test_passes_use_after_wait_and_unrelated_work():
     assert len(names) == 1 and not bad
 
 
+@pytest.mark.skipif(os.path.exists("/dev/kfd"),
+                    reason="build check: runs where the library is built, not on a GPU host "
+                           "(no child processes next to an initialised GPU)")
 def test_library_assembly_is_clean():
     r = subprocess.run(["make", "-C", PKG, "check"], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout + r.stderr

@@ -133,22 +133,3 @@ def test_gen_sampling_is_seeded_and_callback_stops(lm, tmp_path):
     assert n == 0 and ids == [] and stop == lm.GEN_STOP_EOS
     g.close()
 
-
-def test_cli_text_mode(lm, tmp_path):
-    """stories_generate --tokenizer: the session behind the command-line driver."""
-    import subprocess
-    _say("[cli text mode]")
-    d = dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=4, vocab_size=512, seq_len=64)
-    mpath, tpath, _ = _model_files(lm, tmp_path, d, 33)
-    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "ane-training_amd",
-                       "stories_generate")
-    r = subprocess.run([exe, "--ckpt", mpath, "--tokenizer", tpath, "--prompt", "ab ba", "--temp", "0",
-                        "--steps", "12"], capture_output=True, text=True, timeout=120)
-    assert r.returncode == 0, r.stderr
-    last = r.stdout.strip().splitlines()[-1]
-    assert "ms/token" in last and "stop:" in last
-    g = lm.GenSession(mpath, tpath)
-    text, n, stop, _, _ = g.run("ab ba", temperature=0.0, max_tokens=12)
-    g.close()
-    assert r.stdout.startswith("ab ba")
-    assert last.startswith(f"{n} tokens")
