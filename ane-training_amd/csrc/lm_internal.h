@@ -77,6 +77,16 @@ int lmk_ffn13(hipStream_t s, float *x, const float *rms_w,
 int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
                     int F, int B, float *x, const float *part, int nh);
 
+/* Decode rows after a K-split QKV GEMM: attention of head h, row b with q, k,
+ * v summed from the ns partials part[s][b][..] (sstride floats apart) and
+ * RoPE'd at pos[b]; k, v appended to the cache at (slot[b], pos[b]); the head
+ * output to out16[b, h*hd ..] (fp16).  Replaces lmk_qkv_post + lmk_attn_decode
+ * for decode rows. */
+int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int ns, int NQ, int NKV,
+                         const int *pos, const int *slot, int B, int H, int Hkv, int hd,
+                         int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
+                         void *vc, int kv_f32, uint16_t *out16);
+
 /* Attention of head h, row b, fused with that head's share of Wo:
  * part[(b*H + h)*D + r] = Wo[r, h*hd .. +hd] . attn(b, h) (D = H*hd, slot b =
  * row b).  Only for shapes lmk_attn_wo_supported accepts (the Wo head block

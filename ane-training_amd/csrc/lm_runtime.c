@@ -656,6 +656,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                          m->d_rms_att + (size_t)l * D, m->d_xn16));
         pend = NULL;
         pend_ns = 0;
+        int attn_done = 0;   /* attention already ran (fused with the QKV partials) */
         memset(&ep, 0, sizeof(ep));
         if (!dec) {
             /* prefill rows: plain fp32 QKV rows, then a coalesced RoPE + append pass */
@@ -665,9 +666,18 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                               m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc, m->kv_f32));
         } else if (ns_qkv > 1) {
             KCHK(lmk_gemm_split(s, m->d_xn16, D, lw, M, NQKV, D, ns_qkv, m->d_part));
-            KCHK(lmk_qkv_post(s, m->d_part, ns_qkv, (size_t)M * NQKV, M, NQ, NKV, m->hd, m->Hkv,
-                              m->max_seq, pos, slot, m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc,
-                              m->kv_f32));
+            if (seq_rows == 1) {
+                /* decode rows: the attention kernel sums the partials, applies
+                 * RoPE and appends K/V itself */
+                KCHK(lmk_attn_decode_part(s, m->d_part, (size_t)M * NQKV, ns_qkv, NQ, NKV, pos, slot,
+                                          M, m->H, m->Hkv, m->hd, m->max_seq, m->d_rope_cos,
+                                          m->d_rope_sin, kc, vc, m->kv_f32, m->d_a16));
+                attn_done = 1;
+            } else {
+                KCHK(lmk_qkv_post(s, m->d_part, ns_qkv, (size_t)M * NQKV, M, NQ, NKV, m->hd,
+                                  m->Hkv, m->max_seq, pos, slot, m->d_rope_cos, m->d_rope_sin,
+                                  m->d_q, kc, vc, m->kv_f32));
+            }
         } else {
             /* wide enough unsplit: RoPE and the append fused into the GEMM epilogue */
             ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
@@ -675,12 +685,14 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
             KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
         }
-        if (seq_rows > 1)
+        if (attn_done) {
+        } else if (seq_rows > 1) {
             KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
                                   M / seq_rows, m->H, m->Hkv, m->hd, m->max_seq, m->d_a16));
-        else
+        } else {
             KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
                                  m->max_seq, NULL, m->d_a16));
+        }
         if (sep_wo) {
             if (ns_wo > 1) {
                 KCHK(lmk_gemm_split(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, ns_wo, m->d_part));
