@@ -2,32 +2,36 @@
  * k_attn.hip — causal prefill attention on MFMA (gfx950).
  *
  * Rows of a prefill chunk come in whole sequences of S consecutive rows with
- * consecutive positions.  Work-group (query block, head) takes 128 query rows of
- * one sequence; each of its four waves owns 32 of them.  Keys are visited in
- * tiles of 64 positions, 0 .. (last query position of the block); for each tile
- * (forward.h:72-99, restated as an online softmax):
- *   S^T = K Q^T * (1/sqrt(hd))  32x32x16 f16 MFMAs, fp32 accumulation; keys after
- *                               the query's position are masked (-inf)
- *   m' = max(m, max_key S); P = exp(S - m'); l = l*exp(m - m') + sum_key P;
- *   O^T = O^T*exp(m - m') + V^T P^T   P and V rounded to fp16 for the MFMA
- * and finally out = O / l, in fp16 (the operand of the Wo GEMM).
+ * consecutive positions.  Work-group (query block, head) takes 32 query rows of
+ * one sequence; its four waves split the key tiles (64 positions each) of
+ * 0 .. (last query position of the block) round-robin, wave w taking tiles
+ * w, w+4, ..., so the block waits for about one tile's load instead of all of
+ * them.  For each of its tiles a wave computes (forward.h:72-99, restated as an
+ * online softmax, scores in log2 units):
+ *   S^T = K Q^T * (log2 e / sqrt(hd))   32x32x16 f16 MFMAs, fp32 accumulation;
+ *                                       keys after the query's position masked
+ *   m' = max(m, max_key S); P = 2^(S - m'); l = l*2^(m - m') + sum_key P;
+ *   O^T = O^T*2^(m - m') + V^T P^T      P and V rounded to fp16 for the MFMA
+ * and the four waves' (m, l, O) merge through LDS into out = O / l (fp16, the
+ * operand of the Wo GEMM).
  *
  * Computing the transposed scores puts one query in each accumulator column, so
  * lane l holds 32 of the tile's 64 scores of query l % 32 (lane l ^ 32 the other
  * 32): the softmax needs one cross-lane exchange per tile, and the accumulator
  * already has the layout of the B operand of the V^T P^T product, up to an order
  * of the 16 keys of each MFMA step.  That order is undone by storing V^T in LDS
- * with bits 2 and 3 of the key index swapped.  K and V^T of tile t+2 are fetched
- * into registers while tile t computes, and tile t+1 is stored into the other of
- * two LDS buffers.
+ * with bits 2 and 3 of the key index swapped.  Each wave stages its own tiles in
+ * its own LDS region; at hd 64 with an fp16 cache it fetches its next tile into
+ * registers while the current one computes.
  */
 #include "k_common.h"
 #include "lm_internal.h"
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define AT 256          /* threads per work-group */
-#define BQ 128          /* query rows per work-group */
+#define AT 256          /* threads per work-group (4 waves) */
+#define NW 4            /* waves per work-group */
+#define BQ 32           /* query rows per work-group */
 #define BKV 64          /* keys per tile */
 
 __device__ __forceinline__ f32x16 mfma32h(uint4 a, uint4 b, f32x16 c)
@@ -62,10 +66,13 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     constexpr int VLD = BKV + 8;         /* V^T tile row stride (halves) */
     constexpr int KS = HD / 16;          /* MFMA k-steps over head dims  */
     constexpr int DT = HD / 32;          /* 32-dim row tiles of O^T      */
-    constexpr int CPT = BKV * HD / 8 / AT;   /* 16-byte chunks per thread per array */
-    static_assert(CPT >= 1 && BKV * HD / 8 % AT == 0, "staging shape");
-    __shared__ __attribute__((aligned(16))) u16 sk[2][BKV * KLD];
-    __shared__ __attribute__((aligned(16))) u16 svt[2][HD * VLD];
+    constexpr int CPL = BKV * HD / 8 / 64;   /* 16-byte chunks per lane per array (one wave stages a tile) */
+    constexpr bool PREF = HD == 64 && sizeof(KT) == 2;   /* next tile in registers */
+    constexpr int STAGE = BKV * KLD + HD * VLD;          /* halves of one wave's K and V^T */
+    static_assert(BKV * HD / 8 % 256 == 0, "staging shape");
+    constexpr int MLD = HD + 1;                          /* merge row stride (floats) */
+    static_assert(NW * STAGE * 2 >= (NW * BQ * MLD + 2 * NW * BQ) * 4, "merge area fits the staging area");
+    __shared__ __attribute__((aligned(16))) u16 stg[NW * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -80,45 +87,54 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     const size_t cbase = ((size_t)cs * Hkv + kvh) * max_seq * HD;
     /* scores are kept in log2 units: exp(x) = exp2(x * log2 e) */
     const float scale = 1.4426950408889634f / sqrtf((float)HD);
-
     const int last_pos = p0 + nrows - 1;          /* last query position of the block */
     const int ntiles = last_pos / BKV + 1;
+    u16 *sk = stg + wave * STAGE, *svt = sk + BKV * KLD;
 
-    /* K / V chunks of one tile: chunk c = tid + i*AT is key c / (HD/8), dims
-     * (c % (HD/8))*8 .. +8; keys past the block's last position repeat it (they
-     * are masked for every query that reads them) */
-    /* two register sets: tile t sits in set t % 2 from its fetch (two tiles
-     * ahead of its use) until it is stored to LDS (one tile ahead) */
-    uint4 rk0[CPT], rv0[CPT], rk1[CPT], rv1[CPT];
-    auto fetch = [&](int kt, uint4 (&rk)[CPT], uint4 (&rv)[CPT]) {
+    /* K / V chunks of one tile for this wave: chunk c = lane + i*64 is key
+     * c / (HD/8), dims (c % (HD/8))*8 .. +8; keys past the block's last
+     * position repeat it (masked for every query that reads them) */
+    auto load = [&](int kt, int i, uint4 &k8, uint4 &v8) {
+        const int c = lane + i * 64, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+        const size_t off = cbase + (size_t)min(kt * BKV + key, last_pos) * HD + d0;
+        k8 = kv8_f16(kc + off);
+        v8 = kv8_f16(vc + off);
+    };
+    auto put = [&](int i, uint4 k8, uint4 v8) {
+        const int c = lane + i * 64, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+        *(uint4 *)(&sk[key * KLD + d0]) = k8;
+        const unsigned vw[4] = {v8.x, v8.y, v8.z, v8.w};
+        const int pk = vperm(key);
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-            const size_t off = cbase + (size_t)min(kt * BKV + key, last_pos) * HD + d0;
-            rk[i] = kv8_f16(kc + off);
-            rv[i] = kv8_f16(vc + off);
+        for (int j = 0; j < 8; j++) svt[(d0 + j) * VLD + pk] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
+    };
+    /* hd 64 with an fp16 cache: the whole next tile is held in registers while
+     * the current one computes; otherwise a tile is staged 4 chunks at a time */
+    constexpr int RC = PREF ? CPL : 1;
+    uint4 rk[RC], rv[RC];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < RC; i++) load(kt, i, rk[i], rv[i]);
+    };
+    auto stage = [&](int kt) {
+        if constexpr (PREF) {
+#pragma unroll
+            for (int i = 0; i < CPL; i++) put(i, rk[i], rv[i]);
+        } else {
+#pragma unroll
+            for (int i0 = 0; i0 < CPL; i0 += 4) {
+                uint4 k4[4], v4[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) load(kt, i0 + i, k4[i], v4[i]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) put(i0 + i, k4[i], v4[i]);
+            }
         }
     };
-    auto stash = [&](int b, const uint4 (&rk)[CPT], const uint4 (&rv)[CPT]) {
-#pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-            *(uint4 *)(&sk[b][key * KLD + d0]) = rk[i];
-            const unsigned vw[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
-            const int pk = vperm(key);
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                svt[b][(d0 + j) * VLD + pk] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
-        }
-    };
-    fetch(0, rk0, rv0);
-    fetch(1, rk1, rv1);   /* past the last tile: the last position again, unused */
+    if (PREF && wave < ntiles) fetch(wave);       /* wave-uniform */
 
-    /* this wave's queries: block rows wr0 .. wr0+31; lane l takes row wr0 + l%32 */
-    const int wr0 = wave * 32;
-    const bool wave_active = wr0 < nrows;
-    const int wave_last = p0 + min(wr0 + 31, nrows - 1);
-    const int qrow = wr0 + (lane & 31);
+    /* lane l takes query row l%32 of the block */
+    const int qrow = lane & 31;
     const int qp = p0 + qrow;                     /* this lane's query position */
     /* Q^T fragments (B operand): query l%32, dims ks*16 + 8*(l/32) .. +8 */
     uint4 qb16[KS];
@@ -132,99 +148,113 @@ __global__ void __launch_bounds__(AT) k_attn_prefill(
     for (int j = 0; j < DT; j++) o[j] = (f32x16){};
     float mrow = -INFINITY, lrow = 0.f;
 
-    stash(0, rk0, rv0);
-    __syncthreads();
-    /* tile kt: fetch tile kt+2 into the set tile kt left (unconditionally, so
-     * the compiler waits only for the older set), compute kt, store kt+1 */
-    auto body = [&](int kt, uint4 (&rka)[CPT], uint4 (&rva)[CPT], const uint4 (&rkb)[CPT],
-                    const uint4 (&rvb)[CPT]) {
-        const int b = kt & 1;
-        fetch(kt + 2, rka, rva);
+    for (int kt = wave; kt < ntiles; kt += NW) {  /* wave-uniform */
+        stage(kt);
+        __builtin_amdgcn_s_waitcnt(0xc07f);       /* lgkmcnt(0): the wave's LDS writes landed */
+        __builtin_amdgcn_wave_barrier();
+        if (PREF && kt + NW < ntiles) fetch(kt + NW);
         const int k0 = kt * BKV;
-        if (wave_active && k0 <= wave_last) {     /* wave-uniform */
-            const u16 *K = sk[b], *VT = svt[b];
-            /* S^T tiles: rows = keys nt*32 + (0..31), columns = the wave's queries */
-            f32x16 sacc[2];
+        /* S^T tiles: rows = keys nt*32 + (0..31), columns = the block's queries */
+        f32x16 sacc[2];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                sacc[nt] = (f32x16){};
+        for (int nt = 0; nt < 2; nt++) {
+            sacc[nt] = (f32x16){};
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    const uint4 ka = *(const uint4 *)(&K[(nt * 32 + (lane & 31)) * KLD + ks * 16 + g * 8]);
-                    sacc[nt] = mfma32h(ka, qb16[ks], sacc[nt]);
-                }
+            for (int ks = 0; ks < KS; ks++) {
+                const uint4 ka = *(const uint4 *)(&sk[(nt * 32 + (lane & 31)) * KLD + ks * 16 + g * 8]);
+                sacc[nt] = mfma32h(ka, qb16[ks], sacc[nt]);
             }
-            /* element i of tile nt is key k0 + nt*32 + 8*(i/4) + 4*g + i%4 */
-            float mx = -INFINITY;
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int key = k0 + nt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                    const float v = key > qp ? -INFINITY : sacc[nt][i] * scale;
-                    sacc[nt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
-            mx = fmaxf(mx, xor32_f(mx));
-            const float mn = fmaxf(mrow, mx);
-            /* a query with every key so far masked keeps m = -inf: nothing to scale */
-            const float corr = mn == -INFINITY ? 1.f : exp2f(mrow - mn);
-            const float sub = mn == -INFINITY ? 0.f : mn;
-            float ls = 0.f;
-            uint4 pb[2][2];
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    f16x8 hv;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float e = exp2f(sacc[nt][8 * hh + j] - sub);
-                        ls += e;
-                        hv[j] = (_Float16)e;
-                    }
-                    pb[nt][hh] = __builtin_bit_cast(uint4, hv);
-                }
-            lrow = lrow * corr + ls;               /* per-lane partial row sum */
-            mrow = mn;
-#pragma unroll
-            for (int j = 0; j < DT; j++) o[j] *= corr;
-            /* O^T += V^T P^T over the 4 steps of 16 keys */
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-                    for (int j = 0; j < DT; j++) {
-                        const uint4 va = *(const uint4 *)(&VT[(j * 32 + (lane & 31)) * VLD + nt * 32 +
-                                                              hh * 16 + g * 8]);
-                        o[j] = mfma32h(va, pb[nt][hh], o[j]);
-                    }
         }
-        if (kt + 1 < ntiles) stash(b ^ 1, rkb, rvb);
-        __syncthreads();
-    };
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        body(kt, rk0, rv0, rk1, rv1);
-        if (kt + 1 < ntiles) body(kt + 1, rk1, rv1, rk0, rv0);
-    }
-    if (!wave_active) return;
-    /* finish the row sum across the lane pair and write O / l:
-     * element i of o[j] is dim j*32 + 8*(i/4) + 4*g + i%4 of query l%32 */
-    const float l = lrow + xor32_f(lrow);
-    if (qrow < nrows) {
-        const float inv = 1.0f / l;
-        u16 *op = out + (size_t)(row0 + qrow) * NQ + h * HD;
+        /* element i of tile nt is key k0 + nt*32 + 8*(i/4) + 4*g + i%4 */
+        float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < DT; j++)
+        for (int nt = 0; nt < 2; nt++)
 #pragma unroll
-            for (int i4 = 0; i4 < 4; i4++) {
-                const unsigned lo = (unsigned)f2h(o[j][4 * i4] * inv) |
-                                    ((unsigned)f2h(o[j][4 * i4 + 1] * inv) << 16);
-                const unsigned hi = (unsigned)f2h(o[j][4 * i4 + 2] * inv) |
-                                    ((unsigned)f2h(o[j][4 * i4 + 3] * inv) << 16);
-                *(uint2 *)(op + j * 32 + 8 * i4 + 4 * g) = make_uint2(lo, hi);
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + nt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                const float v = key > qp ? -INFINITY : sacc[nt][i] * scale;
+                sacc[nt][i] = v;
+                mx = fmaxf(mx, v);
             }
+        mx = fmaxf(mx, xor32_f(mx));
+        const float mn = fmaxf(mrow, mx);
+        /* a query with every key so far masked keeps m = -inf: nothing to scale */
+        const float corr = mn == -INFINITY ? 1.f : exp2f(mrow - mn);
+        const float sub = mn == -INFINITY ? 0.f : mn;
+        float ls = 0.f;
+        uint4 pb[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                f16x8 hv;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float e = exp2f(sacc[nt][8 * hh + j] - sub);
+                    ls += e;
+                    hv[j] = (_Float16)e;
+                }
+                pb[nt][hh] = __builtin_bit_cast(uint4, hv);
+            }
+        lrow = lrow * corr + ls;                   /* per-lane partial row sum */
+        mrow = mn;
+#pragma unroll
+        for (int j = 0; j < DT; j++) o[j] *= corr;
+        /* O^T += V^T P^T over the 4 steps of 16 keys */
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int j = 0; j < DT; j++) {
+                    const uint4 va = *(const uint4 *)(&svt[(j * 32 + (lane & 31)) * VLD + nt * 32 +
+                                                           hh * 16 + g * 8]);
+                    o[j] = mfma32h(va, pb[nt][hh], o[j]);
+                }
+        __builtin_amdgcn_wave_barrier();           /* the tile's reads precede the next stash */
+    }
+    /* merge the four waves: each writes (m, l, O) of its 32 queries; element i of
+     * o[j] is dim j*32 + 8*(i/4) + 4*g + i%4 of query l%32 */
+    const float lsum = lrow + xor32_f(lrow);
+    __syncthreads();                               /* every wave is done with its staging area */
+    float *mo = (float *)stg;                      /* [NW][BQ][MLD] outputs */
+    float *mm = mo + NW * BQ * MLD, *ml = mm + NW * BQ;
+    if (g == 0) {
+        mm[wave * BQ + qrow] = mrow;
+        ml[wave * BQ + qrow] = lsum;
+    }
+#pragma unroll
+    for (int j = 0; j < DT; j++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            mo[(wave * BQ + qrow) * MLD + j * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[j][i];
+    __syncthreads();
+    /* thread t: query t / 8, dims (t % 8) * HD/8 .. +HD/8 */
+    constexpr int DPT = HD / 8;
+    const int r = tid >> 3, d0 = (tid & 7) * DPT;
+    if (r < nrows) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mm[w * BQ + r]);
+        float wgt[NW], L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = mm[w * BQ + r];
+            wgt[w] = mw == -INFINITY ? 0.f : exp2f(mw - M);
+            L = fmaf(ml[w * BQ + r], wgt[w], L);
+        }
+        const float inv = 1.0f / L;
+        u16 *op = out + (size_t)(row0 + r) * NQ + h * HD + d0;
+#pragma unroll
+        for (int d = 0; d < DPT; d += 2) {
+            float a = 0.f, bsum = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                a = fmaf(mo[(w * BQ + r) * MLD + d0 + d], wgt[w], a);
+                bsum = fmaf(mo[(w * BQ + r) * MLD + d0 + d + 1], wgt[w], bsum);
+            }
+            *(unsigned *)(op + d) = (unsigned)f2h(a * inv) | ((unsigned)f2h(bsum * inv) << 16);
+        }
     }
 }
 

@@ -626,13 +626,27 @@ __global__ void __launch_bounds__(WG) k_ffn13(
     /* with part: the normalised row is x + the nh per-head Wo shares, added in
      * head order (the same sum k_w2_residual stores) */
     if (part) {
+        /* heads in groups of four: a group's loads are all issued before its
+         * adds, which stay in head order */
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
-            for (int hh = 0; hh < nh; hh++)
+            const float *pb = part + (size_t)b * nh * D + threadIdx.x;
+            int hh = 0;
+            for (; hh + 4 <= nh; hh += 4) {
+                float t[4][D / WG];
 #pragma unroll
-                for (int j = 0; j < D / WG; j++)
-                    in.v[b][j] += part[((size_t)b * nh + hh) * D + threadIdx.x + j * WG];
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int j = 0; j < D / WG; j++) t[u][j] = pb[(size_t)(hh + u) * D + j * WG];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int j = 0; j < D / WG; j++) in.v[b][j] += t[u][j];
+            }
+            for (; hh < nh; hh++)
+#pragma unroll
+                for (int j = 0; j < D / WG; j++) in.v[b][j] += pb[(size_t)hh * D + j * WG];
         }
     }
     norm_to_lds<D, NB>(in, B, x, false, xs);
@@ -673,8 +687,20 @@ __global__ void __launch_bounds__(WG) k_w2_residual(
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
-            for (int hh = 0; hh < nh; hh++) {
-                const float2 t = *(const float2 *)(part + ((size_t)b * nh + hh) * D + r);
+            const float *pb = part + (size_t)b * nh * D + r;
+            int hh = 0;
+            for (; hh + 4 <= nh; hh += 4) {   /* loads of four heads, then their adds in order */
+                float2 t[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) t[u] = *(const float2 *)(pb + (size_t)(hh + u) * D);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    xo[b].x += t[u].x;
+                    xo[b].y += t[u].y;
+                }
+            }
+            for (; hh < nh; hh++) {
+                const float2 t = *(const float2 *)(pb + (size_t)hh * D);
                 xo[b].x += t.x;
                 xo[b].y += t.y;
             }

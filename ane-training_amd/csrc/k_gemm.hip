@@ -280,6 +280,114 @@ __device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
                  : "memory");
 }
 
+/* GATE epilogue of a BM x BN work-group tile through LDS: the gates (computed
+ * in the accumulator layout, as epilogue_tile does) are staged as fp16 rows of
+ * BN/2 gates, then written with one 16-byte store per 8 gates instead of one
+ * 2-byte store per gate.  sg: LDS of at least BM * (BN/2 + 8) halves, no longer
+ * read by any wave's main loop. */
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *sg, int m0, int n0,
+                                              int wm, int wn, const EpiArgs &e)
+{
+    constexpr int GW = BN / 2, GLD = GW + 8;
+    const int lane = threadIdx.x & 63, c = lane & 31;
+    const bool lo = c < 16;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int rl = wm * (BM / 2) + i * 32 + 4 * (lane >> 5);
+            const int gl = (wn * (BN / 2) + j * 32) / 2 + (c & 15);
+#pragma unroll
+            for (int k = 0; k < 16; k += 2) {
+                /* lane c < 16: row of element k (h1 own, h3 from lane c + 16);
+                 * lane c + 16: row of element k + 1 (h3 own, h1 from lane c) */
+                const float other = xor16_f(lo ? acc[i][j][k + 1] : acc[i][j][k]);
+                const float h1 = lo ? acc[i][j][k] : other;
+                const float h3 = lo ? other : acc[i][j][k + 1];
+                const int r = rl + 8 * (k >> 2) + (k & 3) + (lo ? 0 : 1);
+                const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
+                const float silu = h1 * __builtin_amdgcn_rcpf(1.0f + ex);   /* forward.h:101 */
+                sg[r * GLD + gl] = f2h(silu * h3);                          /* forward.h:151 */
+            }
+        }
+    __syncthreads();
+    constexpr int CPR = GW / 8;   /* 16-byte chunks per row */
+#pragma unroll
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += GT) {
+        const int r = idx / CPR, ch = idx % CPR;
+        const int row = m0 + r, gi = n0 / 2 + ch * 8;
+        if (row < e.M && gi < e.F)
+            *(uint4 *)(e.g + (size_t)row * e.F + gi) = *(const uint4 *)(sg + r * GLD + ch * 8);
+    }
+}
+
+/* QKV epilogue of a BM x BN work-group tile through LDS (prefill rows): in
+ * rounds of 64 rows (row tile i of both wave rows), the fp32 products are
+ * staged in LDS, then each thread takes 4 consecutive columns of a row (two
+ * RoPE pairs, forward.h:55-70): q columns go to q [M, NQ] with one 16-byte
+ * store, k and v columns to the cache at (slot[row], pos[row]) with one 16- or
+ * 8-byte store.  The arithmetic is that of k_qkv_post.  b0, b1: LDS of at
+ * least 64 * BN floats each, no longer read by any wave's main loop. */
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float *b0, float *b1,
+                                             int m0, int n0, int wm, int wn, const EpiArgs &e)
+{
+    constexpr int WM = BM / 2, WN = BN / 2, C4 = BN / 4;
+    const int lane = threadIdx.x & 63;
+    const int half_hd = e.hd >> 1;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        float *buf = (i & 1) ? b1 : b0;
+        /* buf row wm*32 + r holds tile row m0 + wm*WM + i*32 + r */
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const int r = wm * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
+                buf[r * BN + wn * WN + j * 32 + (lane & 31)] = acc[i][j][k];
+            }
+        __syncthreads();
+#pragma unroll
+        for (int idx = threadIdx.x; idx < 64 * C4; idx += GT) {
+            const int r = idx / C4, c4 = idx % C4;
+            const int row = m0 + (r >> 5) * WM + i * 32 + (r & 31);
+            const int n = n0 + 4 * c4;
+            if (row >= e.M || n >= e.N) continue;
+            const float4 v = *(const float4 *)(buf + r * BN + 4 * c4);
+            const int p = e.pos[row];
+            const bool isq = n < e.NQ, rot = n < e.NQ + e.NKV;
+            const int nn = isq ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
+            const int d = nn % e.hd;
+            float o[4] = {v.x, v.y, v.z, v.w};
+            if (rot) {
+                const int ti = p * half_hd + (d >> 1);
+                const float2 c = *(const float2 *)(e.rope_cos + ti);
+                const float2 sn = *(const float2 *)(e.rope_sin + ti);
+                o[0] = fmaf(v.x, c.x, -(v.y * sn.x));   /* forward.h:64 */
+                o[1] = fmaf(v.x, sn.x, v.y * c.x);      /* forward.h:65 */
+                o[2] = fmaf(v.z, c.y, -(v.w * sn.y));
+                o[3] = fmaf(v.z, sn.y, v.w * c.y);
+            }
+            if (isq) {
+                *(float4 *)(e.q + (size_t)row * e.NQ + n) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                const size_t off =
+                    (((size_t)e.slot[row] * e.Hkv + nn / e.hd) * e.max_seq + p) * e.hd + d;
+                void *dst = rot ? e.kc : e.vc;
+                if (e.kv_f32)
+                    *(float4 *)((float *)dst + off) = make_float4(o[0], o[1], o[2], o[3]);
+                else
+                    *(uint2 *)((u16 *)dst + off) =
+                        make_uint2((unsigned)f2h(o[0]) | ((unsigned)f2h(o[1]) << 16),
+                                   (unsigned)f2h(o[2]) | ((unsigned)f2h(o[3]) << 16));
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int E>
 __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                   const u16 *__restrict__ W, int K, int kc,
@@ -365,6 +473,10 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         unsigned ad[NF];
         frag_addr(st, 0, ad);
         lds_read_wait(f[0], ad);
+        /* The scheduling barriers pin the order reads(ks+1), loads, MFMAs(ks),
+         * wait(ks+1): the MFMAs do not depend on the wait, and without them the
+         * scheduler hoists the wait above the MFMAs, exposing the LDS latency
+         * at every step. */
         static_for<0, BKH / 16>([&](auto KS) {
             constexpr int ks = decltype(KS)::value;
             if (ks + 1 < BKH / 16) {      /* next step's reads run under this step's MFMAs */
@@ -374,12 +486,14 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
             if (ld)
                 issue_range(ahead, kt2, std::integral_constant<int, ks * LDW / 4>{},
                             std::integral_constant<int, (ks + 1) * LDW / 4>{});
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = mfma32(__builtin_bit_cast(uint4, f[ks & 1][i]),
                                        __builtin_bit_cast(uint4, f[ks & 1][TM + j]), acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
             if (ks + 1 < BKH / 16) lds_wait_regs(f[(ks + 1) & 1]);
         });
     };
@@ -401,6 +515,15 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         if (kt + 2 < nk) step(kt + 2, lds2, lds1);
     }
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
+    if constexpr (E == EPI_GATE) {
+        static_assert(BM * (BN / 2 + 8) <= STAGE, "gate staging fits one stage buffer");
+        gate_tile_lds<BM, BN, TM, TN>(acc, lds0, m0, n0, wm, wn, e);
+        return;
+    }
+    if constexpr (E == EPI_QKV && 64 * BN * 2 <= STAGE) {
+        qkv_tile_lds<BM, BN, TM, TN>(acc, (float *)lds0, (float *)lds1, m0, n0, wm, wn, e);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -595,16 +718,21 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
                     }
                 }
             };
-            int q = 0;
-            for (; q + 4 <= ns; q += 4) {
-                float t0[C4 * 4], t1[C4 * 4], t2[C4 * 4], t3[C4 * 4];
-                load_part(q, t0); load_part(q + 1, t1); load_part(q + 2, t2); load_part(q + 3, t3);
-                add_part(t0); add_part(t1); add_part(t2); add_part(t3);
-            }
-            for (; q < ns; q++) {
-                float t0[C4 * 4];
-                load_part(q, t0);
-                add_part(t0);
+            /* groups of eight partials: all loads of a group are issued before
+             * its adds (in split order); past the last partial the group reloads
+             * it and adds zero, so the loads stay unconditional */
+            for (int q = 0; q < ns; q += 8) {
+                float t[8][C4 * 4];
+#pragma unroll
+                for (int u = 0; u < 8; u++) load_part(min(q + u, ns - 1), t[u]);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (q + u >= ns) {
+#pragma unroll
+                        for (int i = 0; i < PER; i++) t[u][i] = 0.f;
+                    }
+                    add_part(t[u]);
+                }
             }
         }
     }
@@ -694,6 +822,30 @@ __global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, 
     }
 }
 
+/* ---- SwiGLU gate of K-split W1/W3 partials ---------------------------------- */
+
+/* part: ns partials [M, 2F] fp32 of the interleaved W1/W3 GEMM (columns
+ * 32j .. 32j+15 are W1 rows 16j .., columns 32j+16 .. 32j+31 the W3 rows),
+ * sstride floats apart; g[m, i] = fp16(silu(h1) * h3) with h1, h3 summed in
+ * split order (forward.h:149-151), the same arithmetic as the GATE epilogue.
+ * One thread per gate, rows on blockIdx.y. */
+__global__ void __launch_bounds__(GT) k_gate_post(const float *__restrict__ part, int ns,
+                                                  size_t sstride, int F, u16 *__restrict__ g)
+{
+    const int m = blockIdx.y;
+    const int gi = blockIdx.x * GT + threadIdx.x;
+    if (gi >= F) return;
+    const size_t c1 = (size_t)m * 2 * F + (gi >> 4) * 32 + (gi & 15);
+    float h1 = part[c1], h3 = part[c1 + 16];
+    for (int q = 1; q < ns; q++) {
+        h1 += part[q * sstride + c1];
+        h3 += part[q * sstride + c1 + 16];
+    }
+    const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
+    const float silu = h1 * __builtin_amdgcn_rcpf(1.0f + ex);   /* forward.h:101 */
+    g[(size_t)m * F + gi] = f2h(silu * h3);
+}
+
 /* ============================== launchers =================================== */
 
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
@@ -779,7 +931,7 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
 {
     if (M < 1 || N < 1 || K < 32 || K % 32 || lda < K || !A || !W || !ep) return hipErrorInvalidValue;
     if (epi == EPI_GATE && (N % 32 || !ep->g)) return hipErrorInvalidValue;
-    if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || (ep->hd & 1) ||
+    if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || (ep->hd & 3) ||
                            N != ep->NQ + 2 * ep->NKV))
         return hipErrorInvalidValue;
     if (epi == EPI_RESID && (!ep->out || ep->ldc < N)) return hipErrorInvalidValue;
@@ -812,9 +964,30 @@ extern "C" int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstr
     return hipGetLastError();
 }
 
-/* K-split count for a decode-row GEMM (M <= 64): with one work-group per 32
+extern "C" int lmk_gate_post(hipStream_t s, const float *part, int ns, size_t sstride, int M, int F,
+                             uint16_t *g)
+{
+    if (M < 1 || M > 65535 || ns < 1 || F < 16 || F % 16 || !part || !g) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gate_post, dim3((F + GT - 1) / GT, M), dim3(GT), 0, s, part, ns, sstride, F,
+                       (u16 *)g);
+    return hipGetLastError();
+}
+
+/* Tile of a K-split tiled GEMM (M > 64): the largest that, with the ns splits,
+ * still gives the 256 CUs about a work-group each. */
+static void split_tile(int M, int N, int ns, int *bm, int *bn)
+{
+    auto wgs = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn) * ns; };
+    if (wgs(256, 128) >= 240) *bm = 256, *bn = 128;
+    else if (wgs(128, 128) >= 240) *bm = 128, *bn = 128;
+    else if (wgs(128, 64) >= 240) *bm = 128, *bn = 64;
+    else *bm = 64, *bn = 64;
+}
+
+/* K-split count for a GEMM.  Decode rows (M <= 64): with one work-group per 32
  * columns a narrow N leaves most CUs idle, so K is cut into the fewest splits
- * (k-chunks a multiple of 64) that give about one work-group per CU. */
+ * (k-chunks a multiple of 64) that give about one work-group per CU.  More
+ * rows: not split. */
 extern "C" int lmk_pick_split(int M, int N, int K)
 {
     const int nb = (N + 31) / 32;
@@ -831,12 +1004,22 @@ extern "C" int lmk_pick_split(int M, int N, int K)
 extern "C" int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
                               int N, int K, int ns, float *part)
 {
-    if (M < 1 || M > 64 || N < 1 || ns < 1 || ns > LMK_MAX_SPLIT || K % (16 * ns) || lda < K ||
-        !A || !W || !part)
+    if (M < 1 || N < 1 || ns < 1 || ns > LMK_MAX_SPLIT || K % (16 * ns) || lda < K || !A || !W ||
+        !part)
         return hipErrorInvalidValue;
     EpiArgs e = {};
     e.M = M; e.N = N; e.out = part; e.ldc = N; e.nparts = (N + 31) / 32;
     e.sstride = (size_t)M * N;
-    launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
+    if (M <= 64) {
+        launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
+        return hipGetLastError();
+    }
+    if (K % (BKH * ns)) return hipErrorInvalidValue;
+    int bm, bn;
+    split_tile(M, N, ns, &bm, &bn);
+    if (bm == 256) launch_tile_split<256, 128>(s, A, lda, W, M, N, K, ns, e);
+    else if (bn == 128) launch_tile_split<128, 128>(s, A, lda, W, M, N, K, ns, e);
+    else if (bm == 128) launch_tile_split<128, 64>(s, A, lda, W, M, N, K, ns, e);
+    else launch_tile_split<64, 64>(s, A, lda, W, M, N, K, ns, e);
     return hipGetLastError();
 }

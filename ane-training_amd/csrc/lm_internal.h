@@ -154,12 +154,17 @@ int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstride, int M,
                  const float *rope_cos, const float *rope_sin, float *q, void *kc, void *vc,
                  int kv_f32);
 
-/* Decode-row GEMM (M <= 64) with K cut into ns splits: part[s][M][N] (fp32) is
- * split s's partial of A W^T; lmk_pick_split chooses ns for a shape. */
+/* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
+ * A W^T.  Decode rows (M <= 64) run the skinny kernel, more rows the tiled
+ * kernel; lmk_pick_split chooses ns for a shape (1: do not split). */
 #define LMK_MAX_SPLIT 16
+#define LMK_MAX_ROW_SPLIT 4    /* most splits lmk_pick_split gives for M > 64 */
 int lmk_pick_split(int M, int N, int K);
 int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                    int K, int ns, float *part);
+/* SwiGLU gate of ns K-split partials [M, 2F] (W1/W3 rows interleaved in blocks
+ * of 16, as the GATE epilogue expects) to g [M, F] fp16. */
+int lmk_gate_post(hipStream_t s, const float *part, int ns, size_t sstride, int M, int F, uint16_t *g);
 
 /* One work-group per row: with emb != NULL x[m] is first set to the embedding row
  * emb[tok[m]]; with ns > 0 the ns partials sp[s][m] (sstride floats apart) of a

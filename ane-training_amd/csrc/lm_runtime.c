@@ -53,8 +53,8 @@ struct LMModel {
     size_t kv_layer_elems;
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
-    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd, *d_qkv;
-    float *d_part;              /* partials of K-split decode-row GEMMs       */
+    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
+    float *d_part;              /* partials of K-split GEMMs, Wo/W2 products    */
     float *d_opart;             /* batch 1-4 chain: per-head Wo shares [4][H][D] */
     int fuse_wo;                /* attention + Wo fused in the batch 1-4 chain  */
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
@@ -262,11 +262,11 @@ static void drop_graphs(LMModel *m)
 
 static void free_rows(LMModel *m)
 {
-    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_qkv, m->d_part, m->d_g16,
+    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_part, m->d_g16,
                    m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
-    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_qkv = m->d_part = NULL;
+    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_part = NULL;
     m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
     m->d_rtok = m->d_rpos = m->d_rslot = NULL;
@@ -291,12 +291,14 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_a16, r * NQ * 2))) return st;
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
-    if ((st = dev_alloc((void **)&m->d_qkv, r * (NQ + 2 * (size_t)m->NKV) * 4))) return st;
     {
-        /* K-split partials of decode rows, or one [R, D] product of prefill rows */
-        const size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
+        /* K-split partials of decode rows (widest: QKV or W1/W3), or one [R, D]
+         * product of prefill rows */
+        size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
+        if (2 * (size_t)F > w) w = 2 * (size_t)F;
         const size_t rd = r < 64 ? r : 64;
         size_t n = LMK_MAX_SPLIT * rd * w;
+        if (r > 64 && LMK_MAX_ROW_SPLIT * r * w > n) n = LMK_MAX_ROW_SPLIT * r * w;
         if (r * D > n) n = r * D;
         if ((st = dev_alloc((void **)&m->d_part, n * 4))) return st;
     }
@@ -641,9 +643,10 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
      * and the row norm that next reads x adds it (the residual add).  Only
      * unsplit decode rows keep the residual add in the GEMM epilogue. */
     const int dec = M <= 64;
-    const int ns_qkv = dec ? lmk_pick_split(M, NQKV, D) : 1;
-    const int ns_wo = dec ? lmk_pick_split(M, D, NQ) : 1;
-    const int ns_w2 = dec ? lmk_pick_split(M, D, F) : 1;
+    const int ns_qkv = lmk_pick_split(M, NQKV, D);
+    const int ns_wo = lmk_pick_split(M, D, NQ);
+    const int ns_w2 = lmk_pick_split(M, D, F);
+    const int ns_w13 = lmk_pick_split(M, 2 * F, D);
     const int sep_wo = !dec || ns_wo > 1, sep_w2 = !dec || ns_w2 > 1;
     const float *pend = NULL;          /* W2 partials not yet added to x */
     int pend_ns = 0;
@@ -658,15 +661,9 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         pend_ns = 0;
         int attn_done = 0;   /* attention already ran (fused with the QKV partials) */
         memset(&ep, 0, sizeof(ep));
-        if (!dec) {
-            /* prefill rows: plain fp32 QKV rows, then a coalesced RoPE + append pass */
-            ep.out = m->d_qkv; ep.ldc = NQKV;
-            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_STORE, &ep));
-            KCHK(lmk_qkv_post(s, m->d_qkv, 1, 0, M, NQ, NKV, m->hd, m->Hkv, m->max_seq, pos, slot,
-                              m->d_rope_cos, m->d_rope_sin, m->d_q, kc, vc, m->kv_f32));
-        } else if (ns_qkv > 1) {
+        if (ns_qkv > 1) {
             KCHK(lmk_gemm_split(s, m->d_xn16, D, lw, M, NQKV, D, ns_qkv, m->d_part));
-            if (seq_rows == 1) {
+            if (dec && seq_rows == 1) {
                 /* decode rows: the attention kernel sums the partials, applies
                  * RoPE and appends K/V itself */
                 KCHK(lmk_attn_decode_part(s, m->d_part, (size_t)M * NQKV, ns_qkv, NQ, NKV, pos, slot,
@@ -679,7 +676,8 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                                   m->d_q, kc, vc, m->kv_f32));
             }
         } else {
-            /* wide enough unsplit: RoPE and the append fused into the GEMM epilogue */
+            /* unsplit: RoPE and the append fused into the GEMM epilogue (for
+             * prefill rows staged through LDS and stored row-contiguously) */
             ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
             ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
             ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
@@ -710,9 +708,16 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, NULL, 0, 0,
                              m->d_rms_ffn + (size_t)l * D, m->d_xn16));
         }
-        memset(&ep, 0, sizeof(ep));
-        ep.g = m->d_g16; ep.F = F;
-        KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
+        if (ns_w13 > 1) {
+            /* too few 32-column blocks to fill the CUs: K-split partials, then
+             * the gate of their sums */
+            KCHK(lmk_gemm_split(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, ns_w13, m->d_part));
+            KCHK(lmk_gate_post(s, m->d_part, ns_w13, (size_t)M * 2 * F, M, F, m->d_g16));
+        } else {
+            memset(&ep, 0, sizeof(ep));
+            ep.g = m->d_g16; ep.F = F;
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
+        }
         if (sep_w2) {
             if (ns_w2 > 1) {
                 KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));
@@ -1235,9 +1240,9 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
 int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, const uint16_t *W,
                            float *parts)
 {
-    if (M < 1 || M > 64 || N < 1 || K < 32 || K % 32 || !A || !W || !parts) return LM_ERR_INVALID;
+    if (M < 1 || M > 4096 || N < 1 || K < 32 || K % 32 || !A || !W || !parts) return LM_ERR_INVALID;
     if (nsplit == 0) nsplit = lmk_pick_split(M, N, K);
-    if (nsplit < 1 || nsplit > LMK_MAX_SPLIT || K % (16 * nsplit)) return LM_ERR_INVALID;
+    if (nsplit < 1 || nsplit > LMK_MAX_SPLIT || K % ((M > 64 ? 64 : 16) * nsplit)) return LM_ERR_INVALID;
     int rc = lm_init();
     if (rc) return rc;
     const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2;

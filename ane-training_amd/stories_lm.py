@@ -399,7 +399,7 @@ def selftest_gemm(A: np.ndarray, W16: np.ndarray, want_parts: bool = False):
 
 
 def gemm_split_count(M: int, N: int, K: int) -> int:
-    """K-split count the runtime uses for a decode-row [M, K] x [N, K]^T GEMM."""
+    """K-split count the runtime uses for an [M, K] x [N, K]^T GEMM."""
     n = lib().lm_gemm_split_count(M, N, K)
     if n < 0:
         raise LMError(n, "lm_gemm_split_count")
@@ -407,8 +407,9 @@ def gemm_split_count(M: int, N: int, K: int) -> int:
 
 
 def selftest_gemm_split(A16: np.ndarray, W16: np.ndarray, nsplit: int = 0) -> np.ndarray:
-    """Partials [n, M, N] of the K-split decode-row GEMM (M <= 64); A16, W16 are
-    uint16 fp16 bits [M, K], [N, K]; nsplit 0 = the runtime's choice."""
+    """Partials [n, M, N] of the K-split GEMM (skinny kernel for M <= 64, tiled
+    up to 4096 rows); A16, W16 are uint16 fp16 bits [M, K], [N, K]; nsplit 0 =
+    the runtime's choice."""
     A16 = np.ascontiguousarray(A16, dtype=np.uint16)
     W16 = np.ascontiguousarray(W16, dtype=np.uint16)
     M, K = A16.shape

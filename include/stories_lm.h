@@ -278,15 +278,16 @@ typedef struct { float val; int idx; } LMArgPartHost;
 int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16_t *W,
                      float *C, LMArgPartHost *part);
 
-/* Run the K-split decode-row GEMM (M <= 64) the batched decode uses for narrow
- * projections: parts[s] [M, N] fp32 = A[:, s*K/n .. (s+1)*K/n) W[:, same]^T for
- * s < n, n = nsplit, or the runtime's own choice when nsplit == 0.  A [M, K]
- * and W [N, K] fp16 bits; parts holds n*M*N floats (size it with
- * lm_gemm_split_count).  Returns n (> 0) or a negative status. */
+/* Run the K-split GEMM the forward uses for narrow projections (the skinny
+ * kernel for M <= 64 rows, the tiled kernel up to 4096 rows, where K must be a
+ * multiple of 64*nsplit): parts[s] [M, N] fp32 = A[:, s*K/n .. (s+1)*K/n)
+ * W[:, same]^T for s < n, n = nsplit, or the runtime's own choice when
+ * nsplit == 0.  A [M, K] and W [N, K] fp16 bits; parts holds n*M*N floats (size
+ * it with lm_gemm_split_count).  Returns n (> 0) or a negative status. */
 int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, const uint16_t *W,
                            float *parts);
 
-/* The split count the runtime uses for an [M, K] x [N, K]^T decode-row GEMM. */
+/* The split count the runtime uses for an [M, K] x [N, K]^T GEMM (1: unsplit). */
 int lm_gemm_split_count(int M, int N, int K);
 
 /* Kernel families of a decode step (index into lm_profile_decode's output). */
