@@ -279,54 +279,11 @@ __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
  * running (max, sum, weighted V).  The four waves merge through LDS and the
  * normalised head output (forward.h:95-97) goes to out[b, h*HD ..] (fp32), or
  * in fp16 to out16 when that is given (the operand of the Wo GEMM). */
-/* Decode rows straight from a K-split QKV GEMM: part holds ns partials
- * [M, NQ + 2*NKV] (sstride floats apart); the row's q, k, v are their sums,
- * RoPE'd at pos[b] with the host tables (forward.h:55-70).  The head's first
- * query head of each kv group appends k, v to the cache (forward.h:118-128);
- * every work-group uses its own registers for the current position, so no
- * work-group waits for another's append. */
-template <typename KT>
-struct QkvPart {
-    const float *part;
-    size_t sstride;
-    int ns, NQ, NKV;
-    const float *rc, *rs;   /* RoPE cos / sin [max_seq][hd/2] */
-    KT *kc, *vc;            /* the cache, written at the current position */
-};
-
-/* 8 consecutive columns c0.. of row b summed over the ns partials */
-__device__ __forceinline__ void part_sum8(const float *__restrict__ part, size_t sstride, int ns,
-                                          size_t off, float v[8])
-{
-#pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = 0.f;
-    for (int s = 0; s < ns; s++) {
-        const float4 a = *(const float4 *)(part + s * sstride + off);
-        const float4 c = *(const float4 *)(part + s * sstride + off + 4);
-        v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
-        v[4] += c.x; v[5] += c.y; v[6] += c.z; v[7] += c.w;
-    }
-}
-
-/* RoPE of the 4 pairs of dims d0 .. d0+7 at position p (forward.h:62-68) */
-__device__ __forceinline__ void rope8(float v[8], int d0, int p, int half_hd,
-                                      const float *__restrict__ rc, const float *__restrict__ rs)
-{
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int ti = p * half_hd + (d0 >> 1) + i;
-        const float c = rc[ti], sn = rs[ti];
-        const float a = v[2 * i], bb = v[2 * i + 1];
-        v[2 * i] = fmaf(a, c, -(bb * sn));
-        v[2 * i + 1] = fmaf(a, sn, bb * c);
-    }
-}
-
 template <int HD, typename KT, typename Hook>
 __device__ __forceinline__ void attn_head(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
+    float *oh, Hook after_first_loads)
 {
     /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
      * would take 256 registers per lane */
@@ -347,26 +304,8 @@ __device__ __forceinline__ void attn_head(
     const KT *K = kc + base;
     const KT *V = vc + base;
     const float scale = 1.0f / sqrtf((float)HD);
-    float qf[8], kcur[8], vcur[8];
-    if (qp) {
-        /* q, and the k, v of the current position, from the split partials */
-        const int g = h / (H / Hkv), W = qp->NQ + 2 * qp->NKV, p = ctx - 1;
-        const size_t row = (size_t)b * W;
-        part_sum8(qp->part, qp->sstride, qp->ns, row + h * HD + dq * 8, qf);
-        part_sum8(qp->part, qp->sstride, qp->ns, row + qp->NQ + g * HD + dq * 8, kcur);
-        part_sum8(qp->part, qp->sstride, qp->ns, row + qp->NQ + qp->NKV + g * HD + dq * 8, vcur);
-        rope8(qf, dq * 8, p, HD / 2, qp->rc, qp->rs);
-        rope8(kcur, dq * 8, p, HD / 2, qp->rc, qp->rs);
-        if (h % (H / Hkv) == 0 && wv == 0 && pp == 0) {
-            KT *kd = qp->kc + ((size_t)cs * Hkv + g) * max_seq * HD + (size_t)p * HD + dq * 8;
-            KT *vd = qp->vc + ((size_t)cs * Hkv + g) * max_seq * HD + (size_t)p * HD + dq * 8;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                kd[j] = kv_pack<KT>(kcur[j]);
-                vd[j] = kv_pack<KT>(vcur[j]);
-            }
-        }
-    } else {
+    float qf[8];
+    {
         const float *qr = q + (size_t)b * H * HD + h * HD + dq * 8;
         const float4 a = *(const float4 *)qr, c = *(const float4 *)(qr + 4);
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
@@ -413,11 +352,6 @@ __device__ __forceinline__ void attn_head(
         for (int i = 0; i < NP; i++) {
             float kf[8];
             kv_raw_unpack(kr[i], kf);
-            if (qp && t * TILE + pp + PP * i == ctx - 1) {   /* the current position */
-                /* the cache is rounded to its element type; so is the own copy */
-#pragma unroll
-                for (int j = 0; j < 8; j++) kf[j] = kv_round<KT>(kcur[j]);
-            }
             float d = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) d = fmaf(qf[j], kf[j], d);
@@ -440,10 +374,6 @@ __device__ __forceinline__ void attn_head(
             l += e;
             float vf[8];
             kv_raw_unpack(vr[i], vf);
-            if (qp && t * TILE + pp + PP * i == ctx - 1) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) vf[j] = kv_round<KT>(vcur[j]);
-            }
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = fmaf(e, vf[j], o[j]);
         }
@@ -493,23 +423,6 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
         if (out16) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
         else out[(size_t)b * H * HD + h * HD + d] = oh[d];
     }
-}
-
-/* Work-group (h, b) for decode rows of the MFMA path whose QKV GEMM ran
- * K-split: q, k, v come from the partials (see QkvPart), the head output goes
- * to out16[b, h*HD ..] in fp16 (the Wo GEMM operand). */
-template <int HD, typename KT>
-__global__ void __launch_bounds__(WG) k_attn_decode_part(
-    const float *__restrict__ part, size_t sstride, int ns, int NQ, int NKV,
-    const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    const float *__restrict__ rc, const float *__restrict__ rs, KT *__restrict__ kc,
-    KT *__restrict__ vc, u16 *__restrict__ out16)
-{
-    __shared__ float oh[HD];
-    const QkvPart<KT> qp = {part, sstride, ns, NQ, NKV, rc, rs, kc, vc};
-    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, [] {}, &qp);
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    if (d < HD) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
 }
 
 /* ---- attention + Wo of one head ------------------------------------------------ */
@@ -952,27 +865,6 @@ extern "C" int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2
     return hipGetLastError();
 }
 
-extern "C" int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int ns, int NQ,
-                                    int NKV, const int *pos, const int *slot, int B, int H, int Hkv,
-                                    int hd, int max_seq, const float *rope_cos, const float *rope_sin,
-                                    void *kc, void *vc, int kv_f32, uint16_t *out16)
-{
-    if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv || ns < 1 || NQ != H * hd ||
-        NKV != Hkv * hd || !part || !pos || !slot || !kc || !vc || !out16)
-        return hipErrorInvalidValue;
-    dim3 grid(H, B);
-#define LAUNCH_ADP(HD_, KT_)                                                                      \
-    hipLaunchKernelGGL((k_attn_decode_part<HD_, KT_>), grid, dim3(WG), 0, s, part, sstride, ns, NQ, \
-                       NKV, pos, slot, H, Hkv, max_seq, rope_cos, rope_sin, (KT_ *)kc, (KT_ *)vc,  \
-                       (u16 *)out16)
-    if (hd == 64 && kv_f32) LAUNCH_ADP(64, float);
-    else if (hd == 64) LAUNCH_ADP(64, u16);
-    else if (hd == 128 && kv_f32) LAUNCH_ADP(128, float);
-    else if (hd == 128) LAUNCH_ADP(128, u16);
-    else return hipErrorInvalidValue;
-#undef LAUNCH_ADP
-    return hipGetLastError();
-}
 
 /* Fused attention + Wo shares: shapes whose Wo head block fits the LDS. */
 extern "C" int lmk_attn_wo_supported(int D, int hd)

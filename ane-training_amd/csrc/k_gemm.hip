@@ -20,18 +20,18 @@
  * A[l%32][8*(l/32) .. +8], B[8*(l/32) .. +8][l%32] (= W[n0 + l%32][k ..]), and
  * accumulator i holds C[8*(i/4) + 4*(l/32) + i%4][l%32].
  *
- * Two tilings:
- *   k_gemm_tile    M > 64 rows: work-group tile BM x BN, four waves 2 x 2, K
- *                  streamed by direct global->LDS loads into a 3-deep ring of
- *                  64-wide stages; XCD-aware tile order
- *   k_gemm_skinny  M <= 64 rows (decode batches): a work-group owns 32 columns
- *                  and all rows of one K-chunk (all of K, or 1/ns of it for a
- *                  K-split GEMM, whose fp32 partials the next row kernel sums);
- *                  its four waves split the chunk, stream their weight
- *                  fragments straight from HBM into registers (each weight byte
- *                  read once) and add their partial tiles through LDS.
- * A classifier over decode rows (N >= 16384) takes the tiled kernel with a
- * 64-row tile instead.
+ * Two kernels:
+ *   k_gemm_tile    work-group tile BM x BN (64 x 64 for most shapes, 256 x 128
+ *                  for the largest, 64 x 128 for decode-row classifiers), four
+ *                  waves 2 x 2, K streamed by direct global->LDS loads into a
+ *                  3-deep ring of 64-wide stages; XCD-aware tile order; an
+ *                  optional K-split over blockIdx.y (fp32 partials, summed by
+ *                  the kernel that next reads them)
+ *   k_gemm_skinny  decode rows (M <= 64) whose K is not a multiple of 64: a
+ *                  work-group owns 32 columns and all rows of one K-chunk; its
+ *                  four waves split the chunk, stream their weight fragments
+ *                  straight from HBM into registers and add their partial tiles
+ *                  through LDS.
  */
 #include <type_traits>
 
@@ -323,20 +323,59 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
     }
 }
 
-/* QKV epilogue of a BM x BN work-group tile through LDS (prefill rows): in
- * rounds of 64 rows (row tile i of both wave rows), the fp32 products are
- * staged in LDS, then each thread takes 4 consecutive columns of a row (two
- * RoPE pairs, forward.h:55-70): q columns go to q [M, NQ] with one 16-byte
- * store, k and v columns to the cache at (slot[row], pos[row]) with one 16- or
- * 8-byte store.  The arithmetic is that of k_qkv_post.  b0, b1: LDS of at
- * least 64 * BN floats each, no longer read by any wave's main loop. */
-template <int BM, int BN, int TM, int TN>
+/* Per-item operands of the QKV epilogue (item: 4 consecutive columns of one
+ * row, two RoPE pairs): position, cache slot and the pairs' rotation. */
+struct QkvItem {
+    int p, sl;
+    float2 c, sn;
+};
+
+/* Position and slot of this thread's items of round `round` (item k: tile row
+ * (tid + k*GT) / (BN/4), columns 4 * ((tid + k*GT) % (BN/4)) ..). */
+template <int BM, int BN, int NI>
+__device__ __forceinline__ void qkv_item_rows(QkvItem (&it)[NI], int round, int m0, const EpiArgs &e)
+{
+    constexpr int WM = BM / 2, C4 = BN / 4;
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int r = (threadIdx.x + k * GT) / C4;
+        const int row = min(m0 + (r >> 5) * WM + round * 32 + (r & 31), e.M - 1);
+        it[k].p = e.pos[row];
+        it[k].sl = e.slot[row];
+    }
+}
+
+/* The items' rotations (clamped indices: the loads stay unconditional). */
+template <int BN, int NI>
+__device__ __forceinline__ void qkv_item_rope(QkvItem (&it)[NI], int n0, const EpiArgs &e)
+{
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int n = n0 + 4 * ((threadIdx.x + k * GT) % (BN / 4));
+        const bool rot = n < e.NQ + e.NKV;
+        const int nn = n < e.NQ ? n : n - e.NQ;
+        const int ti = rot ? it[k].p * (e.hd >> 1) + ((nn % e.hd) >> 1) : 0;
+        it[k].c = *(const float2 *)(e.rope_cos + ti);
+        it[k].sn = *(const float2 *)(e.rope_sin + ti);
+    }
+}
+
+/* QKV epilogue of a BM x BN work-group tile through LDS: in rounds of 64 rows
+ * (row tile i of both wave rows), the fp32 products are staged in LDS, then
+ * each thread takes 4 consecutive columns of a row (two RoPE pairs,
+ * forward.h:55-70): q columns go to q [M, NQ] with one 16-byte store, k and v
+ * columns to the cache at (slot[row], pos[row]) with one 16- or 8-byte store.
+ * pre: positions and slots of round 0's items, loaded before the main loop
+ * (TM = 1), or NULL.  b0, b1:
+ * LDS of at least 64 * BN floats each, no longer read by any wave's main loop. */
+template <int BM, int BN, int TM, int TN, int NI>
 __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float *b0, float *b1,
-                                             int m0, int n0, int wm, int wn, const EpiArgs &e)
+                                             int m0, int n0, int wm, int wn, const EpiArgs &e,
+                                             const QkvItem (*pre)[NI])
 {
     constexpr int WM = BM / 2, WN = BN / 2, C4 = BN / 4;
+    static_assert(NI * GT == 64 * C4, "items per thread");
     const int lane = threadIdx.x & 63;
-    const int half_hd = e.hd >> 1;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < TM; i++) {
@@ -349,23 +388,29 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
                 const int r = wm * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
                 buf[r * BN + wn * WN + j * 32 + (lane & 31)] = acc[i][j][k];
             }
+        QkvItem its[NI];
+        if (i == 0 && pre) {
+#pragma unroll
+            for (int k = 0; k < NI; k++) its[k] = (*pre)[k];
+        } else {
+            qkv_item_rows<BM, BN, NI>(its, i, m0, e);
+        }
+        qkv_item_rope<BN, NI>(its, n0, e);
         __syncthreads();
 #pragma unroll
-        for (int idx = threadIdx.x; idx < 64 * C4; idx += GT) {
-            const int r = idx / C4, c4 = idx % C4;
+        for (int k = 0; k < NI; k++) {
+            const int idx = threadIdx.x + k * GT, r = idx / C4, c4 = idx % C4;
             const int row = m0 + (r >> 5) * WM + i * 32 + (r & 31);
             const int n = n0 + 4 * c4;
             if (row >= e.M || n >= e.N) continue;
             const float4 v = *(const float4 *)(buf + r * BN + 4 * c4);
-            const int p = e.pos[row];
+            const int p = its[k].p;
             const bool isq = n < e.NQ, rot = n < e.NQ + e.NKV;
             const int nn = isq ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
             const int d = nn % e.hd;
             float o[4] = {v.x, v.y, v.z, v.w};
             if (rot) {
-                const int ti = p * half_hd + (d >> 1);
-                const float2 c = *(const float2 *)(e.rope_cos + ti);
-                const float2 sn = *(const float2 *)(e.rope_sin + ti);
+                const float2 c = its[k].c, sn = its[k].sn;
                 o[0] = fmaf(v.x, c.x, -(v.y * sn.x));   /* forward.h:64 */
                 o[1] = fmaf(v.x, sn.x, v.y * c.x);      /* forward.h:65 */
                 o[2] = fmaf(v.z, c.y, -(v.w * sn.y));
@@ -375,7 +420,7 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
                 *(float4 *)(e.q + (size_t)row * e.NQ + n) = make_float4(o[0], o[1], o[2], o[3]);
             } else {
                 const size_t off =
-                    (((size_t)e.slot[row] * e.Hkv + nn / e.hd) * e.max_seq + p) * e.hd + d;
+                    (((size_t)its[k].sl * e.Hkv + nn / e.hd) * e.max_seq + p) * e.hd + d;
                 void *dst = rot ? e.kc : e.vc;
                 if (e.kv_f32)
                     *(float4 *)((float *)dst + off) = make_float4(o[0], o[1], o[2], o[3]);
@@ -507,6 +552,20 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         __builtin_amdgcn_s_barrier();
         compute(cur, ahead, kt + 2, kt + 2 < nk);
     };
+    /* positions and slots of a one-round tile's QKV epilogue, loaded first so
+     * that they arrive during the main loop */
+    constexpr bool QKV_LDS = E == EPI_QKV && 64 * BN * 2 <= STAGE;
+    constexpr int QNI = 64 * BN / 4 / GT;
+    QkvItem qpre[QKV_LDS ? QNI : 1];
+    if constexpr (QKV_LDS && TM == 1) {
+#pragma unroll
+        for (int k = 0; k < QNI; k++) {
+            const int r = (threadIdx.x + k * GT) / (BN / 4);
+            const int row = min(m0 + (r >> 5) * WM + (r & 31), M - 1);
+            qpre[k].p = e.pos[row];
+            qpre[k].sl = e.slot[row];
+        }
+    }
     issue(lds0, 0);
     if (nk > 1) issue(lds1, 1);
     for (int kt = 0; kt < nk; kt += NSTAGE) {
@@ -520,8 +579,9 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         gate_tile_lds<BM, BN, TM, TN>(acc, lds0, m0, n0, wm, wn, e);
         return;
     }
-    if constexpr (E == EPI_QKV && 64 * BN * 2 <= STAGE) {
-        qkv_tile_lds<BM, BN, TM, TN>(acc, (float *)lds0, (float *)lds1, m0, n0, wm, wn, e);
+    if constexpr (QKV_LDS) {
+        qkv_tile_lds<BM, BN, TM, TN, QNI>(acc, (float *)lds0, (float *)lds1, m0, n0, wm, wn, e,
+                                          TM == 1 ? &qpre : nullptr);
         return;
     }
 #pragma unroll
@@ -771,81 +831,6 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
     }
 }
 
-/* ---- RoPE + K/V append of stored QKV rows --------------------------------------- */
-
-/* qkv [M, NQ+2*NKV] fp32 rows (plain GEMM output): q pairs rotated to q [M, NQ];
- * k pairs rotated and v pairs appended to the cache at (slot[m], pos[m])
- * (forward.h:55-70, 118-128); with ns > 1, qkv holds the ns partials of a K-split
- * GEMM, ns x [M, NQ+2*NKV] sstride floats apart, summed first.  One thread per
- * column pair, rows on blockIdx.y. */
-template <typename KT>
-__global__ void __launch_bounds__(GT) k_qkv_post(const float *__restrict__ qkv, int ns,
-                                                 size_t sstride, int NQ, int NKV,
-                                                 int hd, int Hkv, int max_seq,
-                                                 const int *__restrict__ pos,
-                                                 const int *__restrict__ slot,
-                                                 const float *__restrict__ rc,
-                                                 const float *__restrict__ rs,
-                                                 float *__restrict__ q, KT *__restrict__ kc,
-                                                 KT *__restrict__ vc)
-{
-    const int m = blockIdx.y;
-    const int pr = blockIdx.x * GT + threadIdx.x;          /* column pair */
-    const int W = NQ + 2 * NKV;
-    if (2 * pr >= W) return;
-    const int n = 2 * pr;
-    float2 v = *(const float2 *)(qkv + (size_t)m * W + n);
-    for (int q = 1; q < ns; q++) {          /* partials of a K-split GEMM, in split order */
-        const float2 t = *(const float2 *)(qkv + q * sstride + (size_t)m * W + n);
-        v.x += t.x;
-        v.y += t.y;
-    }
-    const int p = pos[m];
-    if (n < NQ + NKV) {
-        const int nn = n < NQ ? n : n - NQ;
-        const int ti = p * (hd >> 1) + ((nn % hd) >> 1);
-        const float c = rc[ti], sn = rs[ti];
-        const float o0 = fmaf(v.x, c, -(v.y * sn));   /* forward.h:64 */
-        const float o1 = fmaf(v.x, sn, v.y * c);      /* forward.h:65 */
-        if (n < NQ) {
-            *(float2 *)(q + (size_t)m * NQ + n) = make_float2(o0, o1);
-        } else {
-            const size_t off = (((size_t)slot[m] * Hkv + nn / hd) * max_seq + p) * hd + nn % hd;
-            kc[off] = kv_pack<KT>(o0);
-            kc[off + 1] = kv_pack<KT>(o1);
-        }
-    } else {
-        const int nn = n - NQ - NKV;
-        const size_t off = (((size_t)slot[m] * Hkv + nn / hd) * max_seq + p) * hd + nn % hd;
-        vc[off] = kv_pack<KT>(v.x);
-        vc[off + 1] = kv_pack<KT>(v.y);
-    }
-}
-
-/* ---- SwiGLU gate of K-split W1/W3 partials ---------------------------------- */
-
-/* part: ns partials [M, 2F] fp32 of the interleaved W1/W3 GEMM (columns
- * 32j .. 32j+15 are W1 rows 16j .., columns 32j+16 .. 32j+31 the W3 rows),
- * sstride floats apart; g[m, i] = fp16(silu(h1) * h3) with h1, h3 summed in
- * split order (forward.h:149-151), the same arithmetic as the GATE epilogue.
- * One thread per gate, rows on blockIdx.y. */
-__global__ void __launch_bounds__(GT) k_gate_post(const float *__restrict__ part, int ns,
-                                                  size_t sstride, int F, u16 *__restrict__ g)
-{
-    const int m = blockIdx.y;
-    const int gi = blockIdx.x * GT + threadIdx.x;
-    if (gi >= F) return;
-    const size_t c1 = (size_t)m * 2 * F + (gi >> 4) * 32 + (gi & 15);
-    float h1 = part[c1], h3 = part[c1 + 16];
-    for (int q = 1; q < ns; q++) {
-        h1 += part[q * sstride + c1];
-        h3 += part[q * sstride + c1 + 16];
-    }
-    const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
-    const float silu = h1 * __builtin_amdgcn_rcpf(1.0f + ex);   /* forward.h:101 */
-    g[(size_t)m * F + gi] = f2h(silu * h3);
-}
-
 /* ============================== launchers =================================== */
 
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
@@ -898,31 +883,24 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
                        (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
 }
 
+/* Tile choice (measured on MI355X over the Stories and scaled-model shapes):
+ * 64 x 64 tiles everywhere, since four of them share a CU and hide each
+ * other's latency, except for GEMMs big enough to give every CU a 256 x 128
+ * tile (classifiers, the 2048-row W1/W3), where the larger tile's lower L2
+ * traffic wins; a decode-row classifier (N >= 16384) takes a 64 x 128 tile.
+ * K not a multiple of 64 (decode rows only) falls back to the skinny kernel. */
 template <int E>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
 {
-    if (M <= 64 && N >= 16384 && K % BKH == 0) {
-        /* a classifier over decode rows: a 64-row MFMA tile stages the rows in
-         * LDS once per 128 columns instead of once per 32 */
-        launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
-        return hipGetLastError();
-    }
-    if (M <= 64) {
+    if (K % BKH) {
+        if (M > 64) return hipErrorInvalidValue;
         launch_skinny<E>(s, A, lda, W, M, N, K, 1, e);
         return hipGetLastError();
     }
-    if (K % BKH) return hipErrorInvalidValue;
-    /* the largest tile that still gives the 256 CUs about a work-group each */
-    auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(256, 128) >= 240)
-        launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
-    else if (tiles(128, 128) >= 240)
-        launch_tile<128, 128, E>(s, A, lda, W, M, N, K, e);
-    else if (tiles(128, 64) >= 240)
-        launch_tile<128, 64, E>(s, A, lda, W, M, N, K, e);
-    else
-        launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
+    if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
+    else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
+    else launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
     return hipGetLastError();
 }
 
@@ -948,59 +926,28 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
     }
 }
 
-extern "C" int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstride, int M, int NQ,
-                            int NKV, int hd, int Hkv, int max_seq, const int *pos, const int *slot,
-                            const float *rope_cos, const float *rope_sin, float *q, void *kc,
-                            void *vc, int kv_f32)
-{
-    if (M < 1 || M > 65535 || ns < 1 || (hd & 1) || NQ % hd || NKV % hd) return hipErrorInvalidValue;
-    dim3 grid(((NQ + 2 * NKV) / 2 + GT - 1) / GT, M);
-    if (kv_f32)
-        hipLaunchKernelGGL(k_qkv_post<float>, grid, dim3(GT), 0, s, qkv, ns, sstride, NQ, NKV, hd, Hkv, max_seq, pos,
-                           slot, rope_cos, rope_sin, q, (float *)kc, (float *)vc);
-    else
-        hipLaunchKernelGGL(k_qkv_post<u16>, grid, dim3(GT), 0, s, qkv, ns, sstride, NQ, NKV, hd, Hkv, max_seq, pos,
-                           slot, rope_cos, rope_sin, q, (u16 *)kc, (u16 *)vc);
-    return hipGetLastError();
-}
-
-extern "C" int lmk_gate_post(hipStream_t s, const float *part, int ns, size_t sstride, int M, int F,
-                             uint16_t *g)
-{
-    if (M < 1 || M > 65535 || ns < 1 || F < 16 || F % 16 || !part || !g) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gate_post, dim3((F + GT - 1) / GT, M), dim3(GT), 0, s, part, ns, sstride, F,
-                       (u16 *)g);
-    return hipGetLastError();
-}
-
-/* Tile of a K-split tiled GEMM (M > 64): the largest that, with the ns splits,
- * still gives the 256 CUs about a work-group each. */
-static void split_tile(int M, int N, int ns, int *bm, int *bn)
-{
-    auto wgs = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn) * ns; };
-    if (wgs(256, 128) >= 240) *bm = 256, *bn = 128;
-    else if (wgs(128, 128) >= 240) *bm = 128, *bn = 128;
-    else if (wgs(128, 64) >= 240) *bm = 128, *bn = 64;
-    else *bm = 64, *bn = 64;
-}
-
-/* K-split count for a GEMM.  Decode rows (M <= 64): with one work-group per 32
- * columns a narrow N leaves most CUs idle, so K is cut into the fewest splits
- * (k-chunks a multiple of 64) that give about one work-group per CU.  More
- * rows: not split. */
+/* K-split count (measured on MI355X): K is cut into the fewest splits whose
+ * k-chunks (a multiple of 64) are at most 512 long, for decode rows (M <= 64,
+ * up to LMK_MAX_SPLIT splits) and for prefill GEMMs with fewer than 128 tiles
+ * of 64 x 64 (up to LMK_MAX_ROW_SPLIT); larger GEMMs are not split. */
 extern "C" int lmk_pick_split(int M, int N, int K)
 {
-    const int nb = (N + 31) / 32;
-    if (M > 64 || nb >= 192) return 1;
+    int cap = LMK_MAX_SPLIT;
+    if (M > 64) {
+        if ((long)((M + 63) / 64) * ((N + 63) / 64) >= 128) return 1;
+        cap = LMK_MAX_ROW_SPLIT;
+    }
     int best = 1;
-    for (int ns = 2; ns <= LMK_MAX_SPLIT; ns++) {
-        if (K % (64 * ns)) continue;
+    for (int ns = 1; ns <= cap; ns++) {
+        if (K % (BKH * ns)) continue;
         best = ns;
-        if (nb * ns >= 256) break;
+        if (K / ns <= 512) break;
     }
     return best;
 }
 
+/* The K-split GEMM on 64 x 64 tiles (grid: tiles x ns), or for decode rows
+ * whose chunks are not a multiple of 64 the skinny kernel. */
 extern "C" int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
                               int N, int K, int ns, float *part)
 {
@@ -1010,16 +957,8 @@ extern "C" int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const u
     EpiArgs e = {};
     e.M = M; e.N = N; e.out = part; e.ldc = N; e.nparts = (N + 31) / 32;
     e.sstride = (size_t)M * N;
-    if (M <= 64) {
-        launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
-        return hipGetLastError();
-    }
-    if (K % (BKH * ns)) return hipErrorInvalidValue;
-    int bm, bn;
-    split_tile(M, N, ns, &bm, &bn);
-    if (bm == 256) launch_tile_split<256, 128>(s, A, lda, W, M, N, K, ns, e);
-    else if (bn == 128) launch_tile_split<128, 128>(s, A, lda, W, M, N, K, ns, e);
-    else if (bm == 128) launch_tile_split<128, 64>(s, A, lda, W, M, N, K, ns, e);
-    else launch_tile_split<64, 64>(s, A, lda, W, M, N, K, ns, e);
+    if (K % (BKH * ns) == 0) launch_tile_split<64, 64>(s, A, lda, W, M, N, K, ns, e);
+    else if (M <= 64) launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -77,15 +77,6 @@ int lmk_ffn13(hipStream_t s, float *x, const float *rms_w,
 int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
                     int F, int B, float *x, const float *part, int nh);
 
-/* Decode rows after a K-split QKV GEMM: attention of head h, row b with q, k,
- * v summed from the ns partials part[s][b][..] (sstride floats apart) and
- * RoPE'd at pos[b]; k, v appended to the cache at (slot[b], pos[b]); the head
- * output to out16[b, h*hd ..] (fp16).  Replaces lmk_qkv_post + lmk_attn_decode
- * for decode rows. */
-int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int ns, int NQ, int NKV,
-                         const int *pos, const int *slot, int B, int H, int Hkv, int hd,
-                         int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
-                         void *vc, int kv_f32, uint16_t *out16);
 
 /* Attention of head h, row b, fused with that head's share of Wo:
  * part[(b*H + h)*D + r] = Wo[r, h*hd .. +hd] . attn(b, h) (D = H*hd, slot b =
@@ -147,24 +138,14 @@ typedef struct {
 int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
              int K, int epi, const LMEpilogue *ep);
 
-/* qkv [M, NQ+2*NKV] fp32 rows (the sum of ns partials sstride floats apart) ->
- * RoPE'd q [M, NQ], RoPE'd k and v appended to the cache at (slot[m], pos[m]). */
-int lmk_qkv_post(hipStream_t s, const float *qkv, int ns, size_t sstride, int M, int NQ, int NKV,
-                 int hd, int Hkv, int max_seq, const int *pos, const int *slot,
-                 const float *rope_cos, const float *rope_sin, float *q, void *kc, void *vc,
-                 int kv_f32);
 
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
- * A W^T.  Decode rows (M <= 64) run the skinny kernel, more rows the tiled
- * kernel; lmk_pick_split chooses ns for a shape (1: do not split). */
+ * A W^T; lmk_pick_split chooses ns for a shape (1: do not split). */
 #define LMK_MAX_SPLIT 16
 #define LMK_MAX_ROW_SPLIT 4    /* most splits lmk_pick_split gives for M > 64 */
 int lmk_pick_split(int M, int N, int K);
 int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                    int K, int ns, float *part);
-/* SwiGLU gate of ns K-split partials [M, 2F] (W1/W3 rows interleaved in blocks
- * of 16, as the GATE epilogue expects) to g [M, F] fp16. */
-int lmk_gate_post(hipStream_t s, const float *part, int ns, size_t sstride, int M, int F, uint16_t *g);
 
 /* One work-group per row: with emb != NULL x[m] is first set to the embedding row
  * emb[tok[m]]; with ns > 0 the ns partials sp[s][m] (sstride floats apart) of a

@@ -292,10 +292,8 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
     {
-        /* K-split partials of decode rows (widest: QKV or W1/W3), or one [R, D]
-         * product of prefill rows */
-        size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
-        if (2 * (size_t)F > w) w = 2 * (size_t)F;
+        /* K-split partials of the Wo and W2 products [ns][R][D] */
+        const size_t w = D;
         const size_t rd = r < 64 ? r : 64;
         size_t n = LMK_MAX_SPLIT * rd * w;
         if (r > 64 && LMK_MAX_ROW_SPLIT * r * w > n) n = LMK_MAX_ROW_SPLIT * r * w;
@@ -390,7 +388,7 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_tok, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
-    m->fuse_wo = lmk_attn_wo_supported(m->D, m->hd);
+    m->fuse_wo = 0;   /* measured slower at B = 1: 12 work-groups stream all of Wo */
     if ((st = dev_alloc((void **)&m->d_opart, (size_t)MAX_GEMV_B * m->H * D * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
     m->pl_grid = lmk_persist_grid();
@@ -643,10 +641,8 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
      * and the row norm that next reads x adds it (the residual add).  Only
      * unsplit decode rows keep the residual add in the GEMM epilogue. */
     const int dec = M <= 64;
-    const int ns_qkv = lmk_pick_split(M, NQKV, D);
     const int ns_wo = lmk_pick_split(M, D, NQ);
     const int ns_w2 = lmk_pick_split(M, D, F);
-    const int ns_w13 = lmk_pick_split(M, 2 * F, D);
     const int sep_wo = !dec || ns_wo > 1, sep_w2 = !dec || ns_w2 > 1;
     const float *pend = NULL;          /* W2 partials not yet added to x */
     int pend_ns = 0;
@@ -659,32 +655,15 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                          m->d_rms_att + (size_t)l * D, m->d_xn16));
         pend = NULL;
         pend_ns = 0;
-        int attn_done = 0;   /* attention already ran (fused with the QKV partials) */
+        /* QKV with RoPE and the K/V append in the GEMM epilogue (staged through
+         * LDS and stored row-contiguously); not K-split, since the partials'
+         * sum would put a memory round trip in front of the attention */
         memset(&ep, 0, sizeof(ep));
-        if (ns_qkv > 1) {
-            KCHK(lmk_gemm_split(s, m->d_xn16, D, lw, M, NQKV, D, ns_qkv, m->d_part));
-            if (dec && seq_rows == 1) {
-                /* decode rows: the attention kernel sums the partials, applies
-                 * RoPE and appends K/V itself */
-                KCHK(lmk_attn_decode_part(s, m->d_part, (size_t)M * NQKV, ns_qkv, NQ, NKV, pos, slot,
-                                          M, m->H, m->Hkv, m->hd, m->max_seq, m->d_rope_cos,
-                                          m->d_rope_sin, kc, vc, m->kv_f32, m->d_a16));
-                attn_done = 1;
-            } else {
-                KCHK(lmk_qkv_post(s, m->d_part, ns_qkv, (size_t)M * NQKV, M, NQ, NKV, m->hd,
-                                  m->Hkv, m->max_seq, pos, slot, m->d_rope_cos, m->d_rope_sin,
-                                  m->d_q, kc, vc, m->kv_f32));
-            }
-        } else {
-            /* unsplit: RoPE and the append fused into the GEMM epilogue (for
-             * prefill rows staged through LDS and stored row-contiguously) */
-            ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
-            ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
-            ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
-            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
-        }
-        if (attn_done) {
-        } else if (seq_rows > 1) {
+        ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
+        ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
+        ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
+        KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
+        if (seq_rows > 1) {
             KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
                                   M / seq_rows, m->H, m->Hkv, m->hd, m->max_seq, m->d_a16));
         } else {
@@ -708,16 +687,9 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             KCHK(lmk_rownorm(s, m->d_x, D, M, NULL, NULL, NULL, 0, 0,
                              m->d_rms_ffn + (size_t)l * D, m->d_xn16));
         }
-        if (ns_w13 > 1) {
-            /* too few 32-column blocks to fill the CUs: K-split partials, then
-             * the gate of their sums */
-            KCHK(lmk_gemm_split(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, ns_w13, m->d_part));
-            KCHK(lmk_gate_post(s, m->d_part, ns_w13, (size_t)M * 2 * F, M, F, m->d_g16));
-        } else {
-            memset(&ep, 0, sizeof(ep));
-            ep.g = m->d_g16; ep.F = F;
-            KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
-        }
+        memset(&ep, 0, sizeof(ep));
+        ep.g = m->d_g16; ep.F = F;
+        KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
         if (sep_w2) {
             if (ns_w2 > 1) {
                 KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));

@@ -217,10 +217,12 @@ int lm_timer_end(LMModel *m, float *ms);
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
-/* LM_OPT_FUSE_ATTN_WO: 1 (default where the shape allows it: D = H*hd with a
- * Wo head block of D x hd fp16 that fits in LDS, e.g. Stories) runs the batch
- * 1-4 chain's attention and Wo as one kernel per layer, each head adding its
- * share of the Wo product to the residual; 0 keeps two kernels. */
+/* LM_OPT_FUSE_ATTN_WO: 1 runs the batch 1-4 chain's attention and Wo as one
+ * kernel per layer, each head adding its share of the Wo product to the
+ * residual (where the shape allows it: D = H*hd with a Wo head block of D x hd
+ * fp16 that fits in LDS, e.g. Stories; otherwise LM_ERR_UNSUPPORTED).  0 (the
+ * default) keeps two kernels, which is faster on MI355X: the fused kernel has
+ * one work-group per head to stream all of Wo. */
 #define LM_OPT_FUSE_ATTN_WO 4
 int lm_set_option(LMModel *m, int option, int value);
 

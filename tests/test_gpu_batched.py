@@ -120,6 +120,23 @@ def test_prefill_chunks_whole_sequences(lm, orc):
     m.close()
 
 
+@pytest.mark.parametrize("name,d,kv32", [("gqa", TINY_GQA, False), ("hd128", TINY_HD128, True)])
+def test_prefill_many_sequences_matches_oracle(lm, orc, name, d, kv32):
+    """40 sequences of 50 tokens in one chunk: enough 128-query blocks for the
+    shared-tile attention kernel (fewer blocks take the wave-split kernel, as in
+    the tests above)."""
+    _say(f"[prefill many sequences {name}]")
+    n, P = 40, 50
+    m, w16 = make(lm, d, 44, n, 64, kv32)
+    toks = np.random.default_rng(44).integers(0, d["vocab_size"], (n, P)).astype(np.int32)
+    lg = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    w32 = lm.f16_to_f32(w16)
+    for i in (0, 17, 39):
+        ref = orc.Oracle(cfg7(d), w32, True, 64, kv_f16=not kv32).forward_full(toks[i])
+        close_enough(lg[i * P:(i + 1) * P], ref)
+    m.close()
+
+
 @pytest.mark.parametrize("B", [5, 16, 33, 64])
 def test_batched_decode_matches_oracle(lm, orc, B):
     """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
