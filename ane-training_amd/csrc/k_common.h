@@ -35,6 +35,11 @@ template <typename KT> __device__ __forceinline__ KT kv_pack(float v);
 template <> __device__ __forceinline__ u16 kv_pack<u16>(float v) { return f2h(v); }
 template <> __device__ __forceinline__ float kv_pack<float>(float v) { return v; }
 
+/* v as stored in a cache of element type KT, read back as fp32. */
+template <typename KT> __device__ __forceinline__ float kv_round(float v);
+template <> __device__ __forceinline__ float kv_round<u16>(float v) { return h2f(f2h(v)); }
+template <> __device__ __forceinline__ float kv_round<float>(float v) { return v; }
+
 /* 8 consecutive cache elements -> fp32 (one 16-byte or two 16-byte loads). */
 __device__ __forceinline__ void kv_load8(const u16 *p, float f[8]) { unpack8(*(const uint4 *)p, f); }
 __device__ __forceinline__ void kv_load8(const float *p, float f[8])

@@ -279,11 +279,27 @@ __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
  * running (max, sum, weighted V).  The four waves merge through LDS and the
  * normalised head output (forward.h:95-97) goes to out[b, h*HD ..] (fp32), or
  * in fp16 to out16 when that is given (the operand of the Wo GEMM). */
+/* Decode rows straight from a K-split QKV GEMM: part holds ns partials
+ * [M, NQ + 2*NKV] (sstride floats apart); the row's q, k, v are their sums in
+ * split order, q and k RoPE'd at pos[b] with the host tables (forward.h:55-70).
+ * The first query head of each kv group appends k, v to the cache
+ * (forward.h:118-128); every work-group takes the current position from its own
+ * copy (rounded to the cache's element type), as one more term of the softmax
+ * merge, so none waits for another's append. */
+template <typename KT>
+struct QkvPart {
+    const float *part;
+    size_t sstride;
+    int ns, NQ, NKV;
+    const float *rc, *rs;   /* RoPE cos / sin [max_seq][hd/2] */
+    KT *kc, *vc;            /* the cache, written at the current position */
+};
+
 template <int HD, typename KT, typename Hook>
 __device__ __forceinline__ void attn_head(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    float *oh, Hook after_first_loads)
+    float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
 {
     /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
      * would take 256 registers per lane */
@@ -294,10 +310,15 @@ __device__ __forceinline__ void attn_head(
     typedef typename KVRaw<KT>::T Raw;
     __shared__ float sm[NWAVE], sl[NWAVE];
     __shared__ __attribute__((aligned(16))) float so[NWAVE][HD];
+    __shared__ __attribute__((aligned(16))) float sqkv[3][HD];   /* q, k, v of a split QKV */
+    __shared__ float scur;                                        /* its current score */
     const int h = blockIdx.x, b = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ctx = pos[b] + 1;
-    const int ntiles = (ctx + TILE - 1) / TILE;
+    /* positions read from the cache: all of them, or with qp all but the
+     * current one, which is added from LDS at the end */
+    const int vis = qp ? ctx - 1 : ctx;
+    const int ntiles = (vis + TILE - 1) / TILE;
     const int dq = lane % G, pp = lane / G;
     const int cs = slot ? slot[b] : b;
     const size_t base = ((size_t)cs * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
@@ -305,7 +326,7 @@ __device__ __forceinline__ void attn_head(
     const KT *V = vc + base;
     const float scale = 1.0f / sqrtf((float)HD);
     float qf[8];
-    {
+    if (!qp) {
         const float *qr = q + (size_t)b * H * HD + h * HD + dq * 8;
         const float4 a = *(const float4 *)qr, c = *(const float4 *)(qr + 4);
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
@@ -327,6 +348,64 @@ __device__ __forceinline__ void attn_head(
             kv_raw_load(K + (size_t)p * HD, kr[i]);
             kv_raw_load(V + (size_t)p * HD, vr[i]);
         }
+        /* keeps the tile's loads ahead of the partials' (the scheduler would
+         * otherwise issue them after the partials' sum, a second round trip) */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (qp) {
+        /* q, k, v from the split partials, after the first K/V tile's loads:
+         * thread t < 3*HD/4 sums 4 columns of q, k or v over the partials (in
+         * split order, groups of four loaded at once), rotates q and k
+         * (forward.h:62-68), appends k, v to the cache from the first query head
+         * of the kv group (forward.h:118-128) and leaves them in LDS */
+        const int t = threadIdx.x;
+        if (t < 3 * HD / 4) {
+            const int vec = t / (HD / 4), e4 = (t % (HD / 4)) * 4;
+            const int g = h / (H / Hkv);
+            const int col = vec == 0 ? h * HD : (vec == 1 ? qp->NQ + g * HD : qp->NQ + qp->NKV + g * HD);
+            const float *src = qp->part + (size_t)b * (qp->NQ + 2 * qp->NKV) + col + e4;
+            const int ns = qp->ns;
+            const int ti = (ctx - 1) * (HD / 2) + (e4 >> 1);
+            const float2 c = *(const float2 *)(qp->rc + ti), sn = *(const float2 *)(qp->rs + ti);
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int s0 = 0; s0 < ns; s0 += 4) {
+                float4 tt[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) tt[u] = *(const float4 *)(src + (size_t)min(s0 + u, ns - 1) * qp->sstride);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {   /* past the last partial: add zero */
+                    const float4 z = s0 + u < ns ? tt[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    acc.x += z.x; acc.y += z.y; acc.z += z.z; acc.w += z.w;
+                }
+            }
+            if (vec < 2) {
+                const float a0 = acc.x, b0 = acc.y, a1 = acc.z, b1 = acc.w;
+                acc.x = fmaf(a0, c.x, -(b0 * sn.x));
+                acc.y = fmaf(a0, sn.x, b0 * c.x);
+                acc.z = fmaf(a1, c.y, -(b1 * sn.y));
+                acc.w = fmaf(a1, sn.y, b1 * c.y);
+            }
+            *(float4 *)(&sqkv[vec][e4]) = acc;
+            if (vec > 0 && h % (H / Hkv) == 0) {
+                KT *dst = (vec == 1 ? qp->kc : qp->vc) + ((size_t)cs * Hkv + g) * max_seq * HD +
+                          (size_t)(ctx - 1) * HD + e4;
+                dst[0] = kv_pack<KT>(acc.x);
+                dst[1] = kv_pack<KT>(acc.y);
+                dst[2] = kv_pack<KT>(acc.z);
+                dst[3] = kv_pack<KT>(acc.w);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; j++) qf[j] = sqkv[0][dq * 8 + j];
+        /* the current position's score, its k rounded as the cache would */
+        if (wv == 0) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = lane; j < HD; j += 64) d = fmaf(sqkv[0][j], kv_round<KT>(sqkv[1][j]), d);
+            d = wave_sum(d);
+            if (lane == 0) scur = d * scale;
+        }
     }
     /* loads issued here queue behind the first tile's (memory loads complete
      * in order for the wait counter), so waiting for that tile does not wait
@@ -337,7 +416,7 @@ __device__ __forceinline__ void attn_head(
 #pragma unroll
             for (int i = 0; i < NP; i++) {
                 const int p = t * TILE + pp + PP * i;
-                if (p < ctx) {
+                if (p < vis) {
                     kv_raw_load(K + (size_t)p * HD, kr[i]);
                     kv_raw_load(V + (size_t)p * HD, vr[i]);
                 } else {
@@ -358,7 +437,7 @@ __device__ __forceinline__ void attn_head(
 #pragma unroll
             for (int off = 1; off < G; off <<= 1) d += __shfl_xor(d, off, 64);
             const int p = t * TILE + pp + PP * i;
-            s[i] = p < ctx ? d * scale : -INFINITY;
+            s[i] = p < vis ? d * scale : -INFINITY;
             tmax = fmaxf(tmax, s[i]);
         }
 #pragma unroll
@@ -393,15 +472,20 @@ __device__ __forceinline__ void attn_head(
     __syncthreads();
     if (threadIdx.x < HD) {
         const int d = threadIdx.x;
-        float M = sm[0];
+        float M = qp ? scur : -INFINITY;
 #pragma unroll
-        for (int w = 1; w < NWAVE; w++) M = fmaxf(M, sm[w]);
+        for (int w = 0; w < NWAVE; w++) M = fmaxf(M, sm[w]);
         float L = 0.f, acc = 0.f;
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) {
             const float f = sm[w] == -INFINITY ? 0.f : expf(sm[w] - M);
             L = fmaf(sl[w], f, L);
             acc = fmaf(so[w][d], f, acc);
+        }
+        if (qp) {   /* the current position, after the cached ones */
+            const float f = expf(scur - M);
+            L += f;
+            acc = fmaf(kv_round<KT>(sqkv[2][d]), f, acc);
         }
         oh[d] = acc / L;
     }
@@ -423,6 +507,23 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
         if (out16) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
         else out[(size_t)b * H * HD + h * HD + d] = oh[d];
     }
+}
+
+/* Work-group (h, b) for decode rows of the MFMA path whose QKV GEMM ran
+ * K-split: q, k, v come from the partials (QkvPart), the head output goes to
+ * out16[b, h*HD ..] in fp16 (the Wo GEMM operand). */
+template <int HD, typename KT>
+__global__ void __launch_bounds__(WG) k_attn_decode_part(
+    const float *__restrict__ part, size_t sstride, int ns, int NQ, int NKV,
+    const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
+    const float *__restrict__ rc, const float *__restrict__ rs, KT *__restrict__ kc,
+    KT *__restrict__ vc, u16 *__restrict__ out16)
+{
+    __shared__ float oh[HD];
+    const QkvPart<KT> qp = {part, sstride, ns, NQ, NKV, rc, rs, kc, vc};
+    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, [] {}, &qp);
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    if (d < HD) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
 }
 
 /* ---- attention + Wo of one head ------------------------------------------------ */
@@ -823,6 +924,28 @@ extern "C" int lmk_attn_decode(hipStream_t s, const float *q, const void *kc, co
     else if (hd == 128) LAUNCH_ATTN(128, u16);
     else return hipErrorInvalidValue;
 #undef LAUNCH_ATTN
+    return hipGetLastError();
+}
+
+extern "C" int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int ns, int NQ,
+                                    int NKV, const int *pos, const int *slot, int B, int H, int Hkv,
+                                    int hd, int max_seq, const float *rope_cos, const float *rope_sin,
+                                    void *kc, void *vc, int kv_f32, uint16_t *out16)
+{
+    if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv || ns < 1 || NQ != H * hd ||
+        NKV != Hkv * hd || !part || !pos || !slot || !kc || !vc || !out16 || !rope_cos || !rope_sin)
+        return hipErrorInvalidValue;
+    dim3 grid(H, B);
+#define LAUNCH_ADP(HD_, KT_)                                                                      \
+    hipLaunchKernelGGL((k_attn_decode_part<HD_, KT_>), grid, dim3(WG), 0, s, part, sstride, ns, NQ, \
+                       NKV, pos, slot, H, Hkv, max_seq, rope_cos, rope_sin, (KT_ *)kc, (KT_ *)vc,  \
+                       (u16 *)out16)
+    if (hd == 64 && kv_f32) LAUNCH_ADP(64, float);
+    else if (hd == 64) LAUNCH_ADP(64, u16);
+    else if (hd == 128 && kv_f32) LAUNCH_ADP(128, float);
+    else if (hd == 128) LAUNCH_ADP(128, u16);
+    else return hipErrorInvalidValue;
+#undef LAUNCH_ADP
     return hipGetLastError();
 }
 

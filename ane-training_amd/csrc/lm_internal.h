@@ -139,6 +139,14 @@ int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M
              int K, int epi, const LMEpilogue *ep);
 
 
+/* Decode rows after a K-split QKV GEMM: attention of head h, row b with q, k,
+ * v summed from the ns partials part[s][b][..] (sstride floats apart) and
+ * RoPE'd at pos[b]; k, v appended to the cache at (slot[b], pos[b]); the head
+ * output to out16[b, h*hd ..] (fp16). */
+int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int ns, int NQ, int NKV,
+                         const int *pos, const int *slot, int B, int H, int Hkv, int hd,
+                         int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
+                         void *vc, int kv_f32, uint16_t *out16);
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
  * A W^T; lmk_pick_split chooses ns for a shape (1: do not split). */
 #define LMK_MAX_SPLIT 16

@@ -292,8 +292,9 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
     if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
     {
-        /* K-split partials of the Wo and W2 products [ns][R][D] */
-        const size_t w = D;
+        /* K-split partials (widest: QKV of decode rows), or one [R, D] product
+         * of prefill rows */
+        const size_t w = NQ + 2 * (size_t)m->NKV > D ? NQ + 2 * (size_t)m->NKV : D;
         const size_t rd = r < 64 ? r : 64;
         size_t n = LMK_MAX_SPLIT * rd * w;
         if (r > 64 && LMK_MAX_ROW_SPLIT * r * w > n) n = LMK_MAX_ROW_SPLIT * r * w;
@@ -641,6 +642,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
      * and the row norm that next reads x adds it (the residual add).  Only
      * unsplit decode rows keep the residual add in the GEMM epilogue. */
     const int dec = M <= 64;
+    const int ns_qkv = dec && seq_rows == 1 ? lmk_pick_split(M, NQKV, D) : 1;
     const int ns_wo = lmk_pick_split(M, D, NQ);
     const int ns_w2 = lmk_pick_split(M, D, F);
     const int sep_wo = !dec || ns_wo > 1, sep_w2 = !dec || ns_w2 > 1;
@@ -655,15 +657,25 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
                          m->d_rms_att + (size_t)l * D, m->d_xn16));
         pend = NULL;
         pend_ns = 0;
-        /* QKV with RoPE and the K/V append in the GEMM epilogue (staged through
-         * LDS and stored row-contiguously); not K-split, since the partials'
-         * sum would put a memory round trip in front of the attention */
-        memset(&ep, 0, sizeof(ep));
-        ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
-        ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
-        ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
-        KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
-        if (seq_rows > 1) {
+        if (ns_qkv > 1) {
+            /* decode rows, too few column tiles to fill the CUs: K-split QKV;
+             * the attention kernel sums the partials, applies RoPE and appends
+             * K/V itself */
+            KCHK(lmk_gemm_split(s, m->d_xn16, D, lw, M, NQKV, D, ns_qkv, m->d_part));
+            KCHK(lmk_attn_decode_part(s, m->d_part, (size_t)M * NQKV, ns_qkv, NQ, NKV, pos, slot, M,
+                                      m->H, m->Hkv, m->hd, m->max_seq, m->d_rope_cos,
+                                      m->d_rope_sin, kc, vc, m->kv_f32, m->d_a16));
+        } else {
+            /* QKV with RoPE and the K/V append in the GEMM epilogue (staged
+             * through LDS and stored row-contiguously) */
+            memset(&ep, 0, sizeof(ep));
+            ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
+            ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
+            ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
+            KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
+        }
+        if (ns_qkv > 1) {
+        } else if (seq_rows > 1) {
             KCHK(lmk_attn_prefill(s, m->d_q, kc, vc, m->kv_f32, pos, slot, seq_rows,
                                   M / seq_rows, m->H, m->Hkv, m->hd, m->max_seq, m->d_a16));
         } else {

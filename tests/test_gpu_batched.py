@@ -137,20 +137,17 @@ def test_prefill_many_sequences_matches_oracle(lm, orc, name, d, kv32):
     m.close()
 
 
-@pytest.mark.parametrize("B", [5, 16, 33, 64])
-def test_batched_decode_matches_oracle(lm, orc, B):
+def _batched_decode_vs_oracle(lm, orc, d, B, seed, kv32=False):
     """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
     decode path) against the oracle, then greedy runs."""
-    _say(f"[batched decode B={B}]")
-    d = TINY
-    m, w16 = make(lm, d, 44 + B, B, 80)
+    m, w16 = make(lm, d, seed, B, 80, kv32)
     w32 = lm.f16_to_f32(w16)
     rng = np.random.default_rng(B)
     P = 12
     seqs = rng.integers(0, d["vocab_size"], (B, P + 6)).astype(np.int32)
     m.prefill_batch(seqs[:, :P], mode=lm.LM_LOGITS_LAST, want_logits=False)
     check = sorted({0, B // 2, B - 1})
-    orcs = {b: orc.Oracle(cfg7(d), w32, True, 80, kv_f16=True) for b in check}
+    orcs = {b: orc.Oracle(cfg7(d), w32, True, 80, kv_f16=not kv32) for b in check}
     for b in check:
         orcs[b].forward_full(seqs[b, :P])           # fills the oracle's cache
         for t in range(P):
@@ -167,6 +164,24 @@ def test_batched_decode_matches_oracle(lm, orc, B):
         ref_ids, ref_lg = orcs[b].greedy(int(first[b]), P + 6, 20, want_logits=True)
         check_greedy(ids[:, b], ref_ids, ref_lg)
     m.close()
+
+
+@pytest.mark.parametrize("B", [5, 16, 33, 64])
+def test_batched_decode_matches_oracle(lm, orc, B):
+    _say(f"[batched decode B={B}]")
+    _batched_decode_vs_oracle(lm, orc, TINY, B, 44 + B)
+
+
+# dim 1024: the QKV GEMM of decode rows runs K-split and the attention kernel
+# sums its partials (RoPE and the K/V append included); head dim 128, GQA
+D1024 = dict(dim=1024, hidden_dim=1024, n_layers=2, n_heads=8, n_kv_heads=4, vocab_size=600, seq_len=96)
+
+
+@pytest.mark.parametrize("kv32", [False, True])
+def test_batched_decode_split_qkv_matches_oracle(lm, orc, kv32):
+    _say(f"[batched decode split QKV kv32={kv32}]")
+    assert lm.gemm_split_count(24, 2048, 1024) > 1
+    _batched_decode_vs_oracle(lm, orc, D1024, 24, 90, kv32)
 
 
 def test_batched_decode_graph_equals_direct(lm):
