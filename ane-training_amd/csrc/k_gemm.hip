@@ -190,7 +190,9 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
 /* ---- tiled GEMM (prefill) ------------------------------------------------- */
 
 #define BKH 64                 /* K (halves) per LDS stage: one 128-byte row per tile row */
-#define NSTAGE 3               /* LDS ring depth */
+#ifndef DEC_RING
+#define DEC_RING 4             /* LDS ring depth of decode-row (M <= 64) tiles (measured: 4 beats 3, 6 and 8) */
+#endif
 
 /* vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding). */
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 0xF) | ((((n) >> 4) & 3) << 14))
@@ -433,7 +435,7 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
     }
 }
 
-template <int BM, int BN, int E>
+template <int BM, int BN, int E, int NS>
 __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                   const u16 *__restrict__ W, int K, int kc,
                                                   EpiArgs e, int tm, int tn)
@@ -444,12 +446,25 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
     constexpr int STAGE = ROWS * 64;            /* halves per stage (128 B per row) */
     constexpr int LDW = ROWS / 8 / 4;           /* load instructions per wave per stage */
     static_assert(TM >= 1 && TN >= 1 && LDW >= 1 && ROWS % 32 == 0, "tile shape");
-    /* three separate arrays (not one indexed ring) so that the compiler can
-     * tell a stage's LDS reads from the direct loads in flight into the others
-     * and does not wait for those loads */
-    __shared__ __attribute__((aligned(1024))) u16 lds0[STAGE];
-    __shared__ __attribute__((aligned(1024))) u16 lds1[STAGE];
-    __shared__ __attribute__((aligned(1024))) u16 lds2[STAGE];
+    static_assert(NS >= 3 && NS <= 8 && LDW * (NS - 2) <= 63, "ring depth (vmcnt holds 63)");
+    /* the NS stage buffers are separate arrays (not one indexed ring) so that
+     * the compiler can tell a stage's LDS reads from the direct loads in flight
+     * into the others and does not wait for those loads */
+#define RING_BUF(i) __shared__ __attribute__((aligned(NS > i ? 1024 : 16))) u16 lds##i[NS > i ? STAGE : 8]
+    RING_BUF(0); RING_BUF(1); RING_BUF(2); RING_BUF(3);
+    RING_BUF(4); RING_BUF(5); RING_BUF(6); RING_BUF(7);
+#undef RING_BUF
+    auto ring = [&](auto I) -> u16 * {
+        constexpr int i = decltype(I)::value % NS;
+        if constexpr (i == 0) return lds0;
+        else if constexpr (i == 1) return lds1;
+        else if constexpr (i == 2) return lds2;
+        else if constexpr (i == 3) return lds3;
+        else if constexpr (i == 4) return lds4;
+        else if constexpr (i == 5) return lds5;
+        else if constexpr (i == 6) return lds6;
+        else return lds7;
+    };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -542,15 +557,23 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
             if (ks + 1 < BKH / 16) lds_wait_regs(f[(ks + 1) & 1]);
         });
     };
-    /* one k-stage: wait for this wave's loads of stage kt (at most the next
-     * stage's may still be outstanding), then a bare barrier (a fenced
-     * __syncthreads would wait for every outstanding load) so all waves' loads
-     * of stage kt have landed and stage kt-1's buffer is free for stage kt+2 */
+    /* one k-stage: wait for this wave's loads of stage kt (those of the up to
+     * NS-2 later stages in flight may still be outstanding), then a bare
+     * barrier (a fenced __syncthreads would wait for every outstanding load) so
+     * all waves' loads of stage kt have landed and stage kt-1's buffer is free
+     * for stage kt+NS-1 */
     const int nk = kc / BKH;
+    auto wait_stage = [&](int kt) {
+        const int later = min(NS - 2, nk - 1 - kt);   /* stages issued after kt */
+        static_for<0, NS - 1>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            if (later == NS - 2 - j) WAIT_VMCNT(LDW * (NS - 2 - j));
+        });
+    };
     auto step = [&](int kt, const u16 *cur, u16 *ahead) {
-        if (kt + 1 < nk) WAIT_VMCNT(LDW); else WAIT_VMCNT(0);
+        wait_stage(kt);
         __builtin_amdgcn_s_barrier();
-        compute(cur, ahead, kt + 2, kt + 2 < nk);
+        compute(cur, ahead, kt + NS - 1, kt + NS - 1 < nk);
     };
     /* positions and slots of a one-round tile's QKV epilogue, loaded first so
      * that they arrive during the main loop */
@@ -567,11 +590,16 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
         }
     }
     issue(lds0, 0);
-    if (nk > 1) issue(lds1, 1);
-    for (int kt = 0; kt < nk; kt += NSTAGE) {
-        step(kt, lds0, lds2);
-        if (kt + 1 < nk) step(kt + 1, lds1, lds0);
-        if (kt + 2 < nk) step(kt + 2, lds2, lds1);
+    static_for<1, NS - 1>([&](auto I) {
+        if (decltype(I)::value < nk) issue(ring(I), decltype(I)::value);
+    });
+    for (int kt = 0; kt < nk; kt += NS) {
+        static_for<0, NS>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if (kt + i < nk)
+                step(kt + i, ring(std::integral_constant<int, i>{}),
+                     ring(std::integral_constant<int, i + NS - 1>{}));
+        });
     }
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
     if constexpr (E == EPI_GATE) {
@@ -864,13 +892,27 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     return e;
 }
 
+/* LDS ring depth: 3 stages where several work-groups share a CU (prefill),
+ * deeper for decode rows (M <= 64), whose few work-groups per CU need more
+ * weight bytes in flight each to cover the memory latency. */
+template <int BM, int BN>
+static constexpr int ring_depth(bool rows64)
+{
+    constexpr int fit = 160 * 1024 / ((BM + BN) * 128);   /* stages that fit the LDS */
+    return BM == 64 && rows64 ? (DEC_RING < fit ? DEC_RING : fit) : 3;
+}
+
 template <int BM, int BN, int E>
 static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                         int K, const EpiArgs &e)
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm_tile<BM, BN, E>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A, lda,
-                       (const u16 *)W, K, K, e, tm, tn);
+    if (M <= 64 && BM == 64)
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true)>), dim3(tm * tn), dim3(GT), 0,
+                           s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+    else
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
+                           lda, (const u16 *)W, K, K, e, tm, tn);
 }
 
 /* The tiled kernel over grid (tiles, ns), split y taking k-chunk y*K/ns. */
@@ -879,8 +921,12 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
                               int N, int K, int ns, const EpiArgs &e)
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE>), dim3(tm * tn, ns), dim3(GT), 0, s,
-                       (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
+    if (M <= 64 && BM == 64)
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, ring_depth<BM, BN>(true)>), dim3(tm * tn, ns),
+                           dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
+    else
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, 3>), dim3(tm * tn, ns), dim3(GT), 0, s,
+                           (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
 }
 
 /* Tile choice (measured on MI355X over the Stories and scaled-model shapes):
