@@ -25,6 +25,31 @@
  */
 #include "k_common.h"
 #include "lm_internal.h"
+#include <hip/hip_ext.h>
+
+/* Launch-timing slot for lm_profile_chain: when armed, the next decode-chain
+ * kernel launch of this host thread goes through hipExtLaunchKernelGGL with the
+ * two events, which the device timestamps at that dispatch's start and end
+ * (the kernel's own duration, as a kernel trace reports it). */
+static thread_local hipEvent_t t_ev0, t_ev1;
+static thread_local int t_armed;
+
+extern "C" void lmk_time_next(hipEvent_t start, hipEvent_t stop)
+{
+    t_ev0 = start;
+    t_ev1 = stop;
+    t_armed = 1;
+}
+
+#define DLAUNCH(K, grid, block, shm, s, ...)                                          \
+    do {                                                                             \
+        if (t_armed) {                                                               \
+            t_armed = 0;                                                             \
+            hipExtLaunchKernelGGL(K, grid, block, shm, s, t_ev0, t_ev1, 0, __VA_ARGS__); \
+        } else {                                                                     \
+            hipLaunchKernelGGL(K, grid, block, shm, s, __VA_ARGS__);                 \
+        }                                                                            \
+    } while (0)
 
 #define WG 256
 #define NWAVE (WG / 64)
@@ -898,11 +923,11 @@ extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const 
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
         if (kv_f32)
-            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, float>), grid, dim3(WG), 0, s, x, emb, tok,
+            DLAUNCH((k_qkv_rope<K_, NB_, float>), grid, dim3(WG), 0, s, x, emb, tok,
                                rms_w, wqkv, NQ, NKV, hd, rope_cos, rope_sin, pos, B, q,
                                (float *)kc, (float *)vc, max_seq, npairs);
         else
-            hipLaunchKernelGGL((k_qkv_rope<K_, NB_, u16>), grid, dim3(WG), 0, s, x, emb, tok,
+            DLAUNCH((k_qkv_rope<K_, NB_, u16>), grid, dim3(WG), 0, s, x, emb, tok,
                                rms_w, wqkv, NQ, NKV, hd, rope_cos, rope_sin, pos, B, q,
                                (u16 *)kc, (u16 *)vc, max_seq, npairs);
     }));
@@ -916,7 +941,7 @@ extern "C" int lmk_attn_decode(hipStream_t s, const float *q, const void *kc, co
     if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv) return hipErrorInvalidValue;
     dim3 grid(H, B);
 #define LAUNCH_ATTN(HD_, KT_)                                                                  \
-    hipLaunchKernelGGL((k_attn_decode<HD_, KT_>), grid, dim3(WG), 0, s, q, (const KT_ *)kc,   \
+    DLAUNCH((k_attn_decode<HD_, KT_>), grid, dim3(WG), 0, s, q, (const KT_ *)kc,   \
                        (const KT_ *)vc, pos, slot, H, Hkv, max_seq, out, (u16 *)out16)
     if (hd == 64 && kv_f32) LAUNCH_ATTN(64, float);
     else if (hd == 64) LAUNCH_ATTN(64, u16);
@@ -957,7 +982,7 @@ extern "C" int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t 
     dim3 grid((npairs + NWAVE - 1) / NWAVE);
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_wo_residual<K_, NB_>), grid, dim3(WG), 0, s, attn, wo, B, x, npairs);
+        DLAUNCH((k_wo_residual<K_, NB_>), grid, dim3(WG), 0, s, attn, wo, B, x, npairs);
     }));
     return hipGetLastError();
 }
@@ -969,7 +994,7 @@ extern "C" int lmk_ffn13(hipStream_t s, float *x, const float *rms_w, const uint
     dim3 grid((F + NWAVE - 1) / NWAVE);
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_ffn13<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, w13, F, B, g, part, nh);
+        DLAUNCH((k_ffn13<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, w13, F, B, g, part, nh);
     }));
     return hipGetLastError();
 }
@@ -982,7 +1007,7 @@ extern "C" int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2
     dim3 grid((npairs + NWAVE - 1) / NWAVE);
     DISPATCH_K(F, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_w2_residual<K_, NB_>), grid, dim3(WG), 0, s, g, w2, D, B, x, npairs,
+        DLAUNCH((k_w2_residual<K_, NB_>), grid, dim3(WG), 0, s, g, w2, D, B, x, npairs,
                            part, nh);
     }));
     return hipGetLastError();
@@ -1007,11 +1032,11 @@ extern "C" int lmk_attn_wo(hipStream_t s, const float *q, const void *kc, const 
 #define LAUNCH_AWO(HD_, D_)                                                                       \
     do {                                                                                          \
         if (kv_f32)                                                                               \
-            hipLaunchKernelGGL((k_attn_wo<HD_, float, D_>), grid, dim3(WG), 0, s, q,             \
+            DLAUNCH((k_attn_wo<HD_, float, D_>), grid, dim3(WG), 0, s, q,             \
                                (const float *)kc, (const float *)vc, pos, H, Hkv, max_seq,       \
                                (const u16 *)wo, part);                                            \
         else                                                                                      \
-            hipLaunchKernelGGL((k_attn_wo<HD_, u16, D_>), grid, dim3(WG), 0, s, q,               \
+            DLAUNCH((k_attn_wo<HD_, u16, D_>), grid, dim3(WG), 0, s, q,               \
                                (const u16 *)kc, (const u16 *)vc, pos, H, Hkv, max_seq,           \
                                (const u16 *)wo, part);                                            \
     } while (0)
@@ -1034,7 +1059,7 @@ extern "C" int lmk_cls(hipStream_t s, const float *x, const float *rms_w, const 
     dim3 grid(lmk_cls_nblk(V));
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_cls<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, wcls, V, B, logits,
+        DLAUNCH((k_cls<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, wcls, V, B, logits,
                            part);
     }));
     return hipGetLastError();
@@ -1044,7 +1069,7 @@ extern "C" int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, 
                                 int *pos, int *hist, int hist_stride)
 {
     if (B < 1 || nblk < 1 || !tok || (hist && !pos)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_argmax_final, dim3(B), dim3(WG), 0, s, part, nblk, tok, pos, hist,
+    DLAUNCH(k_argmax_final, dim3(B), dim3(WG), 0, s, part, nblk, tok, pos, hist,
                        hist_stride);
     return hipGetLastError();
 }

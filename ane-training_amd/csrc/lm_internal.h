@@ -147,6 +147,10 @@ int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int n
                          const int *pos, const int *slot, int B, int H, int Hkv, int hd,
                          int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
                          void *vc, int kv_f32, uint16_t *out16);
+/* Arm the calling thread's next decode-chain kernel launch (qkv_rope, attn,
+ * attn_wo, wo_residual, ffn13, w2_residual, cls, argmax_final) to be timed
+ * with these two events at its dispatch's start and end. */
+void lmk_time_next(hipEvent_t start, hipEvent_t stop);
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
  * A W^T; lmk_pick_split chooses ns for a shape (1: do not split). */
 #define LMK_MAX_SPLIT 16

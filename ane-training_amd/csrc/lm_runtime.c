@@ -1179,6 +1179,75 @@ int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int 
     return rc;
 }
 
+int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int steps,
+                     float *us_per_launch, int *launches_per_step)
+{
+    static const int fams[5] = {LM_KERN_QKV, LM_KERN_ATTN, LM_KERN_WO, LM_KERN_W13, LM_KERN_W2};
+    if (!m || !tokens || !pos || !us_per_launch || B < 1 || steps < 1) return LM_ERR_INVALID;
+    if (B > m->max_batch) return LM_ERR_RANGE;
+    if (B > MAX_GEMV_B) return LM_ERR_UNSUPPORTED;
+    int rc = check_tok_pos(m, tokens, pos, B);
+    if (rc) return rc;
+    for (int b = 0; b < B; b++)
+        if (pos[b] + steps + 1 > m->max_seq) return LM_ERR_RANGE;
+    /* kernels of one step: 5 per layer (Wo none when fused), then cls, argmax */
+    const int nk = 5 * m->L + 2;
+    hipEvent_t *ev = (hipEvent_t *)calloc(2 * (size_t)nk, sizeof(hipEvent_t));
+    int *kfam = (int *)calloc((size_t)nk, sizeof(int));
+    double sum[LM_KERN_COUNT] = {0};
+    int cnt[LM_KERN_COUNT] = {0};
+    if (!ev || !kfam) rc = LM_ERR_OOM;
+    for (int i = 0; i < 2 * nk && rc == LM_OK; i++)
+        if (hipEventCreate(&ev[i]) != hipSuccess) rc = LM_ERR_HIP;
+    int *hio = m->h_io;
+    if (rc == LM_OK) {
+        memcpy(hio, tokens, B * 4);
+        memcpy(hio + B, pos, B * 4);
+        if (hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+            hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
+            rc = LM_ERR_HIP;
+    }
+    for (int st = 0; st <= steps && rc == LM_OK; st++) {   /* step 0 untimed */
+        int k = 0;
+        for (int l = 0; l < m->L && rc == LM_OK; l++)
+            for (int f = 0; f < 5 && rc == LM_OK; f++) {
+                if (fams[f] == LM_KERN_WO && m->fuse_wo) continue;
+                kfam[k] = fams[f];
+                lmk_time_next(ev[2 * k], ev[2 * k + 1]);
+                rc = enqueue_kernel(m, B, fams[f], l, NULL);
+                k++;
+            }
+        for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
+            kfam[k] = f;
+            lmk_time_next(ev[2 * k], ev[2 * k + 1]);
+            rc = enqueue_kernel(m, B, f, 0, NULL);
+            k++;
+        }
+        if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
+        for (int i = 0; i < k && rc == LM_OK && st > 0; i++) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = LM_ERR_HIP;
+            sum[kfam[i]] += ms;
+            cnt[kfam[i]]++;
+        }
+    }
+    for (int f = 0; f < LM_KERN_COUNT; f++) {
+        us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
+        if (launches_per_step)
+            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX
+                                       ? 1
+                                       : (f == LM_KERN_WO && m->fuse_wo ? 0 : m->L);
+    }
+    for (int i = 0; ev && i < 2 * nk; i++)
+        if (ev[i]) hipEventDestroy(ev[i]);
+    free(ev);
+    free(kfam);
+    if (rc == LM_OK)
+        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return rc;
+}
+
 /* Diagnostics: one MFMA GEMM C = A W^T on caller data (plain store epilogue
  * with argmax partials).  A is fp16 bits [M, K] (a_f32 == 0) or fp32 [M, K];
  * W fp16 bits [N, K]; C fp32 [M, N]; part (may be NULL) [M, ceil(N/32)]. */

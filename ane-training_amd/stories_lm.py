@@ -238,6 +238,7 @@ def lib():
         "lm_rope_table": (I, [I, I, fp, fp]),
         "lm_selftest_reduce": (I, [fp, fp]),
         "lm_profile_decode": (I, [P, I, ip, ip, I, fp, ip]),
+        "lm_profile_chain": (I, [P, I, ip, ip, I, fp, ip]),
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
         "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
         "lm_gemm_split_count": (I, [I, I, I]),
@@ -551,6 +552,19 @@ class Model:
         n = np.zeros(len(KERN_NAMES), dtype=np.int32)
         rc = lib().lm_profile_decode(self._h, t.size, _ip(t), _ip(p), reps, _fp(us), _ip(n))
         self._check(rc, "lm_profile_decode")
+        return dict(zip(KERN_NAMES, us.tolist())), dict(zip(KERN_NAMES, n.tolist()))
+
+    def profile_chain(self, tokens, pos, steps=8):
+        """Mean device microseconds per launch of each decode kernel family in
+        `steps` real decode steps (direct launches, each kernel timed by events
+        at its own dispatch's start and end).  Returns (us_per_launch,
+        launches_per_step), dicts keyed by KERN_NAMES."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        p = np.ascontiguousarray(pos, dtype=np.int32)
+        us = np.zeros(len(KERN_NAMES), dtype=np.float32)
+        n = np.zeros(len(KERN_NAMES), dtype=np.int32)
+        rc = lib().lm_profile_chain(self._h, t.size, _ip(t), _ip(p), steps, _fp(us), _ip(n))
+        self._check(rc, "lm_profile_chain")
         return dict(zip(KERN_NAMES, us.tolist())), dict(zip(KERN_NAMES, n.tolist()))
 
     def timer_end(self) -> float:

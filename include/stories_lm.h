@@ -312,6 +312,16 @@ int lm_gemm_split_count(int M, int N, int K);
 int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
                       float *us_per_launch, int *launches_per_step);
 
+/* Mean device microseconds per launch of each decode kernel family inside the
+ * real decode chain: `steps` greedy decode steps of B rows from tokens[b] at
+ * positions pos[b] (advancing as a decode does), launched directly, every
+ * kernel timed by events at its own dispatch's start and end (the durations a
+ * kernel trace reports).  One untimed step runs first.  launches_per_step as in
+ * lm_profile_decode.  Needs pos[b] + steps + 1 <= max_seq; leaves the KV cache
+ * at those positions and the activations overwritten. */
+int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int steps,
+                     float *us_per_launch, int *launches_per_step);
+
 /* ---------------------------------------------------------------------------
  * Text: tokenizer, random stream, samplers (host only, no device needed)
  * ------------------------------------------------------------------------- */

@@ -180,3 +180,26 @@ def test_graph_replay_equals_direct_launches(lm):
         assert np.array_equal(x, y)
     m.close()
     m2.close()
+
+
+@pytest.mark.parametrize("fuse", [0, 1])
+def test_profile_chain_times_every_family(lm, fuse):
+    """lm_profile_chain: every kernel of real decode steps timed at its own
+    dispatch; positive durations, the launch counts of a step, and the range
+    check on the positions it advances through."""
+    _say(f"[profile chain fuse{fuse}]")
+    d = TINY
+    m, _ = make(lm, d, 25, 1, 64, True)
+    m.set_option(lm.LM_OPT_FUSE_ATTN_WO, fuse)
+    us, n = m.profile_chain([1], [20], 6)
+    L = d["n_layers"]
+    assert n == {"qkv": L, "attn": L, "wo": 0 if fuse else L, "w13": L, "w2": L, "cls": 1, "argmax": 1}
+    for k in us:
+        assert (us[k] > 0) == (n[k] > 0), k
+        assert us[k] < 1e4, k
+    with pytest.raises(lm.LMError):
+        m.profile_chain([1], [60], 6)      # 60 + 6 + 1 > max_seq 64
+    # the model still decodes afterwards
+    row = m.forward(1, 0)
+    assert np.all(np.isfinite(row))
+    m.close()
