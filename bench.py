@@ -12,10 +12,11 @@ the argmax fed back on the device, inputs and weights already resident in HBM.
 Alongside the headline the JSON line carries:
   roofline      the dominant kernel family of the decode step (largest device
                 time per token): algorithmic bytes per launch / mean launch
-                duration, measured after the timed region over 16 decode steps
-                of the same chain, each kernel launched with hipEvents at its
-                own dispatch's start and end (lm_profile_chain), so the
-                durations are those of a kernel trace of the chain
+                duration, measured after the timed region over the 254 decode
+                steps of one sequence of the same chain, each kernel launched
+                with hipEvents at its own dispatch's start and end
+                (lm_profile_chain), so the durations are those of a kernel
+                trace of the chain
   step_roofline the whole token: algorithmic bytes per token / time per token
   cpu_baseline  the CPU oracle (a C restatement of the reference's fp32
                 forward, KV-cache decode) timed on this host on the same C0
@@ -240,10 +241,10 @@ def main():
     tok_s = steps / (ms / 1e3)
     us_tok = ms * 1e3 / steps
 
-    # device time per launch of each kernel family inside the decode chain, around
-    # the run's mean context (16 steps from position 120): every kernel timed by
-    # hipEvents at its own dispatch's start and end, as a kernel trace reports it
-    us, launches = m.profile_chain([1], [SEQ // 2 - 8], 16)
+    # device time per launch of each kernel family inside the decode chain over the
+    # positions of a timed sequence (254 steps from position 0): every kernel timed
+    # by hipEvents at its own dispatch's start and end, as a kernel trace reports it
+    us, launches = m.profile_chain([1], [0], SEQ - 2)
     mean_ctx = (SEQ + 1) / 2
     kvb = 2 if args.kv16 else 4
     algo = algorithmic_bytes(cfg, 1, mean_ctx, kvb)
