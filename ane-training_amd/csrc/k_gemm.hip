@@ -287,10 +287,11 @@ __device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
  * BN/2 gates, then written with one 16-byte store per 8 gates instead of one
  * 2-byte store per gate.  sg: LDS of at least BM * (BN/2 + 8) halves, no longer
  * read by any wave's main loop. */
-template <int BM, int BN, int TM, int TN>
+template <int BM, int BN, int TM, int TN, int WVM>
 __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *sg, int m0, int n0,
                                               int wm, int wn, const EpiArgs &e)
 {
+    constexpr int NT = 128 * WVM;   /* threads: WVM x 2 waves */
     constexpr int GW = BN / 2, GLD = GW + 8;
     const int lane = threadIdx.x & 63, c = lane & 31;
     const bool lo = c < 16;
@@ -299,7 +300,7 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int rl = wm * (BM / 2) + i * 32 + 4 * (lane >> 5);
+            const int rl = wm * (BM / WVM) + i * 32 + 4 * (lane >> 5);
             const int gl = (wn * (BN / 2) + j * 32) / 2 + (c & 15);
 #pragma unroll
             for (int k = 0; k < 16; k += 2) {
@@ -317,7 +318,7 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
     __syncthreads();
     constexpr int CPR = GW / 8;   /* 16-byte chunks per row */
 #pragma unroll
-    for (int idx = threadIdx.x; idx < BM * CPR; idx += GT) {
+    for (int idx = threadIdx.x; idx < BM * CPR; idx += NT) {
         const int r = idx / CPR, ch = idx % CPR;
         const int row = m0 + r, gi = n0 / 2 + ch * 8;
         if (row < e.M && gi < e.F)
@@ -435,17 +436,20 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
     }
 }
 
-template <int BM, int BN, int E, int NS>
-__global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int lda,
-                                                  const u16 *__restrict__ W, int K, int kc,
-                                                  EpiArgs e, int tm, int tn)
+template <int BM, int BN, int E, int NS, int WVM>
+__global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__ A, int lda,
+                                                         const u16 *__restrict__ W, int K, int kc,
+                                                         EpiArgs e, int tm, int tn)
 {
-    constexpr int WM = BM / 2, WN = BN / 2;     /* wave tile, waves 2 x 2 */
+    constexpr int NWV = 2 * WVM;                /* waves: WVM along M x 2 along N */
+    constexpr int WM = BM / WVM, WN = BN / 2;   /* wave tile */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
     constexpr int ROWS = BM + BN;               /* tile rows per stage */
     constexpr int STAGE = ROWS * 64;            /* halves per stage (128 B per row) */
-    constexpr int LDW = ROWS / 8 / 4;           /* load instructions per wave per stage */
-    static_assert(TM >= 1 && TN >= 1 && LDW >= 1 && ROWS % 32 == 0, "tile shape");
+    constexpr int LDW = ROWS / 8 / NWV;         /* load instructions per wave per stage */
+    static_assert(TM >= 1 && TN >= 1 && LDW >= 1 && ROWS % (8 * NWV) == 0, "tile shape");
+    /* the LDS-staged QKV epilogue is written for four waves */
+    static_assert(WVM == 2 || E != EPI_QKV, "wave layout");
     static_assert(NS >= 3 && NS <= 8 && LDW * (NS - 2) <= 63, "ring depth (vmcnt holds 63)");
     /* the NS stage buffers are separate arrays (not one indexed ring) so that
      * the compiler can tell a stage's LDS reads from the direct loads in flight
@@ -604,7 +608,7 @@ __global__ void __launch_bounds__(GT) k_gemm_tile(const u16 *__restrict__ A, int
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
     if constexpr (E == EPI_GATE) {
         static_assert(BM * (BN / 2 + 8) <= STAGE, "gate staging fits one stage buffer");
-        gate_tile_lds<BM, BN, TM, TN>(acc, lds0, m0, n0, wm, wn, e);
+        gate_tile_lds<BM, BN, TM, TN, WVM>(acc, lds0, m0, n0, wm, wn, e);
         return;
     }
     if constexpr (QKV_LDS) {
@@ -907,12 +911,17 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
                         int K, const EpiArgs &e)
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    if (M <= 64 && BM == 64)
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true)>), dim3(tm * tn), dim3(GT), 0,
-                           s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
-    else
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
+    if constexpr (BM == 256 && E != EPI_QKV) {   /* eight waves (4 x 2): two per SIMD */
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 4>), dim3(tm * tn), dim3(512), 0, s, (const u16 *)A,
                            lda, (const u16 *)W, K, K, e, tm, tn);
+    } else {
+        if (M <= 64 && BM == 64)
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2>), dim3(tm * tn),
+                               dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+        else
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
+                               lda, (const u16 *)W, K, K, e, tm, tn);
+    }
 }
 
 /* The tiled kernel over grid (tiles, ns), split y taking k-chunk y*K/ns. */
@@ -922,10 +931,10 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
     if (M <= 64 && BM == 64)
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, ring_depth<BM, BN>(true)>), dim3(tm * tn, ns),
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, ring_depth<BM, BN>(true), 2>), dim3(tm * tn, ns),
                            dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
     else
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, 3>), dim3(tm * tn, ns), dim3(GT), 0, s,
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, EPI_STORE, 3, 2>), dim3(tm * tn, ns), dim3(GT), 0, s,
                            (const u16 *)A, lda, (const u16 *)W, K, K / ns, e, tm, tn);
 }
 
