@@ -20,7 +20,9 @@ Alongside the headline the JSON line carries:
   step_roofline the whole token: algorithmic bytes per token / time per token
   cpu_baseline  the CPU oracle (a C restatement of the reference's fp32
                 forward, KV-cache decode) timed on this host on the same C0
-                run; its greedy ids are compared with the GPU's
+                run; its greedy ids are compared with the GPU's.  Under
+                "configs": bounded samples of C0 in the reference's own
+                algorithm (full-window recompute per token), C1 and C3
 """
 import argparse
 import json
@@ -72,6 +74,42 @@ def cpu_baseline(cfg7, w16, S, n_tokens):
             "kind": "port",
             "sample": f"C0 first {n_tokens} greedy tokens from id 1, KV-cache decode, fp32 "
                       f"(oracle/oracle.c restating training/forward.h), {dt:.1f} s"}, ids
+
+
+def cpu_extra(cfg7, w16, S, ids):
+    """Bounded CPU samples of the other baselines, with the same oracle: C0 in
+    the reference's own algorithm (every token recomputes the full 256-position
+    window, BOS + context zero-padded, classifier on one row: generate.m:427-516),
+    C1 (one 256-token prompt, all logits) and C3 (2 of its 8 prompts)."""
+    import oracle as O
+    o = O.Oracle(cfg7, S.f16_to_f32(w16), True, SEQ)
+    out = {}
+    win = np.zeros(SEQ, np.int32)
+    win[0] = 1
+    win[1:1 + min(len(ids), SEQ - 1)] = ids[:SEQ - 1]
+    n = 2
+    t0 = time.perf_counter()
+    for _ in range(n):
+        o.forward_last(win)
+    dt = time.perf_counter() - t0
+    out["c0_reference_algorithm"] = {
+        "value": round(n / dt, 3), "unit": "tok/s",
+        "sample": f"{n} tokens, each a full {SEQ}-position window forward + last-row classifier, {dt:.1f} s"}
+    toks = np.random.default_rng(101).integers(0, 32000, SEQ).astype(np.int32)
+    t0 = time.perf_counter()
+    o.forward_full(toks)
+    dt = time.perf_counter() - t0
+    out["c1_prefill_256"] = {"value": round(SEQ / dt, 1), "unit": "tok/s", "ms": round(dt * 1e3, 1),
+                             "sample": "one 256-token prompt, all 256 x 32000 logits"}
+    toks = np.random.default_rng(103).integers(0, 32000, (8, SEQ)).astype(np.int32)
+    t0 = time.perf_counter()
+    for i in range(2):
+        o.forward_full(toks[i])
+    dt = time.perf_counter() - t0
+    out["c3_forward_8x256"] = {"value": round(2 * SEQ / dt, 1), "unit": "tok/s",
+                               "sample": f"2 of the 8 prompts of 256 tokens, all logits, {dt:.1f} s"}
+    o.close()
+    return out
 
 
 MFMA_PEAK_TFLOPS = 2500.0      # dense fp16
@@ -282,6 +320,7 @@ def main():
     if not args.no_cpu:
         cb, cpu_ids = cpu_baseline(cfg.astuple(), w16, S, args.cpu_tokens)
         cb["ids_match_gpu"] = bool(np.array_equal(cpu_ids, ids[:args.cpu_tokens]))
+        cb["configs"] = cpu_extra(cfg.astuple(), w16, S, ids)
         out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
 

@@ -264,9 +264,10 @@ static void round_kv(float *a, size_t n)
 
 /* The layer stack and classifier over S rows at positions pos0..pos0+S-1.
  * mode_full: attention over the S rows themselves (forward.h:127-128);
- * otherwise S == 1 and attention reads the cache (dashboard.py:236-251). */
+ * otherwise S == 1 and attention reads the cache (dashboard.py:236-251).
+ * last_only: the classifier of the last row only (generate.m:474-487). */
 static int forward_rows(OracleModel *o, const int *tokens, int S, int pos0, int mode_full,
-                        float *logits)
+                        int last_only, float *logits)
 {
     const int D = o->D, F = o->F, NQ = o->NQ, NKV = o->NKV, hd = o->hd;
     const size_t s = (size_t)S;
@@ -310,7 +311,10 @@ static int forward_rows(OracleModel *o, const int *tokens, int S, int pos0, int 
         for (size_t i = 0; i < s * D; i++) x[i] += o_out[i];       /* :159 */
     }
     oracle_rmsnorm(xn, x, o->rms_final, S, D);                     /* :164 */
-    matmul_T(o->wclsT, xn, logits, S, D, o->V);                    /* :169 */
+    if (last_only)
+        matmul_T(o->wclsT, xn + (s - 1) * D, logits, 1, D, o->V);  /* generate.m:486 */
+    else
+        matmul_T(o->wclsT, xn, logits, S, D, o->V);                /* :169 */
 done:
     free(x); free(xn); free(q); free(k); free(v); free(att); free(o_out); free(h1); free(h3);
     return rc;
@@ -321,14 +325,22 @@ int oracle_forward_full(OracleModel *o, const int *tokens, int S, float *logits)
     if (!o || !tokens || !logits || S < 1) return -3;
     for (int t = 0; t < S; t++)
         if (tokens[t] < 0 || tokens[t] >= o->V) return -8;
-    return forward_rows(o, tokens, S, 0, 1, logits);
+    return forward_rows(o, tokens, S, 0, 1, 0, logits);
+}
+
+int oracle_forward_last(OracleModel *o, const int *tokens, int S, float *logits)
+{
+    if (!o || !tokens || !logits || S < 1) return -3;
+    for (int t = 0; t < S; t++)
+        if (tokens[t] < 0 || tokens[t] >= o->V) return -8;
+    return forward_rows(o, tokens, S, 0, 1, 1, logits);
 }
 
 int oracle_decode_step(OracleModel *o, int token, int pos, float *logits)
 {
     if (!o || !logits) return -3;
     if (token < 0 || token >= o->V || pos < 0 || pos >= o->max_seq) return -8;
-    return forward_rows(o, &token, 1, pos, 0, logits);
+    return forward_rows(o, &token, 1, pos, 0, 0, logits);
 }
 
 /* training/forward.h:174-183 */

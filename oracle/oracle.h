@@ -41,6 +41,11 @@ void oracle_free(OracleModel *o);
  * logits [S, vocab] row-major (training/forward.h:104-170). */
 int oracle_forward_full(OracleModel *o, const int *tokens, int S, float *logits);
 
+/* The same forward with the classifier applied to the last row only, logits
+ * [vocab]: the reference's per-token window recompute (generate.m:437-487,
+ * cblas_sgemv on the last position). */
+int oracle_forward_last(OracleModel *o, const int *tokens, int S, float *logits);
+
 /* Mode (ii): one KV-cache decode step of `token` at `pos`; positions < pos
  * must have been stepped before (training/dashboard.py:205-267 with
  * forward.h's arithmetic).  logits [vocab]. */

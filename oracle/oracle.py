@@ -28,6 +28,7 @@ def lib():
             "oracle_create": (P, [ip, fp, I, I, I]),
             "oracle_free": (None, [P]),
             "oracle_forward_full": (I, [P, ip, I, fp]),
+            "oracle_forward_last": (I, [P, ip, I, fp]),
             "oracle_decode_step": (I, [P, I, I, fp]),
             "oracle_loss": (F, [fp, ip, I, I]),
             "oracle_argmax": (I, [fp, I]),
@@ -86,6 +87,15 @@ class Oracle:
         rc = lib().oracle_forward_full(self._h, _i(t), t.size, _f(out))
         if rc:
             raise RuntimeError(f"oracle_forward_full: {rc}")
+        return out
+
+    def forward_last(self, tokens) -> np.ndarray:
+        """Full causal forward, classifier on the last row only: logits [vocab]."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, dtype=np.float32)
+        rc = lib().oracle_forward_last(self._h, _i(t), t.size, _f(out))
+        if rc:
+            raise RuntimeError(f"oracle_forward_last: {rc}")
         return out
 
     def decode_step(self, token: int, pos: int) -> np.ndarray:

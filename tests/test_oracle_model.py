@@ -34,6 +34,15 @@ def test_full_forward_equals_kv_decode_bitwise(lm, orc, d, kv16):
     assert np.array_equal(full, rows)
 
 
+def test_forward_last_is_last_row_of_full(lm, orc):
+    """The window-recompute mode (classifier on the last row only) gives the
+    full forward's last row bit for bit."""
+    w = _weights(lm, TINY_GQA, 7)
+    o = orc.Oracle(cfg7(TINY_GQA), w, True, 64)
+    toks = np.random.default_rng(7).integers(0, TINY_GQA["vocab_size"], 29)
+    assert np.array_equal(o.forward_last(toks), o.forward_full(toks)[-1])
+
+
 def test_causality(lm, orc):
     w = _weights(lm, TINY, 6)
     o = orc.Oracle(cfg7(TINY), w, True, 64)
