@@ -326,9 +326,13 @@ __device__ __forceinline__ void attn_head(
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
     float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
 {
+    /* hd 128 with an fp16 cache double-buffers its tiles: the next tile's K/V
+     * loads are in flight while the current one computes, in tiles of 32
+     * positions so that two fit the registers */
+    constexpr bool DB = HD == 128 && sizeof(KT) == 2;
     /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
-     * would take 256 registers per lane */
-    constexpr int TILE = (sizeof(KT) == 4 && HD == 128) ? 32 : 64;
+     * would take 256 registers per lane, or when double-buffered */
+    constexpr int TILE = ((sizeof(KT) == 4 && HD == 128) || DB) ? 32 : 64;
     constexpr int G = HD / 8;        /* lanes per position            */
     constexpr int PP = 64 / G;       /* positions per pass            */
     constexpr int NP = TILE / PP;    /* passes per tile               */
@@ -436,26 +440,14 @@ __device__ __forceinline__ void attn_head(
      * in order for the wait counter), so waiting for that tile does not wait
      * for them */
     after_first_loads();
-    for (int t = wv; t < ntiles; t += NWAVE) {
-        if (!EARLY || t != wv) {
-#pragma unroll
-            for (int i = 0; i < NP; i++) {
-                const int p = t * TILE + pp + PP * i;
-                if (p < vis) {
-                    kv_raw_load(K + (size_t)p * HD, kr[i]);
-                    kv_raw_load(V + (size_t)p * HD, vr[i]);
-                } else {
-                    kv_raw_zero(kr[i]);
-                    kv_raw_zero(vr[i]);
-                }
-            }
-        }
+    /* online softmax update with tile t (forward.h:82-97), held in kr/vr */
+    auto consume = [&](int t, const Raw (&tk)[NP], const Raw (&tv)[NP]) {
         float s[NP];
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             float kf[8];
-            kv_raw_unpack(kr[i], kf);
+            kv_raw_unpack(tk[i], kf);
             float d = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) d = fmaf(qf[j], kf[j], d);
@@ -477,11 +469,55 @@ __device__ __forceinline__ void attn_head(
             const float e = expf(s[i] - mn);   /* 0 for masked positions */
             l += e;
             float vf[8];
-            kv_raw_unpack(vr[i], vf);
+            kv_raw_unpack(tv[i], vf);
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = fmaf(e, vf[j], o[j]);
         }
         m = mn;
+    };
+    if constexpr (DB) {
+        /* positions past the visible ones load the last visible position again
+         * (masked in consume), so every load is unconditional and the wait for
+         * a tile never covers the next tile's loads */
+        const int plast = max(vis - 1, 0);
+        auto fetch = [&](int t, Raw (&tk)[NP], Raw (&tv)[NP]) {
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                const int p = min(t * TILE + pp + PP * i, plast);
+                kv_raw_load(K + (size_t)p * HD, tk[i]);
+                kv_raw_load(V + (size_t)p * HD, tv[i]);
+            }
+        };
+        Raw kr1[NP], vr1[NP];
+        fetch(wv, kr, vr);
+        /* the scheduling barriers keep each fetch ahead of the compute it
+         * overlaps (the compiler would sink the loads to their first use) */
+        for (int t = wv; t < ntiles; t += 2 * NWAVE) {   /* wave-uniform */
+            fetch(t + NWAVE, kr1, vr1);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(t, kr, vr);
+            if (t + NWAVE >= ntiles) break;
+            fetch(t + 2 * NWAVE, kr, vr);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(t + NWAVE, kr1, vr1);
+        }
+    } else {
+        for (int t = wv; t < ntiles; t += NWAVE) {
+            if (!EARLY || t != wv) {
+#pragma unroll
+                for (int i = 0; i < NP; i++) {
+                    const int p = t * TILE + pp + PP * i;
+                    if (p < vis) {
+                        kv_raw_load(K + (size_t)p * HD, kr[i]);
+                        kv_raw_load(V + (size_t)p * HD, vr[i]);
+                    } else {
+                        kv_raw_zero(kr[i]);
+                        kv_raw_zero(vr[i]);
+                    }
+                }
+            }
+            consume(t, kr, vr);
+        }
     }
 #pragma unroll
     for (int off = G; off < 64; off <<= 1) {
