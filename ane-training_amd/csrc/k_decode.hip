@@ -327,12 +327,12 @@ __device__ __forceinline__ void attn_head(
     float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
 {
     /* hd 128 with an fp16 cache double-buffers its tiles: the next tile's K/V
-     * loads are in flight while the current one computes, in tiles of 32
-     * positions so that two fit the registers */
+     * loads are in flight while the current one computes */
     constexpr bool DB = HD == 128 && sizeof(KT) == 2;
-    /* positions per tile: 64, or 32 when K and V of a 64-tile (fp32, hd 128)
-     * would take 256 registers per lane, or when double-buffered */
-    constexpr int TILE = ((sizeof(KT) == 4 && HD == 128) || DB) ? 32 : 64;
+    /* positions per tile: 32 (measured against 64: the four waves share short
+     * contexts more evenly, and two tiles fit the registers where
+     * double-buffered) */
+    constexpr int TILE = 32;
     constexpr int G = HD / 8;        /* lanes per position            */
     constexpr int PP = 64 / G;       /* positions per pass            */
     constexpr int NP = TILE / PP;    /* passes per tile               */
