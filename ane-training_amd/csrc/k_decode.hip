@@ -287,8 +287,6 @@ __device__ __forceinline__ void kv_raw_load(const float *p, KV8f &r)
     r.a = *(const float4 *)p;
     r.b = *(const float4 *)(p + 4);
 }
-__device__ __forceinline__ void kv_raw_zero(KV8h &r) { r.a = make_uint4(0, 0, 0, 0); }
-__device__ __forceinline__ void kv_raw_zero(KV8f &r) { r.a = r.b = make_float4(0, 0, 0, 0); }
 __device__ __forceinline__ void kv_raw_unpack(const KV8h &r, float f[8]) { unpack8(r.a, f); }
 __device__ __forceinline__ void kv_raw_unpack(const KV8f &r, float f[8])
 {
@@ -326,13 +324,12 @@ __device__ __forceinline__ void attn_head(
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
     float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
 {
-    /* hd 128 with an fp16 cache double-buffers its tiles: the next tile's K/V
-     * loads are in flight while the current one computes */
-    constexpr bool DB = HD == 128 && sizeof(KT) == 2;
     /* positions per tile: 32 (measured against 64: the four waves share short
-     * contexts more evenly, and two tiles fit the registers where
-     * double-buffered) */
+     * contexts more evenly).  Two tiles fit the registers except at hd 128 with
+     * an fp32 cache, so the next tile's K/V loads are in flight while the
+     * current one computes (DB) */
     constexpr int TILE = 32;
+    constexpr bool DB = !(HD == 128 && sizeof(KT) == 4);
     constexpr int G = HD / 8;        /* lanes per position            */
     constexpr int PP = 64 / G;       /* positions per pass            */
     constexpr int NP = TILE / PP;    /* passes per tile               */
@@ -365,9 +362,9 @@ __device__ __forceinline__ void attn_head(
 #pragma unroll
     for (int j = 0; j < 8; j++) o[j] = 0.f;
     /* hd 64: the wave's first tile is loaded before pos[b] has arrived
-     * (positions clamped into the cache, masked below), so the K/V fetch does
-     * not wait for it; later tiles, and every tile at hd 128 (where holding a
-     * tile across the loop would halve occupancy), load positions < ctx only */
+     * (positions clamped into the cache, masked below; the cache is zeroed at
+     * allocation, so every value read is finite), so the K/V fetch does not
+     * wait for it */
     constexpr bool EARLY = HD == 64;
     Raw kr[NP], vr[NP];
     if (EARLY) {
@@ -475,10 +472,10 @@ __device__ __forceinline__ void attn_head(
         }
         m = mn;
     };
-    if constexpr (DB) {
-        /* positions past the visible ones load the last visible position again
-         * (masked in consume), so every load is unconditional and the wait for
-         * a tile never covers the next tile's loads */
+    {
+        /* later tiles: positions past the visible ones load the last visible
+         * position again (masked in consume), so every load is unconditional
+         * and the wait for a tile never covers the next tile's loads */
         const int plast = max(vis - 1, 0);
         auto fetch = [&](int t, Raw (&tk)[NP], Raw (&tv)[NP]) {
 #pragma unroll
@@ -488,35 +485,25 @@ __device__ __forceinline__ void attn_head(
                 kv_raw_load(V + (size_t)p * HD, tv[i]);
             }
         };
-        Raw kr1[NP], vr1[NP];
-        fetch(wv, kr, vr);
-        /* the scheduling barriers keep each fetch ahead of the compute it
-         * overlaps (the compiler would sink the loads to their first use) */
-        for (int t = wv; t < ntiles; t += 2 * NWAVE) {   /* wave-uniform */
-            fetch(t + NWAVE, kr1, vr1);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(t, kr, vr);
-            if (t + NWAVE >= ntiles) break;
-            fetch(t + 2 * NWAVE, kr, vr);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(t + NWAVE, kr1, vr1);
-        }
-    } else {
-        for (int t = wv; t < ntiles; t += NWAVE) {
-            if (!EARLY || t != wv) {
-#pragma unroll
-                for (int i = 0; i < NP; i++) {
-                    const int p = t * TILE + pp + PP * i;
-                    if (p < vis) {
-                        kv_raw_load(K + (size_t)p * HD, kr[i]);
-                        kv_raw_load(V + (size_t)p * HD, vr[i]);
-                    } else {
-                        kv_raw_zero(kr[i]);
-                        kv_raw_zero(vr[i]);
-                    }
-                }
+        if (!EARLY) fetch(wv, kr, vr);
+        if constexpr (DB) {
+            Raw kr1[NP], vr1[NP];
+            /* the scheduling barriers keep each fetch ahead of the compute it
+             * overlaps (the compiler would sink the loads to their first use) */
+            for (int t = wv; t < ntiles; t += 2 * NWAVE) {   /* wave-uniform */
+                fetch(t + NWAVE, kr1, vr1);
+                __builtin_amdgcn_sched_barrier(0);
+                consume(t, kr, vr);
+                if (t + NWAVE >= ntiles) break;
+                fetch(t + 2 * NWAVE, kr, vr);
+                __builtin_amdgcn_sched_barrier(0);
+                consume(t + NWAVE, kr1, vr1);
             }
-            consume(t, kr, vr);
+        } else {
+            for (int t = wv; t < ntiles; t += NWAVE) {      /* wave-uniform */
+                if (t != wv) fetch(t, kr, vr);
+                consume(t, kr, vr);
+            }
         }
     }
 #pragma unroll
