@@ -7,16 +7,22 @@
  * online softmax with each tile (forward.h:72-99, scores in log2 units):
  *   S^T = K Q^T * (log2 e / sqrt(hd))   32x32x16 f16 MFMAs, fp32 accumulation;
  *                                       keys after the query's position masked
- *   m' = max(m, max_key S); P = 2^(S - m'); l = l*2^(m - m') + sum_key P;
+ *   m' = max_key S if it exceeds m by more than 8, else m;
+ *   P = 2^(S - m'); l = l*2^(m - m') + sum_key P;
  *   O^T = O^T*2^(m - m') + V^T P^T      P and V rounded to fp16 for the MFMA
- * and out = O / l, in fp16 (the operand of the Wo GEMM).
+ * and out = O / l, in fp16 (the operand of the Wo GEMM).  Any m' at or below
+ * the true maximum gives the same O / l; keeping m unless it falls 8 behind
+ * bounds P by 2^8 and skips the rescale of O on most tiles.  Only tiles that
+ * hold a key after some query of the wave are masked.
  *
  * Computing the transposed scores puts one query in each accumulator column, so
  * lane l holds 32 of the tile's 64 scores of query l % 32 (lane l ^ 32 the other
  * 32): the softmax needs one cross-lane exchange per tile, and the accumulator
  * already has the layout of the B operand of the V^T P^T product, up to an order
  * of the 16 keys of each MFMA step.  That order is undone by storing V^T in LDS
- * with bits 2 and 3 of the key index swapped.
+ * with bits 2 and 3 of the key index swapped; V^T rows are XOR-swizzled in
+ * 16-byte units so that neither the transposing writes nor the fragment reads
+ * conflict in the LDS banks.
  *
  * Two work-group shapes share that per-tile step:
  *   k_attn_prefill_blk    128 queries per work-group, 32 per wave; the four
@@ -57,24 +63,55 @@ __device__ __forceinline__ uint4 kv8_f16(const float *p)
 
 /* LDS column of key k of a tile in V^T: bits 2 and 3 swapped, so that the 8 keys
  * lane l contributes to an MFMA step (4 from each of two groups of 8) are
- * contiguous */
+ * contiguous.  The map is its own inverse. */
 __device__ __forceinline__ int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k >> 1) & 4); }
 
-/* Store one 16-byte chunk (8 dims d0.. of key `key`) of K and V into a staged
- * tile: K rows of KLD halves, V^T rows of VLD halves in vperm key order. */
-template <int KLD, int VLD>
-__device__ __forceinline__ void stage_chunk(u16 *sk, u16 *svt, int key, int d0, uint4 k8, uint4 v8)
+/* V^T tile: row d (a head dim) holds the tile's BKV keys in vperm order as 16-byte
+ * units; unit u of row d sits in slot u ^ vswz(d).  The 8 rows that one 16-byte
+ * fragment read serves per LDS cycle (d .. d+7) and the 8 rows d0 + j, d0 = 0, 8,
+ * .. 56 that one staging write serves then fall in 8 different slots: no bank
+ * conflicts on either side. */
+__device__ __forceinline__ int vswz(int d) { return (d ^ (d >> 3)) & 7; }
+__device__ __forceinline__ int vt_off(int d, int col) { return d * BKV + (((col >> 3) ^ vswz(d)) << 3) + (col & 7); }
+
+/* Staging unit `pr` (0 .. BKV/2 * HD/8 - 1) of a tile: dims d0 .. d0+7 of the keys
+ * in V^T columns pk and pk+1 (keys vperm(pk), vperm(pk) + 1: pk is even and vperm
+ * keeps bit 0).  Consecutive units take the 8 dim groups of one column pair, then
+ * the next pair: one wave's 32-lane half covers 4 pairs of one 16-byte unit. */
+template <int HD>
+__device__ __forceinline__ void pair_of(int pr, int &pk, int &d0)
 {
-    *(uint4 *)(&sk[key * KLD + d0]) = k8;
-    const unsigned vw[4] = {v8.x, v8.y, v8.z, v8.w};
-    const int pk = vperm(key);
-#pragma unroll
-    for (int j = 0; j < 8; j++) svt[(d0 + j) * VLD + pk] = (u16)(vw[j >> 1] >> (16 * (j & 1)));
+    pk = ((pr >> 3) & (BKV / 2 - 1)) * 2;
+    d0 = ((pr & 7) + (pr / (BKV / 2 * 8)) * 8) * 8;
 }
 
+/* Store one staging unit: K rows of KLD halves (two 16-byte writes), V^T in the
+ * swizzled layout (8 dword writes, each the two keys of one dim). */
+template <int KLD>
+__device__ __forceinline__ void stage_pair(u16 *sk, u16 *svt, int pk, int d0, uint4 ka, uint4 kb,
+                                           uint4 va, uint4 vb)
+{
+    const int key = vperm(pk);
+    *(uint4 *)(&sk[key * KLD + d0]) = ka;
+    *(uint4 *)(&sk[(key + 1) * KLD + d0]) = kb;
+    const unsigned wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const unsigned a = wa[j >> 1], b = wb[j >> 1];
+        const unsigned w = (j & 1) ? (a >> 16) | (b & 0xffff0000u) : (a & 0xffffu) | (b << 16);
+        *(unsigned *)(&svt[vt_off(d0 + j, pk)]) = w;
+    }
+}
+
+/* The running maximum m of a query is raised only when a tile's maximum exceeds
+ * it by more than this (log2 units), so P = 2^(S - m) <= 2^8 stays well inside
+ * fp16 and the rescale of O and l is skipped for most tiles. */
+#define M_SLACK 8.0f
+
 /* Online-softmax update of one wave's 32 queries (lane l: query l % 32 at
- * position qp) with the staged tile of keys k0 .. k0+63 (K rows, V^T). */
-template <int HD, int KLD, int VLD>
+ * position qp) with the staged tile of keys k0 .. k0+63 (K rows, V^T).  MASK:
+ * the tile holds keys after some query's position (wave-uniform choice). */
+template <int HD, int KLD, bool MASK>
 __device__ __forceinline__ void tile_update(const u16 *sk, const u16 *svt, const uint4 (&qb16)[HD / 16],
                                             int k0, int qp, float scale, f32x16 (&o)[HD / 32],
                                             float &mrow, float &lrow)
@@ -92,22 +129,31 @@ __device__ __forceinline__ void tile_update(const u16 *sk, const u16 *svt, const
             sacc[nt] = mfma32h(ka, qb16[ks], sacc[nt]);
         }
     }
-    /* element i of tile nt is key k0 + nt*32 + 8*(i/4) + 4*g + i%4 */
+    /* element i of tile nt is key k0 + nt*32 + 8*(i/4) + 4*g + i%4; the maximum
+     * is taken over the raw dot products (scale > 0) */
     float mx = -INFINITY;
 #pragma unroll
     for (int nt = 0; nt < 2; nt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int key = k0 + nt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-            const float v = key > qp ? -INFINITY : sacc[nt][i] * scale;
-            sacc[nt][i] = v;
-            mx = fmaxf(mx, v);
+            if constexpr (MASK) {
+                const int key = k0 + nt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (key > qp) sacc[nt][i] = -INFINITY;
+            }
+            mx = fmaxf(mx, sacc[nt][i]);
         }
-    mx = fmaxf(mx, xor32_f(mx));
-    const float mn = fmaxf(mrow, mx);
-    /* a query with every key so far masked keeps m = -inf: nothing to scale */
-    const float corr = mn == -INFINITY ? 1.f : exp2f(mrow - mn);
-    const float sub = mn == -INFINITY ? 0.f : mn;
+    mx = fmaxf(mx, xor32_f(mx)) * scale;
+    /* a query with every key so far masked keeps m = -inf (and O = l = 0) */
+    const bool raise = mx > mrow + M_SLACK;
+    if (__builtin_amdgcn_ballot_w64(raise)) {     /* wave-uniform */
+        const float mn = raise ? mx : mrow;
+        const float corr = __builtin_amdgcn_exp2f(mrow - mn);   /* 0 from m = -inf, 1 if kept */
+        lrow *= corr;
+#pragma unroll
+        for (int j = 0; j < DT; j++) o[j] *= corr;
+        mrow = mn;
+    }
+    const float sub = mrow == -INFINITY ? 0.f : mrow;
     float ls = 0.f;
     uint4 pb[2][2];
 #pragma unroll
@@ -117,16 +163,13 @@ __device__ __forceinline__ void tile_update(const u16 *sk, const u16 *svt, const
             f16x8 hv;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float e = exp2f(sacc[nt][8 * hh + j] - sub);
+                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[nt][8 * hh + j], scale, -sub));
                 ls += e;
                 hv[j] = (_Float16)e;
             }
             pb[nt][hh] = __builtin_bit_cast(uint4, hv);
         }
-    lrow = lrow * corr + ls;                   /* per-lane partial row sum */
-    mrow = mn;
-#pragma unroll
-    for (int j = 0; j < DT; j++) o[j] *= corr;
+    lrow += ls;                                /* per-lane partial row sum */
     /* O^T += V^T P^T over the 4 steps of 16 keys */
 #pragma unroll
     for (int nt = 0; nt < 2; nt++)
@@ -134,8 +177,7 @@ __device__ __forceinline__ void tile_update(const u16 *sk, const u16 *svt, const
         for (int hh = 0; hh < 2; hh++)
 #pragma unroll
             for (int j = 0; j < DT; j++) {
-                const uint4 va =
-                    *(const uint4 *)(&svt[(j * 32 + (lane & 31)) * VLD + nt * 32 + hh * 16 + g * 8]);
+                const uint4 va = *(const uint4 *)(&svt[vt_off(j * 32 + (lane & 31), nt * 32 + hh * 16 + g * 8)]);
                 o[j] = mfma32h(va, pb[nt][hh], o[j]);
             }
 }
@@ -161,12 +203,11 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_blk(
     int max_seq, u16 *__restrict__ out)
 {
     constexpr int KLD = HD + 8;          /* K tile row stride (halves)   */
-    constexpr int VLD = BKV + 8;         /* V^T tile row stride (halves) */
     constexpr int DT = HD / 32;          /* 32-dim row tiles of O^T      */
-    constexpr int CPT = BKV * HD / 8 / AT;   /* 16-byte chunks per thread per array */
-    static_assert(CPT >= 1 && BKV * HD / 8 % AT == 0, "staging shape");
+    constexpr int PPT = BKV * HD / 16 / AT;  /* staging units per thread */
+    static_assert(PPT >= 1 && BKV * HD / 16 % AT == 0, "staging shape");
     __shared__ __attribute__((aligned(16))) u16 sk[2][BKV * KLD];
-    __shared__ __attribute__((aligned(16))) u16 svt[2][HD * VLD];
+    __shared__ __attribute__((aligned(16))) u16 svt[2][HD * BKV];
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -184,26 +225,32 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_blk(
     const int last_pos = p0 + nrows - 1;          /* last query position of the block */
     const int ntiles = last_pos / BKV + 1;
 
-    /* K / V chunks of one tile: chunk c = tid + i*AT is key c / (HD/8), dims
-     * (c % (HD/8))*8 .. +8; keys past the block's last position repeat it (they
+    /* K / V of one tile: thread t stages units t + i*AT (two keys, 8 dims each:
+     * [0] key, [1] key + 1); keys past the block's last position repeat it (they
      * are masked for every query that reads them).  Two register sets: tile t
      * sits in set t % 2 from its fetch (two tiles ahead of its use) until it is
      * stored to LDS (one tile ahead). */
-    uint4 rk0[CPT], rv0[CPT], rk1[CPT], rv1[CPT];
-    auto fetch = [&](int kt, uint4 (&rk)[CPT], uint4 (&rv)[CPT]) {
+    uint4 rk0[PPT][2], rv0[PPT][2], rk1[PPT][2], rv1[PPT][2];
+    auto fetch = [&](int kt, uint4 (&rk)[PPT][2], uint4 (&rv)[PPT][2]) {
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + i * AT, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-            const size_t off = cbase + (size_t)min(kt * BKV + key, last_pos) * HD + d0;
-            rk[i] = kv8_f16(kc + off);
-            rv[i] = kv8_f16(vc + off);
+        for (int i = 0; i < PPT; i++) {
+            int pk, d0;
+            pair_of<HD>(tid + i * AT, pk, d0);
+            const int key = kt * BKV + vperm(pk);
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const size_t off = cbase + (size_t)min(key + e, last_pos) * HD + d0;
+                rk[i][e] = kv8_f16(kc + off);
+                rv[i][e] = kv8_f16(vc + off);
+            }
         }
     };
-    auto stash = [&](int b, const uint4 (&rk)[CPT], const uint4 (&rv)[CPT]) {
+    auto stash = [&](int b, const uint4 (&rk)[PPT][2], const uint4 (&rv)[PPT][2]) {
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int c = tid + i * AT;
-            stage_chunk<KLD, VLD>(sk[b], svt[b], c / (HD / 8), (c % (HD / 8)) * 8, rk[i], rv[i]);
+        for (int i = 0; i < PPT; i++) {
+            int pk, d0;
+            pair_of<HD>(tid + i * AT, pk, d0);
+            stage_pair<KLD>(sk[b], svt[b], pk, d0, rk[i][0], rk[i][1], rv[i][0], rv[i][1]);
         }
     };
     fetch(0, rk0, rv0);
@@ -212,7 +259,7 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_blk(
     /* this wave's queries: block rows wr0 .. wr0+31; lane l takes row wr0 + l%32 */
     const int wr0 = wave * 32;
     const bool wave_active = wr0 < nrows;
-    const int wave_last = p0 + min(wr0 + 31, nrows - 1);
+    const int wave_first = p0 + wr0, wave_last = p0 + min(wr0 + 31, nrows - 1);
     const int qrow = wr0 + (lane & 31);
     const int qp = p0 + qrow;                     /* this lane's query position */
     uint4 qb16[HD / 16];
@@ -226,13 +273,17 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_blk(
     __syncthreads();
     /* tile kt: fetch tile kt+2 into the set tile kt left (unconditionally, so
      * the compiler waits only for the older set), compute kt, store kt+1 */
-    auto body = [&](int kt, uint4 (&rka)[CPT], uint4 (&rva)[CPT], const uint4 (&rkb)[CPT],
-                    const uint4 (&rvb)[CPT]) {
+    auto body = [&](int kt, uint4 (&rka)[PPT][2], uint4 (&rva)[PPT][2], const uint4 (&rkb)[PPT][2],
+                    const uint4 (&rvb)[PPT][2]) {
         const int b = kt & 1;
         fetch(kt + 2, rka, rva);
         const int k0 = kt * BKV;
-        if (wave_active && k0 <= wave_last)       /* wave-uniform */
-            tile_update<HD, KLD, VLD>(sk[b], svt[b], qb16, k0, qp, scale, o, mrow, lrow);
+        if (wave_active && k0 <= wave_last) {     /* wave-uniform */
+            if (k0 + BKV - 1 <= wave_first)       /* every key visible to every query */
+                tile_update<HD, KLD, false>(sk[b], svt[b], qb16, k0, qp, scale, o, mrow, lrow);
+            else
+                tile_update<HD, KLD, true>(sk[b], svt[b], qb16, k0, qp, scale, o, mrow, lrow);
+        }
         if (kt + 1 < ntiles) stash(b ^ 1, rkb, rvb);
         __syncthreads();
     };
@@ -271,12 +322,11 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_split(
     int max_seq, u16 *__restrict__ out)
 {
     constexpr int KLD = HD + 8;          /* K tile row stride (halves)   */
-    constexpr int VLD = BKV + 8;         /* V^T tile row stride (halves) */
     constexpr int KS = HD / 16;          /* MFMA k-steps over head dims  */
     constexpr int DT = HD / 32;          /* 32-dim row tiles of O^T      */
-    constexpr int CPL = BKV * HD / 8 / 64;   /* 16-byte chunks per lane per array (one wave stages a tile) */
+    constexpr int PPL = BKV * HD / 16 / 64;  /* staging units per lane (one wave stages a tile) */
     constexpr bool PREF = HD == 64 && sizeof(KT) == 2;   /* next tile in registers */
-    constexpr int STAGE = BKV * KLD + HD * VLD;          /* halves of one wave's K and V^T */
+    constexpr int STAGE = BKV * KLD + HD * BKV;          /* halves of one wave's K and V^T */
     static_assert(BKV * HD / 8 % 256 == 0, "staging shape");
     constexpr int MLD = HD + 1;                          /* merge row stride (floats) */
     static_assert(NW * STAGE * 2 >= (NW * BQS * MLD + 2 * NW * BQS) * 4, "merge area fits the staging area");
@@ -299,23 +349,29 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_split(
     const int ntiles = last_pos / BKV + 1;
     u16 *sk = stg + wave * STAGE, *svt = sk + BKV * KLD;
 
-    /* K / V chunks of one tile for this wave: chunk c = lane + i*64 is key
-     * c / (HD/8), dims (c % (HD/8))*8 .. +8; keys past the block's last
-     * position repeat it (masked for every query that reads them) */
-    auto load = [&](int kt, int i, uint4 &k8, uint4 &v8) {
-        const int c = lane + i * 64, key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-        const size_t off = cbase + (size_t)min(kt * BKV + key, last_pos) * HD + d0;
-        k8 = kv8_f16(kc + off);
-        v8 = kv8_f16(vc + off);
+    /* K / V of one tile for this wave: lane l stages units l + i*64 (two keys, 8
+     * dims each); keys past the block's last position repeat it (masked for
+     * every query that reads them) */
+    auto load = [&](int kt, int i, uint4 (&k8)[2], uint4 (&v8)[2]) {
+        int pk, d0;
+        pair_of<HD>(lane + i * 64, pk, d0);
+        const int key = kt * BKV + vperm(pk);
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const size_t off = cbase + (size_t)min(key + e, last_pos) * HD + d0;
+            k8[e] = kv8_f16(kc + off);
+            v8[e] = kv8_f16(vc + off);
+        }
     };
-    auto put = [&](int i, uint4 k8, uint4 v8) {
-        const int c = lane + i * 64;
-        stage_chunk<KLD, VLD>(sk, svt, c / (HD / 8), (c % (HD / 8)) * 8, k8, v8);
+    auto put = [&](int i, const uint4 (&k8)[2], const uint4 (&v8)[2]) {
+        int pk, d0;
+        pair_of<HD>(lane + i * 64, pk, d0);
+        stage_pair<KLD>(sk, svt, pk, d0, k8[0], k8[1], v8[0], v8[1]);
     };
     /* hd 64 with an fp16 cache: the whole next tile is held in registers while
-     * the current one computes; otherwise a tile is staged 4 chunks at a time */
-    constexpr int RC = PREF ? CPL : 1;
-    uint4 rk[RC], rv[RC];
+     * the current one computes; otherwise a tile is staged 2 units at a time */
+    constexpr int RC = PREF ? PPL : 1;
+    uint4 rk[RC][2], rv[RC][2];
     auto fetch = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < RC; i++) load(kt, i, rk[i], rv[i]);
@@ -323,15 +379,15 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_split(
     auto stage = [&](int kt) {
         if constexpr (PREF) {
 #pragma unroll
-            for (int i = 0; i < CPL; i++) put(i, rk[i], rv[i]);
+            for (int i = 0; i < PPL; i++) put(i, rk[i], rv[i]);
         } else {
 #pragma unroll
-            for (int i0 = 0; i0 < CPL; i0 += 4) {
-                uint4 k4[4], v4[4];
+            for (int i0 = 0; i0 < PPL; i0 += 2) {
+                uint4 k4[2][2], v4[2][2];
 #pragma unroll
-                for (int i = 0; i < 4; i++) load(kt, i0 + i, k4[i], v4[i]);
+                for (int i = 0; i < 2; i++) load(kt, i0 + i, k4[i], v4[i]);
 #pragma unroll
-                for (int i = 0; i < 4; i++) put(i0 + i, k4[i], v4[i]);
+                for (int i = 0; i < 2; i++) put(i0 + i, k4[i], v4[i]);
             }
         }
     };
@@ -352,7 +408,10 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_split(
         __builtin_amdgcn_s_waitcnt(0xc07f);       /* lgkmcnt(0): the wave's LDS writes landed */
         __builtin_amdgcn_wave_barrier();
         if (PREF && kt + NW < ntiles) fetch(kt + NW);
-        tile_update<HD, KLD, VLD>(sk, svt, qb16, kt * BKV, qp, scale, o, mrow, lrow);
+        if (kt * BKV + BKV - 1 <= p0)             /* wave-uniform: no key after any query */
+            tile_update<HD, KLD, false>(sk, svt, qb16, kt * BKV, qp, scale, o, mrow, lrow);
+        else
+            tile_update<HD, KLD, true>(sk, svt, qb16, kt * BKV, qp, scale, o, mrow, lrow);
         __builtin_amdgcn_wave_barrier();           /* the tile's reads precede the next stash */
     }
     /* merge the four waves: each writes (m, l, O) of its 32 queries; element i of

@@ -138,9 +138,13 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         const int gi = (n0 / 32) * 16 + (c & 15);
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-            const float other = xor16_f(lo ? acc[i + 1] : acc[i]);
-            const float h1 = lo ? acc[i] : other;
-            const float h3 = lo ? other : acc[i + 1];
+            /* the empty asm keeps a lane-dependent select between the two
+             * elements from becoming a 16-way select over the vector */
+            float a0 = acc[i], a1 = acc[i + 1];
+            asm("" : "+v"(a0), "+v"(a1));
+            const float other = xor16_f(lo ? a1 : a0);
+            const float h1 = lo ? a0 : other;
+            const float h3 = lo ? other : a1;
             const int r = lo ? rr[i] : rr[i + 1];
             const bool okr = lo ? ok[i] : ok[i + 1];
             const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
@@ -305,10 +309,15 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
 #pragma unroll
             for (int k = 0; k < 16; k += 2) {
                 /* lane c < 16: row of element k (h1 own, h3 from lane c + 16);
-                 * lane c + 16: row of element k + 1 (h3 own, h1 from lane c) */
-                const float other = xor16_f(lo ? acc[i][j][k + 1] : acc[i][j][k]);
-                const float h1 = lo ? acc[i][j][k] : other;
-                const float h3 = lo ? other : acc[i][j][k + 1];
+                 * lane c + 16: row of element k + 1 (h3 own, h1 from lane c).
+                 * The empty asm keeps the two elements separate values: a
+                 * select between them would otherwise become an element read at
+                 * a lane-dependent index, i.e. a 16-way select chain. */
+                float a0 = acc[i][j][k], a1 = acc[i][j][k + 1];
+                asm("" : "+v"(a0), "+v"(a1));
+                const float other = xor16_f(lo ? a1 : a0);
+                const float h1 = lo ? a0 : other;
+                const float h3 = lo ? other : a1;
                 const int r = rl + 8 * (k >> 2) + (k & 3) + (lo ? 0 : 1);
                 const float ex = __builtin_amdgcn_exp2f(-h1 * 1.4426950408889634f);
                 const float silu = h1 * __builtin_amdgcn_rcpf(1.0f + ex);   /* forward.h:101 */
