@@ -747,15 +747,96 @@ static void launch_skinny(hipStream_t s, const uint16_t *A, int lda, const uint1
 
 /* ---- per-row RMSNorm ------------------------------------------------------------ */
 
-/* One work-group per row m (forward.h:46-53): with emb != NULL the row is first
- * set to the fp16 embedding row emb[tok[m]] (forward.h:108-110); with ns > 0 the
- * ns partials of a K-split projection are added to it first, in split order (the
- * residual add, forward.h:134-136, 157-159); then
- * xn[m, k] = fp16(x[m, k] * (1/sqrt(mean(x[m]^2) + 1e-5)) * gain[k]), the GEMM
- * operand of the projection that follows.  Thread t owns the D/256 values
- * 4t .. 4t+3 (+1024 ...), so every load of the row is issued at once. */
+/* Row norm, one wave per row m, four rows per work-group (forward.h:46-53): with
+ * emb != NULL the row is first set to the fp16 embedding row emb[tok[m]]
+ * (forward.h:108-110); with ns > 0 the ns partials of a K-split projection are
+ * added to it, in split order (the residual add, forward.h:134-136, 157-159);
+ * then xn[m, k] = fp16(x[m, k] * (1/sqrt(mean(x[m]^2) + 1e-5)) * gain[k]), the
+ * GEMM operand of the projection that follows.  Lane l holds columns
+ * c*256 + 4l .. +3 (c < D/256) as float4 groups, so every access is a 16-byte
+ * (x, partials, gain) or 8-byte (embedding, xn) lane segment, and the sum of
+ * squares is a wave reduction (no LDS, no barrier).  Partials are loaded four
+ * at a time.  Used from 512 rows: 4.5 against 6.3 us for one work-group per row
+ * at 2048 rows with one partial (C3 2-3% faster); below that the work-group
+ * per row spreads the rows over more CUs (C1 and 32 decode rows of 2048 were
+ * faster with it in the full forward). */
 template <int D>
-__global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
+__global__ void __launch_bounds__(256) k_rownorm(float *__restrict__ x, int M,
+                                                   const u16 *__restrict__ emb,
+                                                   const int *__restrict__ tok,
+                                                   const float *__restrict__ sp, int ns,
+                                                   size_t sstride,
+                                                   const float *__restrict__ gain,
+                                                   u16 *__restrict__ xn)
+{
+    constexpr int C4 = D / 256;
+    static_assert(D % 256 == 0, "row width");
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;                       /* wave-uniform; no barrier below */
+    float *xr = x + (size_t)m * D + 4 * lane;
+    float4 v[C4];
+    if (emb) {
+        const u16 *er = emb + (size_t)tok[m] * D + 4 * lane;
+#pragma unroll
+        for (int c = 0; c < C4; c++) {
+            const uint2 h = *(const uint2 *)(er + c * 256);
+            const f16x2 a = __builtin_bit_cast(f16x2, h.x), b = __builtin_bit_cast(f16x2, h.y);
+            v[c] = make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < C4; c++) v[c] = *(const float4 *)(xr + c * 256);
+        const float *pr = sp + (size_t)m * D + 4 * lane;
+        for (int q = 0; q < ns; q += 4) {
+            /* past the last partial a group reloads it and adds zero, so the
+             * loads stay unconditional */
+            float4 t[4][C4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int c = 0; c < C4; c++)
+                    t[u][c] = *(const float4 *)(pr + (size_t)min(q + u, ns - 1) * sstride + c * 256);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float z = q + u < ns ? 1.f : 0.f;
+#pragma unroll
+                for (int c = 0; c < C4; c++) {
+                    v[c].x += t[u][c].x * z; v[c].y += t[u][c].y * z;
+                    v[c].z += t[u][c].z * z; v[c].w += t[u][c].w * z;
+                }
+            }
+        }
+    }
+    if (emb || ns > 0) {
+#pragma unroll
+        for (int c = 0; c < C4; c++) *(float4 *)(xr + c * 256) = v[c];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < C4; c++) {
+        ss = fmaf(v[c].x, v[c].x, ss); ss = fmaf(v[c].y, v[c].y, ss);
+        ss = fmaf(v[c].z, v[c].z, ss); ss = fmaf(v[c].w, v[c].w, ss);
+    }
+    ss = wave_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / D + 1e-5f);
+    u16 *xo = xn + (size_t)m * D + 4 * lane;
+    const float *gr = gain + 4 * lane;
+#pragma unroll
+    for (int c = 0; c < C4; c++) {
+        const float4 g = *(const float4 *)(gr + c * 256);
+        const unsigned lo = (unsigned)f2h(v[c].x * rs * g.x) | ((unsigned)f2h(v[c].y * rs * g.y) << 16);
+        const unsigned hi = (unsigned)f2h(v[c].z * rs * g.z) | ((unsigned)f2h(v[c].w * rs * g.w) << 16);
+        *(uint2 *)(xo + c * 256) = make_uint2(lo, hi);
+    }
+}
+
+/* The same row norm with one 256-thread work-group per row (four waves share
+ * it: thread t owns the D/256 values 4t .. 4t+3 (+1024 ...), so every load of
+ * the row is issued at once, and the sum of squares goes through LDS), for
+ * fewer than 512 rows. */
+template <int D>
+__global__ void __launch_bounds__(GT) k_rownorm_blk(float *__restrict__ x, int M,
                                                 const u16 *__restrict__ emb,
                                                 const int *__restrict__ tok,
                                                 const float *__restrict__ sp, int ns,
@@ -874,18 +955,31 @@ __global__ void __launch_bounds__(GT) k_rownorm(float *__restrict__ x, int M,
 
 /* ============================== launchers =================================== */
 
+
 extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
                            const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn)
 {
     if (M < 1 || (emb && !tok) || !gain || !xn || ns < 0 || (ns && (!sp || emb)))
         return hipErrorInvalidValue;
-    dim3 grid(M);
+    if (M < 512) {   /* a work-group per row */
+        dim3 grid(M);
+        switch (D) {
+        case 256: hipLaunchKernelGGL(k_rownorm_blk<256>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 512: hipLaunchKernelGGL(k_rownorm_blk<512>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 768: hipLaunchKernelGGL(k_rownorm_blk<768>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 1024: hipLaunchKernelGGL(k_rownorm_blk<1024>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 2048: hipLaunchKernelGGL(k_rownorm_blk<2048>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    dim3 grid((M + 3) / 4);
     switch (D) {
-    case 256: hipLaunchKernelGGL(k_rownorm<256>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
-    case 512: hipLaunchKernelGGL(k_rownorm<512>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
-    case 768: hipLaunchKernelGGL(k_rownorm<768>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
-    case 1024: hipLaunchKernelGGL(k_rownorm<1024>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
-    case 2048: hipLaunchKernelGGL(k_rownorm<2048>, grid, dim3(GT), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 256: hipLaunchKernelGGL(k_rownorm<256>, grid, dim3(256), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 512: hipLaunchKernelGGL(k_rownorm<512>, grid, dim3(256), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 768: hipLaunchKernelGGL(k_rownorm<768>, grid, dim3(256), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 1024: hipLaunchKernelGGL(k_rownorm<1024>, grid, dim3(256), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+    case 2048: hipLaunchKernelGGL(k_rownorm<2048>, grid, dim3(256), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
