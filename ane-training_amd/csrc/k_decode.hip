@@ -350,7 +350,8 @@ __device__ __forceinline__ void attn_head(
     const size_t base = ((size_t)cs * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
     const KT *K = kc + base;
     const KT *V = vc + base;
-    const float scale = 1.0f / sqrtf((float)HD);
+    /* scores in log2 units: exp(x) = exp2(x * log2 e), the hardware exp2 */
+    const float scale = 1.4426950408889634f / sqrtf((float)HD);
     float qf[8];
     if (!qp) {
         const float *qr = q + (size_t)b * H * HD + h * HD + dq * 8;
@@ -364,9 +365,12 @@ __device__ __forceinline__ void attn_head(
     /* hd 64: the wave's first tile is loaded before pos[b] has arrived
      * (positions clamped into the cache, masked below; the cache is zeroed at
      * allocation, so every value read is finite), so the K/V fetch does not
-     * wait for it */
+     * wait for it.  (Loading the second tile that early as well was 3% slower
+     * for 64 rows at 192-255 positions: the waves with one tile then read a
+     * whole tile of unused cache rows.) */
     constexpr bool EARLY = HD == 64;
     Raw kr[NP], vr[NP];
+    Raw kr1[NP], vr1[NP];            /* the wave's next tile (DB) */
     if (EARLY) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
@@ -457,13 +461,13 @@ __device__ __forceinline__ void attn_head(
 #pragma unroll
         for (int off = G; off < 64; off <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off, 64));
         const float mn = fmaxf(m, tmax);
-        const float corr = expf(m - mn);
+        const float corr = __builtin_amdgcn_exp2f(m - mn);   /* 0 on the first tile */
         l *= corr;
 #pragma unroll
         for (int j = 0; j < 8; j++) o[j] *= corr;
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const float e = expf(s[i] - mn);   /* 0 for masked positions */
+            const float e = __builtin_amdgcn_exp2f(s[i] - mn);   /* 0 for masked positions */
             l += e;
             float vf[8];
             kv_raw_unpack(tv[i], vf);
@@ -487,17 +491,24 @@ __device__ __forceinline__ void attn_head(
         };
         if (!EARLY) fetch(wv, kr, vr);
         if constexpr (DB) {
-            Raw kr1[NP], vr1[NP];
-            /* the scheduling barriers keep each fetch ahead of the compute it
-             * overlaps (the compiler would sink the loads to their first use) */
-            for (int t = wv; t < ntiles; t += 2 * NWAVE) {   /* wave-uniform */
-                fetch(t + NWAVE, kr1, vr1);
-                __builtin_amdgcn_sched_barrier(0);
-                consume(t, kr, vr);
-                if (t + NWAVE >= ntiles) break;
-                fetch(t + 2 * NWAVE, kr, vr);
-                __builtin_amdgcn_sched_barrier(0);
-                consume(t + NWAVE, kr1, vr1);
+            /* kr holds the wave's first tile and kr1 its second (both in
+             * flight); the first tile is consumed outside the loop, which keeps
+             * the loop's registers at two tiles (143 -> 109 VGPRs at hd 64).
+             * The scheduling barriers keep each fetch ahead of the compute it
+             * overlaps (the compiler would sink the loads to their first use). */
+            fetch(wv + NWAVE, kr1, vr1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (wv < ntiles) {                                   /* wave-uniform */
+                consume(wv, kr, vr);
+                for (int t = wv + NWAVE; t < ntiles; t += 2 * NWAVE) {   /* kr1: tile t */
+                    fetch(t + NWAVE, kr, vr);
+                    __builtin_amdgcn_sched_barrier(0);
+                    consume(t, kr1, vr1);
+                    if (t + NWAVE >= ntiles) break;
+                    fetch(t + 2 * NWAVE, kr1, vr1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    consume(t + NWAVE, kr, vr);
+                }
             }
         } else {
             for (int t = wv; t < ntiles; t += NWAVE) {      /* wave-uniform */
@@ -526,12 +537,12 @@ __device__ __forceinline__ void attn_head(
         float L = 0.f, acc = 0.f;
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) {
-            const float f = sm[w] == -INFINITY ? 0.f : expf(sm[w] - M);
+            const float f = sm[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sm[w] - M);
             L = fmaf(sl[w], f, L);
             acc = fmaf(so[w][d], f, acc);
         }
         if (qp) {   /* the current position, after the cached ones */
-            const float f = expf(scur - M);
+            const float f = __builtin_amdgcn_exp2f(scur - M);
             L += f;
             acc = fmaf(kv_round<KT>(sqkv[2][d]), f, acc);
         }
