@@ -63,6 +63,7 @@ __device__ __forceinline__ float dpp_f(float v)
 #define DPP_ROW_HALF_MIRROR 0x141
 #define DPP_ROW_BCAST15 0x142
 #define DPP_ROW_BCAST31 0x143
+#define DPP_ROW_ROR8 0x128      /* row_ror:8, lane l of a 16-lane row reads lane l ^ 8 */
 
 /* Sum over each 32-lane half: afterwards lanes 16..31 hold the sum of lanes
  * 0..31 and lanes 48..63 the sum of lanes 32..63 (read lanes 31 and 63). */

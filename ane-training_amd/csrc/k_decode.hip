@@ -441,6 +441,27 @@ __device__ __forceinline__ void attn_head(
      * in order for the wait counter), so waiting for that tile does not wait
      * for them */
     after_first_loads();
+    /* Sum over each aligned group of G lanes, in every lane of the group: the
+     * xor-1/2/4(/8) butterfly as DPP moves (after each step the value is
+     * uniform over quads, then octets, so the half-row and row mirrors pair the
+     * lanes exactly as xor 4 and xor 8 would).  The same pairing as shuffles,
+     * so the same sums, without LDS permutes. */
+    auto gsum = [](float d) {
+        d += dpp_f<DPP_QUAD_XOR1>(d);
+        d += dpp_f<DPP_QUAD_XOR2>(d);
+        d += dpp_f<DPP_ROW_HALF_MIRROR>(d);
+        if constexpr (G == 16) d += dpp_f<DPP_ROW_MIRROR>(d);
+        return d;
+    };
+    /* Combine the lanes with the same l % G (the same dims) across the 64/G
+     * groups: xor 8 as a DPP rotate of each 16-lane row by 8 (G = 8), then xor
+     * 16 and xor 32 as permlane swaps. */
+    auto across = [](float v, auto op) {
+        if constexpr (G == 8) v = op(v, dpp_f<DPP_ROW_ROR8>(v));
+        v = op(v, xor16_f(v));
+        return op(v, xor32_f(v));
+    };
+    auto fadd = [](float a, float b) { return a + b; };
     /* online softmax update with tile t (forward.h:82-97), held in kr/vr */
     auto consume = [&](int t, const Raw (&tk)[NP], const Raw (&tv)[NP]) {
         float s[NP];
@@ -452,14 +473,12 @@ __device__ __forceinline__ void attn_head(
             float d = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) d = fmaf(qf[j], kf[j], d);
-#pragma unroll
-            for (int off = 1; off < G; off <<= 1) d += __shfl_xor(d, off, 64);
+            d = gsum(d);
             const int p = t * TILE + pp + PP * i;
             s[i] = p < vis ? d * scale : -INFINITY;
             tmax = fmaxf(tmax, s[i]);
         }
-#pragma unroll
-        for (int off = G; off < 64; off <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off, 64));
+        tmax = across(tmax, [](float a, float b) { return fmaxf(a, b); });
         const float mn = fmaxf(m, tmax);
         const float corr = __builtin_amdgcn_exp2f(m - mn);   /* 0 on the first tile */
         l *= corr;
@@ -517,12 +536,9 @@ __device__ __forceinline__ void attn_head(
             }
         }
     }
+    l = across(l, fadd);
 #pragma unroll
-    for (int off = G; off < 64; off <<= 1) {
-        l += __shfl_xor(l, off, 64);
-#pragma unroll
-        for (int j = 0; j < 8; j++) o[j] += __shfl_xor(o[j], off, 64);
-    }
+    for (int j = 0; j < 8; j++) o[j] = across(o[j], fadd);
     if (lane < G) {
 #pragma unroll
         for (int j = 0; j < 8; j++) so[wv][dq * 8 + j] = o[j];
