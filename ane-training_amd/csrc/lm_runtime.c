@@ -1317,6 +1317,34 @@ int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, c
     return nsplit;
 }
 
+int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t *W, uint16_t *g)
+{
+    if (M < 1 || N < 2 * LMK_GATE_BLOCK || N % (2 * LMK_GATE_BLOCK) || K < 32 || K % 32 || !A || !W || !g)
+        return LM_ERR_INVALID;
+    int rc = lm_init();
+    if (rc) return rc;
+    const int F = N / 2;
+    const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2, gsz = (size_t)M * F * 2;
+    void *dA = NULL, *dW = NULL, *dG = NULL;
+    hipError_t e = hipMalloc(&dA, asz);
+    if (e == hipSuccess) e = hipMalloc(&dW, wsz);
+    if (e == hipSuccess) e = hipMalloc(&dG, gsz);
+    if (e == hipSuccess) e = hipMemcpy(dA, A, asz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dW, W, wsz, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(dG, 0xFF, gsz);
+    if (e == hipSuccess) {
+        LMEpilogue ep;
+        memset(&ep, 0, sizeof(ep));
+        ep.g = (uint16_t *)dG; ep.F = F;
+        e = (hipError_t)lmk_gemm(0, (const uint16_t *)dA, K, (const uint16_t *)dW, M, N, K, LMK_EPI_GATE, &ep);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(g, dG, gsz, hipMemcpyDeviceToHost);
+    hipFree(dA); hipFree(dW); hipFree(dG);
+    HIPCHK(e);
+    return LM_OK;
+}
+
 int lm_gemm_split_count(int M, int N, int K)
 {
     if (M < 1 || N < 1 || K < 32 || K % 32) return LM_ERR_INVALID;

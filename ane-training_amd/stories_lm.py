@@ -242,6 +242,8 @@ def lib():
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
         "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
         "lm_gemm_split_count": (I, [I, I, I]),
+        "lm_selftest_gemm_gate": (I, [I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16),
+                                      C.POINTER(C.c_uint16)]),
         "lm_tokenizer_load": (P, [C.c_char_p, I, ip]),
         "lm_tokenizer_free": (None, [P]),
         "lm_tokenizer_vocab_size": (I, [P]),
@@ -422,6 +424,21 @@ def selftest_gemm_split(A16: np.ndarray, W16: np.ndarray, nsplit: int = 0) -> np
         raise LMError(rc, "lm_selftest_gemm_split")
     assert rc == n
     return out
+
+
+def selftest_gemm_gate(A16: np.ndarray, W16: np.ndarray) -> np.ndarray:
+    """Gate [M, N/2] (fp16 bits) of the W1/W3 GEMM with the SiLU-gate epilogue,
+    through the tile the runtime picks for M rows; W16 rows are W1/W3
+    interleaved in blocks of 16."""
+    A16 = np.ascontiguousarray(A16, dtype=np.uint16)
+    W16 = np.ascontiguousarray(W16, dtype=np.uint16)
+    M, K = A16.shape
+    N = W16.shape[0]
+    g = np.empty((M, N // 2), dtype=np.uint16)
+    rc = lib().lm_selftest_gemm_gate(M, N, K, _u16p(A16), _u16p(W16), _u16p(g))
+    if rc:
+        raise LMError(rc, "lm_selftest_gemm_gate")
+    return g
 
 
 class Model:

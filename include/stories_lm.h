@@ -289,6 +289,14 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
 int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, const uint16_t *W,
                            float *parts);
 
+/* Run the W1/W3 GEMM with the SiLU-gate epilogue the forward uses (the tile
+ * the runtime picks for M rows): W [N, K] holds W1 and W3 rows interleaved in
+ * blocks of 16 (block j: W1 rows 16j .. 16j+15, then W3 rows 16j .. 16j+15),
+ * h = A W^T in fp32, and g[m, 16j + c] = fp16(silu(h[m, 32j + c]) *
+ * h[m, 32j + 16 + c]) for c < 16.  A [M, K] fp16 bits, g [M, N/2] fp16 bits;
+ * N a multiple of 32, K of 32. */
+int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t *W, uint16_t *g);
+
 /* The split count the runtime uses for an [M, K] x [N, K]^T GEMM (1: unsplit). */
 int lm_gemm_split_count(int M, int N, int K);
 

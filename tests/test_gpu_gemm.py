@@ -47,3 +47,21 @@ def test_gemm_split_partials(lm, M, N, K, nsplit):
         w = W[:, s * kc:(s + 1) * kc].astype(np.float64)
         scale = np.abs(a) @ np.abs(w).T
         assert np.all(np.abs(P[s] - a @ w.T) <= 1e-5 * scale + 1e-6), s
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 4096, 768), (7, 4096, 768), (32, 11264, 2048), (1, 512, 512),
+                                   (256, 4096, 768), (2048, 4096, 768), (130, 1024, 1024), (33, 2048, 256)])
+def test_gemm_gate_epilogue(lm, M, N, K):
+    """The W1/W3 GEMM with the SiLU-gate epilogue (decode-row tiles, 64x64
+    prefill tiles and 256x128 tiles of eight waves, by M) against float64:
+    silu(h1) * h3 rounded to fp16, W1/W3 rows interleaved in blocks of 16."""
+    rng = np.random.default_rng(M + 5 * N + 7 * K)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float16)
+    g16 = lm.selftest_gemm_gate(A.view(np.uint16), W.view(np.uint16))
+    h = A.astype(np.float64) @ W.astype(np.float64).T
+    i = np.arange(N // 2)
+    h1, h3 = h[:, 32 * (i // 16) + i % 16], h[:, 32 * (i // 16) + 16 + i % 16]
+    ref = h1 / (1.0 + np.exp(-h1)) * h3
+    got = g16.view(np.float16).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(ref) + 2e-5)
