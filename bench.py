@@ -10,13 +10,16 @@ generated token; the timed region replays captured multi-step hipGraphs with
 the argmax fed back on the device, inputs and weights already resident in HBM.
 
 Alongside the headline the JSON line carries:
-  roofline      the dominant kernel family of the decode step (largest device
-                time per token): algorithmic bytes per launch / mean launch
-                duration, measured after the timed region over the 254 decode
-                steps of one sequence of the same chain, each kernel launched
-                with hipEvents at its own dispatch's start and end
-                (lm_profile_chain), so the durations are those of a kernel
-                trace of the chain
+  roofline      the attention kernel of the decode step, the largest kernel of
+                the step in its kernel trace (profiles/): algorithmic bytes per
+                launch / mean launch duration, measured after the timed region
+                over the 254 decode steps of one sequence of the same chain,
+                each kernel launched with hipEvents at its own dispatch's start
+                and end (lm_profile_chain).  Those event times carry a per-launch
+                overhead (no kernel of the step measures under about 3.9 us that
+                way, against 2.7-4.2 us in the trace), too coarse to rank the
+                five layer kernels, so the family is fixed rather than ranked;
+                every family's event time is in kernel_us_per_launch
   step_roofline the whole token: algorithmic bytes per token / time per token
   cpu_baseline  the CPU oracle (a C restatement of the reference's fp32
                 forward, KV-cache decode) timed on this host on the same C0
@@ -289,7 +292,7 @@ def main():
     if launches["wo"] == 0:   # Wo runs inside the attention kernel (per-head shares)
         algo["attn"] += algo.pop("wo")
         del us["wo"], launches["wo"]
-    dom = max(us, key=lambda k: us[k] * launches[k])
+    dom = "attn"   # largest in the kernel trace; event times cannot rank the layer kernels
     dur_us = us[dom]
     achieved = algo[dom] / (dur_us * 1e-6) / 1e9
     step_bytes = sum(algo[k] * launches[k] for k in algo)
