@@ -72,6 +72,7 @@ struct EpiArgs {
     float *q;               /* QKV */
     void *kc, *vc;
     int kv_f32, NQ, NKV, hd, Hkv, max_seq;
+    int lghd;               /* QKV: log2(hd) (hd is a power of two) */
     const int *slot, *pos;
     const float *rope_cos, *rope_sin;
     size_t sstride;         /* STORE of a K-split GEMM: out of split s is out + s*sstride */
@@ -156,7 +157,7 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         const bool rot = n < e.NQ + e.NKV;
         const bool isq = n < e.NQ;
         const int nn = isq ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
-        const int h = nn / e.hd, d = nn % e.hd;
+        const int h = nn >> e.lghd, d = nn & (e.hd - 1);
         const int half_hd = e.hd >> 1;
         int pr[16], sr[16];
         float cr[16], sn[16];
@@ -366,7 +367,7 @@ __device__ __forceinline__ void qkv_item_rope(QkvItem (&it)[NI], int n0, const E
         const int n = n0 + 4 * ((threadIdx.x + k * GT) % (BN / 4));
         const bool rot = n < e.NQ + e.NKV;
         const int nn = n < e.NQ ? n : n - e.NQ;
-        const int ti = rot ? it[k].p * (e.hd >> 1) + ((nn % e.hd) >> 1) : 0;
+        const int ti = rot ? it[k].p * (e.hd >> 1) + ((nn & (e.hd - 1)) >> 1) : 0;
         it[k].c = *(const float2 *)(e.rope_cos + ti);
         it[k].sn = *(const float2 *)(e.rope_sin + ti);
     }
@@ -419,7 +420,7 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
             const int p = its[k].p;
             const bool isq = n < e.NQ, rot = n < e.NQ + e.NKV;
             const int nn = isq ? n : (rot ? n - e.NQ : n - e.NQ - e.NKV);
-            const int d = nn % e.hd;
+            const int d = nn & (e.hd - 1);
             float o[4] = {v.x, v.y, v.z, v.w};
             if (rot) {
                 const float2 c = its[k].c, sn = its[k].sn;
@@ -432,7 +433,7 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
                 *(float4 *)(e.q + (size_t)row * e.NQ + n) = make_float4(o[0], o[1], o[2], o[3]);
             } else {
                 const size_t off =
-                    (((size_t)its[k].sl * e.Hkv + nn / e.hd) * e.max_seq + p) * e.hd + d;
+                    (((size_t)its[k].sl * e.Hkv + (nn >> e.lghd)) * e.max_seq + p) * e.hd + d;
                 void *dst = rot ? e.kc : e.vc;
                 if (e.kv_f32)
                     *(float4 *)((float *)dst + off) = make_float4(o[0], o[1], o[2], o[3]);
@@ -993,6 +994,7 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     e.g = (u16 *)p->g; e.F = p->F;
     e.q = p->q; e.kc = p->kc; e.vc = p->vc; e.kv_f32 = p->kv_f32;
     e.NQ = p->NQ; e.NKV = p->NKV; e.hd = p->hd; e.Hkv = p->Hkv; e.max_seq = p->max_seq;
+    e.lghd = p->hd > 0 ? __builtin_ctz((unsigned)p->hd) : 0;
     e.slot = p->slot; e.pos = p->pos; e.rope_cos = p->rope_cos; e.rope_sin = p->rope_sin;
     e.sstride = 0;
     e.nt = p->stream_out;
@@ -1080,7 +1082,8 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
 {
     if (M < 1 || N < 1 || K < 32 || K % 32 || lda < K || !A || !W || !ep) return hipErrorInvalidValue;
     if (epi == EPI_GATE && (N % 32 || !ep->g)) return hipErrorInvalidValue;
-    if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || (ep->hd & 3) ||
+    if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || ep->hd < 4 ||
+                           (ep->hd & (ep->hd - 1)) ||
                            N != ep->NQ + 2 * ep->NKV))
         return hipErrorInvalidValue;
     if (epi == EPI_RESID && (!ep->out || ep->ldc < N)) return hipErrorInvalidValue;
