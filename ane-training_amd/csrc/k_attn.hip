@@ -211,9 +211,9 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_blk(
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int seq = blockIdx.x / nqb, qb = blockIdx.x % nqb;
+    const int seq = small_div(blockIdx.x, nqb), qb = blockIdx.x - seq * nqb;
     const int h = blockIdx.y;
-    const int kvh = h / (H / Hkv);
+    const int kvh = small_div(h, small_div(H, Hkv));
     const int NQ = H * HD;
     const int row0 = seq * S + qb * BQB;          /* first row of the block       */
     const int nrows = min(BQB, S - qb * BQB);     /* valid rows of the block      */
@@ -334,9 +334,9 @@ __global__ void __launch_bounds__(AT) k_attn_prefill_split(
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int seq = blockIdx.x / nqb, qb = blockIdx.x % nqb;
+    const int seq = small_div(blockIdx.x, nqb), qb = blockIdx.x - seq * nqb;
     const int h = blockIdx.y;
-    const int kvh = h / (H / Hkv);
+    const int kvh = small_div(h, small_div(H, Hkv));
     const int NQ = H * HD;
     const int row0 = seq * S + qb * BQS;           /* first row of the block       */
     const int nrows = min(BQS, S - qb * BQS);       /* valid rows of the block      */

@@ -109,6 +109,15 @@ __device__ __forceinline__ float wave_sum(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+/* n / d for 0 <= n < 2^20 and 1 <= d < 2^12 without the integer-division
+ * sequence: the quotient (n + 0.5) / d keeps at least 1/(2d) from an integer,
+ * far more than the error of the hardware reciprocal and the product
+ * (about n * 2^-22), so truncation gives the exact integer quotient. */
+__device__ __forceinline__ int small_div(int n, int d)
+{
+    return (int)(((float)n + 0.5f) * __builtin_amdgcn_rcpf((float)d));
+}
+
 __device__ __forceinline__ float readlane_f(float v, int lane)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));

@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(WG) k_qkv_rope(
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         ps[b] = b < B ? pos[b] : 0;
-        const int ti = ps[b] * half_hd + ((rr % hd) >> 1);
+        const int ti = ps[b] * half_hd + ((rr & (hd - 1)) >> 1);
         cr[b] = rot ? rc[ti] : 1.f;
         sr[b] = rot ? rs[ti] : 0.f;
     }
@@ -248,8 +248,10 @@ __global__ void __launch_bounds__(WG) k_qkv_rope(
     hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
     if (lane != 0) return;
-    const int Hkv = NKV / hd;
-    const int h = rr / hd, d = rr % hd;
+    /* hd is a power of two (64 or 128) */
+    const int lg = __builtin_ctz((unsigned)hd);
+    const int Hkv = NKV >> lg;
+    const int h = rr >> lg, d = rr & (hd - 1);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         if (b >= B) break;
@@ -347,7 +349,7 @@ __device__ __forceinline__ void attn_head(
     const int ntiles = (vis + TILE - 1) / TILE;
     const int dq = lane % G, pp = lane / G;
     const int cs = slot ? slot[b] : b;
-    const size_t base = ((size_t)cs * Hkv + h / (H / Hkv)) * max_seq * HD + dq * 8;
+    const size_t base = ((size_t)cs * Hkv + small_div(h, small_div(H, Hkv))) * max_seq * HD + dq * 8;
     const KT *K = kc + base;
     const KT *V = vc + base;
     /* scores in log2 units: exp(x) = exp2(x * log2 e), the hardware exp2 */
@@ -391,7 +393,7 @@ __device__ __forceinline__ void attn_head(
         const int t = threadIdx.x;
         if (t < 3 * HD / 4) {
             const int vec = t / (HD / 4), e4 = (t % (HD / 4)) * 4;
-            const int g = h / (H / Hkv);
+            const int g = small_div(h, small_div(H, Hkv));
             const int col = vec == 0 ? h * HD : (vec == 1 ? qp->NQ + g * HD : qp->NQ + qp->NKV + g * HD);
             const float *src = qp->part + (size_t)b * (qp->NQ + 2 * qp->NKV) + col + e4;
             const int ns = qp->ns;
