@@ -20,18 +20,23 @@
  * A[l%32][8*(l/32) .. +8], B[8*(l/32) .. +8][l%32] (= W[n0 + l%32][k ..]), and
  * accumulator i holds C[8*(i/4) + 4*(l/32) + i%4][l%32].
  *
- * Two kernels:
- *   k_gemm_tile    work-group tile BM x BN (64 x 64 for most shapes, 256 x 128
- *                  for the largest, 64 x 128 for decode-row classifiers), four
- *                  waves 2 x 2, K streamed by direct global->LDS loads into a
- *                  3-deep ring of 64-wide stages; XCD-aware tile order; an
- *                  optional K-split over blockIdx.y (fp32 partials, summed by
- *                  the kernel that next reads them)
+ * Kernels:
+ *   k_gemm_tile    work-group tile BM x BN: 64 x 64 for most shapes (four waves
+ *                  2 x 2), 256 x 128 for the largest (eight waves 4 x 2), 64 x 128
+ *                  for decode-row classifiers, 32 x 64 for up to 32 rows (two
+ *                  waves); K streamed by direct global->LDS loads into a ring of
+ *                  64-wide stages (3 deep for prefill, 4 for decode rows, 6 for
+ *                  32-row gate tiles); XCD-aware tile order; an optional K-split
+ *                  over blockIdx.y (fp32 partials, summed by the kernel that
+ *                  next reads them)
  *   k_gemm_skinny  decode rows (M <= 64) whose K is not a multiple of 64: a
  *                  work-group owns 32 columns and all rows of one K-chunk; its
  *                  four waves split the chunk, stream their weight fragments
  *                  straight from HBM into registers and add their partial tiles
- *                  through LDS.
+ *                  through LDS
+ *   k_rownorm      row norm with the residual add of pending partials, one wave
+ *                  per row (from 512 rows); k_rownorm_blk, one work-group per
+ *                  row, below that
  */
 #include <type_traits>
 
