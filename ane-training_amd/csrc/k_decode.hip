@@ -1,5 +1,8 @@
 /*
- * k_decode.hip — small-batch (B <= 4) decode kernels for gfx950.
+ * k_decode.hip — decode kernels for gfx950: the small-batch (B <= 4) chain, and
+ * the attention of decode rows for every batch size (k_attn_decode; after a
+ * K-split QKV GEMM of 5..64 rows, k_attn_decode_part, which first sums q, k, v
+ * from the GEMM's partials, rotates and appends them).
  *
  * One decode step of one layer is five launches, shaped after the reference's
  * fused forward programs (training/training_dynamic/mil_dynamic.h:56-288) and
@@ -29,8 +32,9 @@
 
 /* Launch-timing slot for lm_profile_chain: when armed, the next decode-chain
  * kernel launch of this host thread goes through hipExtLaunchKernelGGL with the
- * two events, which the device timestamps at that dispatch's start and end
- * (the kernel's own duration, as a kernel trace reports it). */
+ * two events, which the device timestamps at that dispatch's start and end.
+ * That span includes dispatch overhead a kernel trace leaves out: no kernel of
+ * the chain measures under about 3.9 us this way. */
 static thread_local hipEvent_t t_ev0, t_ev1;
 static thread_local int t_armed;
 
