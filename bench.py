@@ -284,7 +284,7 @@ def main():
 
     # device time per launch of each kernel family inside the decode chain over the
     # positions of a timed sequence (254 steps from position 0): every kernel timed
-    # by hipEvents at its own dispatch's start and end, as a kernel trace reports it
+    # by hipEvents at its own dispatch's start and end (plus dispatch overhead)
     us, launches = m.profile_chain([1], [0], SEQ - 2)
     mean_ctx = (SEQ + 1) / 2
     kvb = 2 if args.kv16 else 4

@@ -323,8 +323,9 @@ int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int 
 /* Mean device microseconds per launch of each decode kernel family inside the
  * real decode chain: `steps` greedy decode steps of B rows from tokens[b] at
  * positions pos[b] (advancing as a decode does), launched directly, every
- * kernel timed by events at its own dispatch's start and end (the durations a
- * kernel trace reports).  One untimed step runs first.  launches_per_step as in
+ * kernel timed by events at its own dispatch's start and end (the kernel plus
+ * a dispatch overhead a kernel trace leaves out; no kernel measures under
+ * about 3.9 us).  One untimed step runs first.  launches_per_step as in
  * lm_profile_decode.  Needs pos[b] + steps + 1 <= max_seq; leaves the KV cache
  * at those positions and the activations overwritten. */
 int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int steps,
