@@ -31,7 +31,7 @@ def test_gemm_matches_numpy(lm, M, N, K, a_f32):
 
 @pytest.mark.parametrize("M,N,K", [(64, 768, 768), (64, 768, 2048), (64, 2304, 768), (7, 768, 768),
                                    (32, 2048, 5632), (33, 200, 512), (200, 768, 768), (130, 200, 512),
-                                   (1000, 768, 2048), (20, 200, 96)])
+                                   (1000, 768, 2048), (20, 200, 96), (2048, 768, 2048), (1100, 700, 2048)])
 @pytest.mark.parametrize("nsplit", [0, 2])
 def test_gemm_split_partials(lm, M, N, K, nsplit):
     """Each K-split partial is the product over its own K-chunk."""
