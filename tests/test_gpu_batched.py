@@ -210,6 +210,22 @@ def test_stories_c1_prefill_logits(lm, orc):
     m.close()
 
 
+def test_stories_c3_forward_logits(lm, orc):
+    """Config C3: 8 prompts of 256 tokens in one batched prefill (2048 rows: the
+    256x128 gate tiles and the W2 on 128x128 tiles K-split in 2), all logits;
+    prompts 0 and 7 against the oracle."""
+    _say("[stories C3 forward]")
+    d = lm.STORIES_110M
+    m, w16 = make(lm, d, 1, 8, 256)
+    toks = np.random.default_rng(103).integers(0, 32000, (8, 256)).astype(np.int32)
+    lg = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL).reshape(8, 256, -1)
+    o = orc.Oracle(cfg7(d), lm.f16_to_f32(w16), True, 256, kv_f16=True)
+    for b in (0, 7):
+        close_enough(lg[b], o.forward_full(toks[b]))
+    o.close()
+    m.close()
+
+
 def test_stories_c2_batched_decode(lm, orc):
     """Config C2 shape (64 slots, Stories) on short prompts: 4 sequences checked
     against the oracle, teacher-forced and greedy."""
