@@ -22,9 +22,10 @@
  *
  * Kernels:
  *   k_gemm_tile    work-group tile BM x BN: 64 x 64 for most shapes (four waves
- *                  2 x 2), 256 x 128 for the largest (eight waves 4 x 2), 64 x 128
- *                  for decode-row classifiers, 32 x 64 for up to 32 rows (two
- *                  waves); K streamed by direct global->LDS loads into a ring of
+ *                  2 x 2), 256 x 128 for the largest (eight waves 4 x 2), 128 x 128
+ *                  (eight waves) K-split in 2 for long-K narrow GEMMs of 1024+
+ *                  rows, 64 x 128 for decode-row classifiers, 32 x 64 for up to
+ *                  32 rows (two waves); K streamed by direct global->LDS loads into a ring of
  *                  64-wide stages (3 deep for prefill, 4 for decode rows, 6 for
  *                  32-row gate tiles); XCD-aware tile order; an optional K-split
  *                  over blockIdx.y (fp32 partials, summed by the kernel that
