@@ -782,6 +782,9 @@ __global__ void __launch_bounds__(256) k_rownorm(float *__restrict__ x, int M,
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;                       /* wave-uniform; no barrier below */
     float *xr = x + (size_t)m * D + 4 * lane;
+    float4 gv[C4];                            /* gain, loaded first: its latency */
+#pragma unroll                                /* overlaps the row's loads        */
+    for (int c = 0; c < C4; c++) gv[c] = *(const float4 *)(gain + 4 * lane + c * 256);
     float4 v[C4];
     if (emb) {
         const u16 *er = emb + (size_t)tok[m] * D + 4 * lane;
@@ -828,10 +831,9 @@ __global__ void __launch_bounds__(256) k_rownorm(float *__restrict__ x, int M,
     ss = wave_sum(ss);
     const float rs = 1.0f / sqrtf(ss / D + 1e-5f);
     u16 *xo = xn + (size_t)m * D + 4 * lane;
-    const float *gr = gain + 4 * lane;
 #pragma unroll
     for (int c = 0; c < C4; c++) {
-        const float4 g = *(const float4 *)(gr + c * 256);
+        const float4 g = gv[c];
         const unsigned lo = (unsigned)f2h(v[c].x * rs * g.x) | ((unsigned)f2h(v[c].y * rs * g.y) << 16);
         const unsigned hi = (unsigned)f2h(v[c].z * rs * g.z) | ((unsigned)f2h(v[c].w * rs * g.w) << 16);
         *(uint2 *)(xo + c * 256) = make_uint2(lo, hi);
@@ -861,6 +863,19 @@ __global__ void __launch_bounds__(GT) k_rownorm_blk(float *__restrict__ x, int M
     /* value i of this thread is column col(i) = (i/4)*1024 + 4t + i%4 (D >= 1024),
      * or t*PER + i (D < 1024) */
     auto col = [&](int c) { return PER >= 4 ? c * (4 * GT) + 4 * t : t * PER; };
+    /* gain, loaded first so its latency overlaps the row's loads (C2 and C4
+     * decode steps 0.5% faster than loading it after the reduction) */
+    float gl[C4 * 4];
+#pragma unroll
+    for (int c = 0; c < C4; c++) {
+        if (PER >= 4) {
+            const float4 g4 = *(const float4 *)(gain + col(c));
+            gl[4 * c] = g4.x; gl[4 * c + 1] = g4.y; gl[4 * c + 2] = g4.z; gl[4 * c + 3] = g4.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; i++) gl[i] = gain[col(0) + i];
+        }
+    }
     float v[C4 * 4];
     if (emb) {
         const u16 *er = emb + (size_t)tok[m] * D;
@@ -949,13 +964,13 @@ __global__ void __launch_bounds__(GT) k_rownorm_blk(float *__restrict__ x, int M
 #pragma unroll
     for (int c = 0; c < C4; c++) {
         if (PER >= 4) {
-            const float4 g = *(const float4 *)(gain + col(c));
-            const unsigned lo = (unsigned)f2h(v[4 * c] * rs * g.x) | ((unsigned)f2h(v[4 * c + 1] * rs * g.y) << 16);
-            const unsigned hi = (unsigned)f2h(v[4 * c + 2] * rs * g.z) | ((unsigned)f2h(v[4 * c + 3] * rs * g.w) << 16);
+            const float *g = gl + 4 * c;
+            const unsigned lo = (unsigned)f2h(v[4 * c] * rs * g[0]) | ((unsigned)f2h(v[4 * c + 1] * rs * g[1]) << 16);
+            const unsigned hi = (unsigned)f2h(v[4 * c + 2] * rs * g[2]) | ((unsigned)f2h(v[4 * c + 3] * rs * g[3]) << 16);
             *(uint2 *)(xo + col(c)) = make_uint2(lo, hi);
         } else {
 #pragma unroll
-            for (int i = 0; i < PER; i++) xo[col(0) + i] = f2h(v[i] * rs * gain[col(0) + i]);
+            for (int i = 0; i < PER; i++) xo[col(0) + i] = f2h(v[i] * rs * gl[i]);
         }
     }
 }
