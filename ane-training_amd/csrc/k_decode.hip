@@ -324,11 +324,11 @@ struct QkvPart {
     KT *kc, *vc;            /* the cache, written at the current position */
 };
 
-template <int HD, typename KT, typename Hook>
+template <int HD, typename KT>
 __device__ __forceinline__ void attn_head(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    float *oh, Hook after_first_loads, const QkvPart<KT> *qp = nullptr)
+    float *oh, const QkvPart<KT> *qp = nullptr)
 {
     /* positions per tile: 32 (measured against 64: the four waves share short
      * contexts more evenly).  Two tiles fit the registers except at hd 128 with
@@ -443,10 +443,6 @@ __device__ __forceinline__ void attn_head(
             if (lane == 0) scur = d * scale;
         }
     }
-    /* loads issued here queue behind the first tile's (memory loads complete
-     * in order for the wait counter), so waiting for that tile does not wait
-     * for them */
-    after_first_loads();
     /* Sum over each aligned group of G lanes, in every lane of the group: the
      * xor-1/2/4(/8) butterfly as DPP moves (after each step the value is
      * uniform over quads, then octets, so the half-row and row mirrors pair the
@@ -582,7 +578,7 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
     float *__restrict__ out, u16 *__restrict__ out16)
 {
     __shared__ float oh[HD];
-    attn_head<HD, KT>(q, kc, vc, pos, slot, H, Hkv, max_seq, oh, [] {});
+    attn_head<HD, KT>(q, kc, vc, pos, slot, H, Hkv, max_seq, oh);
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     if (d < HD) {
         if (out16) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
@@ -602,70 +598,9 @@ __global__ void __launch_bounds__(WG) k_attn_decode_part(
 {
     __shared__ float oh[HD];
     const QkvPart<KT> qp = {part, sstride, ns, NQ, NKV, rc, rs, kc, vc};
-    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, [] {}, &qp);
+    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, &qp);
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     if (d < HD) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
-}
-
-/* ---- attention + Wo of one head ------------------------------------------------ */
-
-/* Work-group (h, b), batch-1..4 decode: the head's Wo columns Wo[:, h*HD ..+HD]
- * (D rows of HD fp16, row stride NQ) are copied into LDS by direct global->LDS
- * loads issued first, so they arrive while the attention runs (forward.h:72-99);
- * then part[(b*H + h)*D + r] = Wo[r, h*HD ..] . o_h, the head's share of the Wo
- * product (forward.h:134).  The W1/W3 and W2 kernels add the H shares to the
- * residual stream in head order (forward.h:136).  8 (HD 64) or 16 (HD 128)
- * lanes per Wo row; their partial sums meet through DPP. */
-template <int HD, typename KT, int D>
-__global__ void __launch_bounds__(WG) k_attn_wo(
-    const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
-    const int *__restrict__ pos, int H, int Hkv, int max_seq, const u16 *__restrict__ Wo,
-    float *__restrict__ part)
-{
-    constexpr int CPR = HD / 8;                /* 16-byte chunks per Wo row segment */
-    constexpr int NI = D * CPR / WG;           /* load instructions per lane        */
-    static_assert(D * CPR % WG == 0 && (CPR == 8 || CPR == 16), "shape");
-    __shared__ __attribute__((aligned(1024))) u16 swo[D * HD];
-    __shared__ float oh[HD];
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int NQ = H * HD;
-    /* instruction i of wave w moves chunks c = (i*NWAVE + w)*64 + lane: row
-     * c / CPR, chunk c % CPR, to swo[c*8 ..] (rows of HD halves back to back) */
-    auto load_wo = [&] {
-#pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const int c = (i * NWAVE + wave) * 64 + lane;
-            const u16 *src = Wo + (size_t)(c / CPR) * NQ + h * HD + (c % CPR) * 8;
-            __builtin_amdgcn_global_load_lds(
-                (const void *)src,
-                (__attribute__((address_space(3))) void *)(swo + (i * NWAVE + wave) * 64 * 8), 16, 0, 0);
-        }
-    };
-    attn_head<HD, KT>(q, kc, vc, pos, nullptr, H, Hkv, max_seq, oh, load_wo);
-    __builtin_amdgcn_s_waitcnt(0x0F70);        /* vmcnt(0): this wave's Wo chunks landed */
-    __syncthreads();                            /* ... and every wave's */
-    const int cc = tid % CPR;                   /* chunk of the row segment */
-    float o8[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) o8[j] = oh[cc * 8 + j];
-    constexpr int RPP = WG / CPR;               /* rows per pass */
-    float *pb = part + ((size_t)b * H + h) * D;
-#pragma unroll 8
-    for (int j = 0; j < D / RPP; j++) {
-        const int r = tid / CPR + j * RPP;
-        float w[8];
-        unpack8(*(const uint4 *)(swo + (r * CPR + cc) * 8), w);
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) s = fmaf(w[j], o8[j], s);
-        s += dpp_f<DPP_QUAD_XOR1>(s);
-        s += dpp_f<DPP_QUAD_XOR2>(s);
-        s += dpp_f<DPP_ROW_HALF_MIRROR>(s);
-        if (CPR == 16) s += dpp_f<DPP_ROW_MIRROR>(s);
-        if (cc == 0) pb[r] = s;
-    }
 }
 
 /* ---- Wo + residual ---------------------------------------------------------- */
@@ -706,7 +641,7 @@ __global__ void __launch_bounds__(WG) k_wo_residual(
 template <int D, int NB>
 __global__ void __launch_bounds__(WG) k_ffn13(
     float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W13,
-    int F, int B, float *__restrict__ g, const float *__restrict__ part, int nh)
+    int F, int B, float *__restrict__ g)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     const int i0 = blockIdx.x * NWAVE + (threadIdx.x >> 6);
@@ -718,32 +653,6 @@ __global__ void __launch_bounds__(WG) k_ffn13(
     hw_load<D>(W13 + row * D, hl, wv);
     NormIn<D, NB> in;
     norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
-    /* with part: the normalised row is x + the nh per-head Wo shares, added in
-     * head order (the same sum k_w2_residual stores) */
-    if (part) {
-        /* heads in groups of four: a group's loads are all issued before its
-         * adds, which stay in head order */
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if (b >= B) break;
-            const float *pb = part + (size_t)b * nh * D + threadIdx.x;
-            int hh = 0;
-            for (; hh + 4 <= nh; hh += 4) {
-                float t[4][D / WG];
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-#pragma unroll
-                    for (int j = 0; j < D / WG; j++) t[u][j] = pb[(size_t)(hh + u) * D + j * WG];
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-#pragma unroll
-                    for (int j = 0; j < D / WG; j++) in.v[b][j] += t[u][j];
-            }
-            for (; hh < nh; hh++)
-#pragma unroll
-                for (int j = 0; j < D / WG; j++) in.v[b][j] += pb[(size_t)hh * D + j * WG];
-        }
-    }
     norm_to_lds<D, NB>(in, B, x, false, xs);
     if (i0 >= F) return;
     float acc[NB], h1[NB], h3[NB];
@@ -764,7 +673,7 @@ __global__ void __launch_bounds__(WG) k_ffn13(
 template <int F, int NB>
 __global__ void __launch_bounds__(WG) k_w2_residual(
     const float *__restrict__ g, const u16 *__restrict__ W, int D, int B,
-    float *__restrict__ x, int npairs, const float *__restrict__ part, int nh)
+    float *__restrict__ x, int npairs)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * F];
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
@@ -778,29 +687,6 @@ __global__ void __launch_bounds__(WG) k_w2_residual(
 #pragma unroll
     for (int b = 0; b < NB; b++)
         xo[b] = b < B ? *(const float2 *)(x + (size_t)b * D + r) : make_float2(0.f, 0.f);
-    if (part) {   /* residual of the per-head Wo shares first, in head order */
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if (b >= B) break;
-            const float *pb = part + (size_t)b * nh * D + r;
-            int hh = 0;
-            for (; hh + 4 <= nh; hh += 4) {   /* loads of four heads, then their adds in order */
-                float2 t[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) t[u] = *(const float2 *)(pb + (size_t)(hh + u) * D);
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    xo[b].x += t[u].x;
-                    xo[b].y += t[u].y;
-                }
-            }
-            for (; hh < nh; hh++) {
-                const float2 t = *(const float2 *)(pb + (size_t)hh * D);
-                xo[b].x += t.x;
-                xo[b].y += t.y;
-            }
-        }
-    }
     rows_to_lds<F, NB>(in, xs);
     if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
@@ -1044,67 +930,30 @@ extern "C" int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t 
 }
 
 extern "C" int lmk_ffn13(hipStream_t s, float *x, const float *rms_w, const uint16_t *w13, int D,
-                         int F, int B, float *g, const float *part, int nh)
+                         int F, int B, float *g)
 {
-    if (B < 1 || B > 4 || F % LMK_GATE_BLOCK || (part && nh < 1)) return hipErrorInvalidValue;
+    if (B < 1 || B > 4 || F % LMK_GATE_BLOCK) return hipErrorInvalidValue;
     dim3 grid((F + NWAVE - 1) / NWAVE);
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        DLAUNCH((k_ffn13<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, w13, F, B, g, part, nh);
+        DLAUNCH((k_ffn13<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, w13, F, B, g);
     }));
     return hipGetLastError();
 }
 
 extern "C" int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D, int F, int B,
-                               float *x, const float *part, int nh)
+                               float *x)
 {
-    if (B < 1 || B > 4 || (D & 1) || (part && nh < 1)) return hipErrorInvalidValue;
+    if (B < 1 || B > 4 || (D & 1)) return hipErrorInvalidValue;
     const int npairs = D / 2;
     dim3 grid((npairs + NWAVE - 1) / NWAVE);
     DISPATCH_K(F, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        DLAUNCH((k_w2_residual<K_, NB_>), grid, dim3(WG), 0, s, g, w2, D, B, x, npairs,
-                           part, nh);
+        DLAUNCH((k_w2_residual<K_, NB_>), grid, dim3(WG), 0, s, g, w2, D, B, x, npairs);
     }));
     return hipGetLastError();
 }
 
-
-/* Fused attention + Wo shares: shapes whose Wo head block fits the LDS. */
-extern "C" int lmk_attn_wo_supported(int D, int hd)
-{
-    return (hd == 64 && (D == 256 || D == 512 || D == 768 || D == 1024)) ||
-           (hd == 128 && (D == 256 || D == 512));
-}
-
-extern "C" int lmk_attn_wo(hipStream_t s, const float *q, const void *kc, const void *vc, int kv_f32,
-                           const int *pos, int B, int H, int Hkv, int hd, int max_seq, int D,
-                           const uint16_t *wo, float *part)
-{
-    if (B < 1 || B > 65535 || H < 1 || Hkv < 1 || H % Hkv || H * hd != D ||
-        !lmk_attn_wo_supported(D, hd) || !q || !kc || !vc || !pos || !wo || !part)
-        return hipErrorInvalidValue;
-    dim3 grid(H, B);
-#define LAUNCH_AWO(HD_, D_)                                                                       \
-    do {                                                                                          \
-        if (kv_f32)                                                                               \
-            DLAUNCH((k_attn_wo<HD_, float, D_>), grid, dim3(WG), 0, s, q,             \
-                               (const float *)kc, (const float *)vc, pos, H, Hkv, max_seq,       \
-                               (const u16 *)wo, part);                                            \
-        else                                                                                      \
-            DLAUNCH((k_attn_wo<HD_, u16, D_>), grid, dim3(WG), 0, s, q,               \
-                               (const u16 *)kc, (const u16 *)vc, pos, H, Hkv, max_seq,           \
-                               (const u16 *)wo, part);                                            \
-    } while (0)
-    if (hd == 64 && D == 256) LAUNCH_AWO(64, 256);
-    else if (hd == 64 && D == 512) LAUNCH_AWO(64, 512);
-    else if (hd == 64 && D == 768) LAUNCH_AWO(64, 768);
-    else if (hd == 64 && D == 1024) LAUNCH_AWO(64, 1024);
-    else if (hd == 128 && D == 256) LAUNCH_AWO(128, 256);
-    else LAUNCH_AWO(128, 512);
-#undef LAUNCH_AWO
-    return hipGetLastError();
-}
 
 extern "C" int lmk_cls_nblk(int V) { return (V + CLS_ROWS_PER_WG - 1) / CLS_ROWS_PER_WG; }
 

@@ -30,11 +30,6 @@
  *                  32-row gate tiles); XCD-aware tile order; an optional K-split
  *                  over blockIdx.y (fp32 partials, summed by the kernel that
  *                  next reads them)
- *   k_gemm_skinny  decode rows (M <= 64) whose K is not a multiple of 64: a
- *                  work-group owns 32 columns and all rows of one K-chunk; its
- *                  four waves split the chunk, stream their weight fragments
- *                  straight from HBM into registers and add their partial tiles
- *                  through LDS
  *   k_rownorm      row norm with the residual add of pending partials, one wave
  *                  per row (from 512 rows); k_rownorm_blk, one work-group per
  *                  row, below that
@@ -639,119 +634,6 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
             epilogue_tile<E>(acc[i][j], m0 + wm * WM + i * 32, n0 + wn * WN + j * 32, e);
 }
 
-/* ---- skinny GEMM (decode batches, M <= 64) ---------------------------------- */
-
-/* Work-group (32-column block x, K-split y): columns 32x .. 32x+31, k-steps of
- * 16 of its chunk cut between the four waves.  A wave fetches SK k-steps at a
- * time (one weight fragment and MT activation fragments per step, straight into
- * registers) one stage ahead of the MFMAs.  Every fetch is unconditional: steps
- * past the wave's range load the last valid step again and are zeroed, so the
- * loads form straight-line code whose outstanding count the compiler tracks
- * exactly (a load behind a branch would make it wait for every load in flight,
- * the next stage's included).  SK matches the wave's step count for short
- * chunks. */
-template <int MT, int SK, int E>
-__global__ void __launch_bounds__(GT) k_gemm_skinny(const u16 *__restrict__ A, int lda,
-                                                    const u16 *__restrict__ W, int K, int kc,
-                                                    EpiArgs e)
-{
-    __shared__ float red[3][MT * 16][64];
-    /* MFMA instructions execute whatever the EXEC mask says, so every branch
-     * around them must be wave-uniform in the compiler's eyes: the wave index
-     * goes through readfirstlane and all K-range tests become scalar branches */
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * 32;
-    const int M = e.M, N = e.N;
-    const int nsteps = kc / 16;                   /* k-steps of this work-group    */
-    const int sb = blockIdx.y * nsteps;           /* its first k-step              */
-    const int per = (nsteps + 3) / 4;             /* k-steps of this wave's slice  */
-    const int s0 = sb + wave * per, s1 = min(sb + nsteps, s0 + per);
-    const int nstage = s1 > s0 ? (s1 - s0 + SK - 1) / SK : 0;
-    const int wrow = min(n0 + (lane & 31), N - 1);
-    const int koff = (lane >> 5) * 8;
-    const u16 *wp = W + (size_t)wrow * K + koff;
-    const u16 *ap[MT];
-#pragma unroll
-    for (int i = 0; i < MT; i++) ap[i] = A + (size_t)min(i * 32 + (lane & 31), M - 1) * lda + koff;
-
-    f32x16 acc[MT];
-#pragma unroll
-    for (int i = 0; i < MT; i++) acc[i] = (f32x16){};
-
-    uint4 fb[2][SK], fa[2][SK][MT];
-    auto fetch = [&](int st, int b) {
-#pragma unroll
-        for (int j = 0; j < SK; j++) {
-            const int sv = s0 + st * SK + j;
-            const int sc = min(sv, s1 - 1);
-            const uint4 w = *(const uint4 *)(wp + sc * 16);
-            fb[b][j] = sv < s1 ? w : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < MT; i++) fa[b][j][i] = *(const uint4 *)(ap[i] + sc * 16);
-        }
-    };
-    auto consume = [&](int b) {
-#pragma unroll
-        for (int j = 0; j < SK; j++)
-#pragma unroll
-            for (int i = 0; i < MT; i++) acc[i] = mfma32(fa[b][j][i], fb[b][j], acc[i]);
-    };
-    if (nstage == 1) {
-        fetch(0, 0);
-        consume(0);
-    } else if (nstage > 1) {
-        fetch(0, 0);
-        for (int st = 0; st < nstage; st += 2) {
-            fetch(st + 1, 1);
-            consume(0);
-            fetch(st + 2, 0);
-            consume(1);
-        }
-    }
-    /* sum the four waves' partial tiles */
-    if (wave > 0) {
-#pragma unroll
-        for (int i = 0; i < MT; i++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) red[wave - 1][i * 16 + v][lane] = acc[i][v];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-#pragma unroll
-            for (int v = 0; v < 16; v++)
-                acc[i][v] += red[0][i * 16 + v][lane] + red[1][i * 16 + v][lane] +
-                             red[2][i * 16 + v][lane];
-            epilogue_tile<E>(acc[i], i * 32, n0, e);
-        }
-    }
-}
-
-/* Launch the skinny kernel over grid (N/32, ns) with k-chunk kc = K/ns. */
-template <int E>
-static void launch_skinny(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
-                          int N, int K, int ns, const EpiArgs &e)
-{
-    const int kc = K / ns;
-    const int per = (kc / 16 + 3) / 4;            /* k-steps per wave */
-    dim3 grid((N + 31) / 32, ns);
-#define SKL(MT_, SK_)                                                                            \
-    hipLaunchKernelGGL((k_gemm_skinny<MT_, SK_, E>), grid, dim3(GT), 0, s, (const u16 *)A, lda,   \
-                       (const u16 *)W, K, kc, e)
-#define SKL_MT(SK_)            \
-    if (M <= 32) SKL(1, SK_);  \
-    else SKL(2, SK_);
-    if (per <= 1) { SKL_MT(1) }
-    else if (per <= 2) { SKL_MT(2) }
-    else if (per <= 4) { SKL_MT(4) }
-    else { SKL_MT(8) }
-#undef SKL_MT
-#undef SKL
-}
-
 /* ---- per-row RMSNorm ------------------------------------------------------------ */
 
 /* Row norm, one wave per row m, four rows per work-group (forward.h:46-53): with
@@ -1082,17 +964,13 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * traffic wins; a decode-row classifier (N >= 16384) takes a 64 x 128 tile;
  * up to 32 rows take 32 x 64 tiles of two waves (a 64-row tile would stage and
  * multiply half padding: 5% faster on the scaled model's 32-row QKV and W2;
- * the LDS-staged QKV epilogue keeps its four-wave 64-row tile).
- * K not a multiple of 64 (decode rows only) falls back to the skinny kernel. */
+ * the LDS-staged QKV epilogue keeps its four-wave 64-row tile).  K is a
+ * multiple of the 64-wide stage. */
 template <int E>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
 {
-    if (K % BKH) {
-        if (M > 64) return hipErrorInvalidValue;
-        launch_skinny<E>(s, A, lda, W, M, N, K, 1, e);
-        return hipGetLastError();
-    }
+    if (K % BKH) return hipErrorInvalidValue;
     if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
     else if (E != EPI_QKV && M <= 32) {
@@ -1104,7 +982,7 @@ static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t
 extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                         int K, int epi, const LMEpilogue *ep)
 {
-    if (M < 1 || N < 1 || K < 32 || K % 32 || lda < K || !A || !W || !ep) return hipErrorInvalidValue;
+    if (M < 1 || N < 1 || K < BKH || K % BKH || lda < K || !A || !W || !ep) return hipErrorInvalidValue;
     if (epi == EPI_GATE && (N % 32 || !ep->g)) return hipErrorInvalidValue;
     if (epi == EPI_QKV && (!ep->q || !ep->kc || !ep->vc || !ep->slot || !ep->pos || ep->hd < 4 ||
                            (ep->hd & (ep->hd - 1)) ||
@@ -1151,21 +1029,19 @@ extern "C" int lmk_pick_split(int M, int N, int K)
     return best;
 }
 
-/* The K-split GEMM on 64 x 64 tiles (grid: tiles x ns), or for decode rows
- * whose chunks are not a multiple of 64 the skinny kernel. */
+/* The K-split GEMM (grid: tiles x ns); every k-chunk is a multiple of the
+ * 64-wide stage. */
 extern "C" int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M,
                               int N, int K, int ns, float *part)
 {
-    if (M < 1 || N < 1 || ns < 1 || ns > LMK_MAX_SPLIT || K % (16 * ns) || lda < K || !A || !W ||
+    if (M < 1 || N < 1 || ns < 1 || ns > LMK_MAX_SPLIT || K % (BKH * ns) || lda < K || !A || !W ||
         !part)
         return hipErrorInvalidValue;
     EpiArgs e = {};
     e.M = M; e.N = N; e.out = part; e.ldc = N; e.nparts = (N + 31) / 32;
     e.sstride = (size_t)M * N;
     if (ns == 2 && wide_split(M, N, K)) launch_tile_split<128, 128>(s, A, lda, W, M, N, K, ns, e);
-    else if (K % (BKH * ns) == 0 && M <= 32) launch_tile_split<32, 64>(s, A, lda, W, M, N, K, ns, e);
-    else if (K % (BKH * ns) == 0) launch_tile_split<64, 64>(s, A, lda, W, M, N, K, ns, e);
-    else if (M <= 64) launch_skinny<EPI_STORE>(s, A, lda, W, M, N, K, ns, e);
-    else return hipErrorInvalidValue;
+    else if (M <= 32) launch_tile_split<32, 64>(s, A, lda, W, M, N, K, ns, e);
+    else launch_tile_split<64, 64>(s, A, lda, W, M, N, K, ns, e);
     return hipGetLastError();
 }

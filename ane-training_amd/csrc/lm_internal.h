@@ -67,25 +67,13 @@ int lmk_attn_decode(hipStream_t s, const float *q, const void *kc,
 int lmk_wo_residual(hipStream_t s, const float *attn, const uint16_t *wo, int D,
                     int B, float *x);
 
-/* xn = rmsnorm(x[b] (+ the nh Wo shares part[b][h], in head order, when part
- * != NULL)) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
+/* xn = rmsnorm(x[b]) * w; g[b, i] = silu(W1[i] . xn) * (W3[i] . xn). */
 int lmk_ffn13(hipStream_t s, float *x, const float *rms_w,
-              const uint16_t *w13, int D, int F, int B, float *g, const float *part, int nh);
+              const uint16_t *w13, int D, int F, int B, float *g);
 
-/* x[b, r] += (the nh Wo shares part[b][h][r], in head order, when part !=
- * NULL) + W2[r, :] . g[b, :] */
+/* x[b, r] += W2[r, :] . g[b, :] */
 int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
-                    int F, int B, float *x, const float *part, int nh);
-
-
-/* Attention of head h, row b, fused with that head's share of Wo:
- * part[(b*H + h)*D + r] = Wo[r, h*hd .. +hd] . attn(b, h) (D = H*hd, slot b =
- * row b).  Only for shapes lmk_attn_wo_supported accepts (the Wo head block
- * must fit in LDS). */
-int lmk_attn_wo_supported(int D, int hd);
-int lmk_attn_wo(hipStream_t s, const float *q, const void *kc, const void *vc, int kv_f32,
-                const int *pos, int B, int H, int Hkv, int hd, int max_seq, int D,
-                const uint16_t *wo, float *part);
+                    int F, int B, float *x);
 
 /* xn = rmsnorm(x[b]) * w; logits[b, v] = Wcls[v] . xn (logits may be NULL);
  * argmax partials (lowest index on ties) to part[b * nblk + blk], nblk =
@@ -111,8 +99,8 @@ int lmk_attn_prefill(hipStream_t s, const float *q, const void *kc, const void *
 
 /* ---- MFMA GEMMs (k_gemm.hip) ----------------------------------------------
  * C[m, n] = sum_k A[m, k] W[n, k], A fp16 [M, lda], W fp16 [N, K], fp32
- * accumulation; rows M <= 64 take the skinny (decode) kernel (K % 32 == 0),
- * larger M the LDS-tiled (prefill) kernel (K % 64 == 0). */
+ * accumulation, on the LDS-tiled MFMA kernel (K % 64 == 0; the tile shape
+ * follows M). */
 
 #define LMK_EPI_STORE   0   /* out fp32 [M, ldc]                                   */
 #define LMK_EPI_RESID   1   /* out[m, n] += C (fp32 residual stream)               */
@@ -148,7 +136,7 @@ int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int n
                          int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
                          void *vc, int kv_f32, uint16_t *out16);
 /* Arm the calling thread's next decode-chain kernel launch (qkv_rope, attn,
- * attn_wo, wo_residual, ffn13, w2_residual, cls, argmax_final) to be timed
+ * wo_residual, ffn13, w2_residual, cls, argmax_final) to be timed
  * with these two events at its dispatch's start and end. */
 void lmk_time_next(hipEvent_t start, hipEvent_t stop);
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
@@ -165,36 +153,6 @@ int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W,
  * xn[m] = fp16(x[m] / sqrt(mean(x[m]^2) + 1e-5) * gain). */
 int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
                 const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn);
-
-/* ---- persistent batch-1 decode (k_persist.hip) --------------------------- */
-
-typedef struct {
-    const uint16_t *layers;          /* layer blocks, layout of lm_runtime.c          */
-    size_t layer_elems, off_wo, off_w13, off_w2;
-    const uint16_t *embed, *wcls;
-    const float *rms_att, *rms_ffn, *rms_final, *rope_cos, *rope_sin;
-    void *kc, *vc;                   /* slot-0 cache of layer 0; layer l at +l*kv_layer_elems */
-    size_t kv_layer_elems;
-    int kv_f32;
-    void *ll;                        /* lmk_persist_ll_words() 64-bit tagged words     */
-    float *logits;                   /* V floats of the last step, or NULL            */
-    int *out_tok;                    /* n_steps greedy ids                            */
-    int *state_tok, *state_pos;      /* final token / position                        */
-    int *err;                        /* set on a wait time-out                        */
-    int D, F, V, L, H, Hkv, hd, max_seq;
-    int tok0, pos0, n_steps;
-    unsigned tag0;                   /* tag of the first step; steps use tag0 + t     */
-    int grid;                        /* work-groups, <= lmk_persist_grid()            */
-} LMPersistArgs;
-
-/* Work-groups of the persistent decode (one per CU, at most 256); 0 on error. */
-int lmk_persist_grid(void);
-/* Non-zero when the persistent kernel is instantiated for this shape. */
-int lmk_persist_supported(int D, int F, int hd, int H);
-/* 64-bit words of tagged-word buffers the kernel needs. */
-size_t lmk_persist_ll_words(int D, int F, int L, int H, int Hkv, int hd, int grid);
-/* Run p->n_steps greedy decode steps of slot 0 as one cooperative launch. */
-int lmk_decode_persist(hipStream_t s, const LMPersistArgs *p);
 
 /* ---- diagnostics kernels (k_decode.hip) ---------------------------------- */
 

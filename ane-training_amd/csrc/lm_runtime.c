@@ -55,8 +55,6 @@ struct LMModel {
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
     float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
     float *d_part;              /* partials of K-split GEMMs, Wo/W2 products    */
-    float *d_opart;             /* batch 1-4 chain: per-head Wo shares [4][H][D] */
-    int fuse_wo;                /* attention + Wo fused in the batch 1-4 chain  */
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
@@ -69,13 +67,7 @@ struct LMModel {
     /* captured decode graphs: [B][0] one step, [B][1] GRAPH_STEPS steps
      * (greedy feedback stays on the device) */
     hipGraphExec_t (*step_graph)[2];   /* [max_batch + 1][2]   */
-    int use_graph, decode_path;
-    /* persistent batch-1 decode */
-    int pl_ok, pl_grid;         /* kernel instantiated for this shape; work-groups */
-    void *d_ll;                 /* tagged-word buffers                        */
-    size_t ll_words;
-    unsigned pl_tag;            /* next step tag (buffers start at tag 0)      */
-    int *d_ptok, *d_err;        /* per-step ids [max_seq], wait time-out flag  */
+    int use_graph;
 };
 
 static int g_init_status = 1; /* 1 = not attempted */
@@ -357,7 +349,6 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     m->max_seq = max_seq;
     m->cls_nblk = lmk_cls_nblk(m->V);
     m->use_graph = 1;
-    m->decode_path = 0;
 
     const size_t D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, V = m->V, L = m->L;
     m->off_wo = (NQ + 2 * NKV) * D;
@@ -389,21 +380,7 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
     if ((st = dev_alloc((void **)&m->d_tok, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
-    m->fuse_wo = 0;   /* measured slower at B = 1: 12 work-groups stream all of Wo */
-    if ((st = dev_alloc((void **)&m->d_opart, (size_t)MAX_GEMV_B * m->H * D * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
-    m->pl_grid = lmk_persist_grid();
-    m->pl_ok = m->pl_grid > 0 && lmk_persist_supported(m->D, m->F, m->hd, m->H);
-    if (m->pl_ok) {
-        m->ll_words = lmk_persist_ll_words(m->D, m->F, m->L, m->H, m->Hkv, m->hd, m->pl_grid);
-        if ((st = dev_alloc(&m->d_ll, m->ll_words * 8))) goto fail;
-        if ((st = dev_alloc((void **)&m->d_ptok, (size_t)max_seq * 4))) goto fail;
-        if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
-        if (hipMemset(m->d_ll, 0, m->ll_words * 8) != hipSuccess ||
-            hipMemset(m->d_err, 0, 4) != hipSuccess)
-            FAIL(LM_ERR_HIP);
-        m->pl_tag = 1;
-    }
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
 
@@ -490,8 +467,7 @@ void lm_free(LMModel *m)
     free_rows(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_opart, m->d_ll, m->d_ptok,
-                   m->d_err};
+                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_logits) hipHostFree(m->h_logits);
@@ -513,20 +489,8 @@ int lm_set_option(LMModel *m, int option, int value)
 {
     if (!m) return LM_ERR_INVALID;
     switch (option) {
-    case LM_OPT_DECODE_PATH:
-        if (value < 0 || value > 2) return LM_ERR_INVALID;
-        if (value == 2 && !m->pl_ok) return LM_ERR_UNSUPPORTED;
-        m->decode_path = value;
-        return LM_OK;
     case LM_OPT_USE_GRAPH:
         m->use_graph = value ? 1 : 0;
-        return LM_OK;
-    case LM_OPT_FUSE_ATTN_WO:
-        if (value && !lmk_attn_wo_supported(m->D, m->hd)) return LM_ERR_UNSUPPORTED;
-        if ((value ? 1 : 0) == m->fuse_wo) return LM_OK;
-        HIPCHK(hipStreamSynchronize(m->stream));
-        drop_graphs(m);
-        m->fuse_wo = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_KV_F32:
         if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
@@ -569,23 +533,17 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
                           m->max_seq));
         break;
     case LM_KERN_ATTN:
-        if (m->fuse_wo)
-            KCHK(lmk_attn_wo(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, B, m->H, m->Hkv, m->hd,
-                             m->max_seq, D, lw + m->off_wo, m->d_opart));
-        else
-            KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
-                                 m->hd, m->max_seq, m->d_attn, NULL));
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
+                             m->hd, m->max_seq, m->d_attn, NULL));
         break;
-    case LM_KERN_WO:   /* fused: the attention kernel wrote the per-head shares */
-        if (!m->fuse_wo) KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
+    case LM_KERN_WO:
+        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
         break;
     case LM_KERN_W13:
-        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g,
-                       m->fuse_wo ? m->d_opart : NULL, m->H));
+        KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
         break;
     case LM_KERN_W2:
-        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x,
-                             m->fuse_wo ? m->d_opart : NULL, m->H));
+        KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
         break;
     case LM_KERN_CLS:
         KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
@@ -792,57 +750,6 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
 
 static int run_decode_step(LMModel *m, int B) { return run_decode_steps(m, B, 1); }
 
-/* Whether a batch-1 step goes to the persistent kernel (LM_OPT_DECODE_PATH 2).
- * Auto (0) takes the kernel chain: on MI355X its launches cost less than the
- * persistent kernel's in-kernel hand-offs (206 vs 271 us per Stories token). */
-static int use_persistent(const LMModel *m, int B)
-{
-    return B == 1 && m->pl_ok && m->decode_path == 2;
-}
-
-/* n greedy steps of slot 0 from token tok0 at pos0 as one persistent launch;
- * logits of the last step to d_logits when want_logits; ids to out (host, may
- * be NULL); d_tok/d_pos left at the final token/position. */
-static int run_persistent(LMModel *m, int tok0, int pos0, int n, int want_logits, int *out)
-{
-    if (m->pl_tag > 0xFFFFFFF0u - (unsigned)n) {   /* tags would wrap: clear the buffers */
-        HIPCHK(hipMemsetAsync(m->d_ll, 0, m->ll_words * 8, m->stream));
-        m->pl_tag = 1;
-    }
-    LMPersistArgs p;
-    memset(&p, 0, sizeof(p));
-    p.layers = m->d_layers; p.layer_elems = m->layer_elems;
-    p.off_wo = m->off_wo; p.off_w13 = m->off_w13; p.off_w2 = m->off_w2;
-    p.embed = m->d_embed; p.wcls = m->d_wcls;
-    p.rms_att = m->d_rms_att; p.rms_ffn = m->d_rms_ffn; p.rms_final = m->d_rms_final;
-    p.rope_cos = m->d_rope_cos; p.rope_sin = m->d_rope_sin;
-    p.kc = m->d_kc; p.vc = m->d_vc; p.kv_layer_elems = m->kv_layer_elems; p.kv_f32 = m->kv_f32;
-    p.ll = m->d_ll; p.logits = want_logits ? m->d_logits : NULL; p.out_tok = m->d_ptok;
-    p.state_tok = m->d_tok; p.state_pos = m->d_pos; p.err = m->d_err;
-    p.D = m->D; p.F = m->F; p.V = m->V; p.L = m->L; p.H = m->H; p.Hkv = m->Hkv; p.hd = m->hd;
-    p.max_seq = m->max_seq; p.tok0 = tok0; p.pos0 = pos0; p.n_steps = n; p.tag0 = m->pl_tag;
-    p.grid = m->pl_grid;
-    m->pl_tag += (unsigned)n;
-    int e = lmk_decode_persist(m->stream, &p);
-    if (e != 0) {
-        fprintf(stderr, "stories_lm: persistent decode launch failed: %s\n",
-                hipGetErrorString((hipError_t)e));
-        return LM_ERR_HIP;
-    }
-    int *hio = m->h_io;
-    HIPCHK(hipMemcpyAsync(hio, m->d_err, 4, hipMemcpyDeviceToHost, m->stream));
-    if (out) HIPCHK(hipMemcpyAsync(out, m->d_ptok, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
-    HIPCHK(hipStreamSynchronize(m->stream));
-    if (hio[0]) {
-        fprintf(stderr, "stories_lm: persistent decode: a hand-off wait timed out\n");
-        HIPCHK(hipMemset(m->d_err, 0, 4));
-        HIPCHK(hipMemset(m->d_ll, 0, m->ll_words * 8));
-        m->pl_tag = 1;
-        return LM_ERR_HIP;
-    }
-    return LM_OK;
-}
-
 static int check_tok_pos(const LMModel *m, const int *tokens, const int *pos, int B)
 {
     for (int b = 0; b < B; b++) {
@@ -865,19 +772,13 @@ int lm_forward_batch(LMModel *m, const int *tokens, const int *pos, int B, float
     int rc = check_tok_pos(m, tokens, pos, B);
     if (rc) return rc;
     int *hio = m->h_io;
-    if (use_persistent(m, B)) {
-        int id = 0;
-        if ((rc = run_persistent(m, tokens[0], pos[0], 1, 1, &id))) return rc;
-        hio[2 * B] = id;
-    } else {
-        memcpy(hio, tokens, B * 4);
-        memcpy(hio + B, pos, B * 4);
-        HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
-        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
-        if ((rc = run_decode_step(m, B))) return rc;
-        if (argmax)
-            HIPCHK(hipMemcpyAsync(hio + 2 * B, m->d_tok, B * 4, hipMemcpyDeviceToHost, m->stream));
-    }
+    memcpy(hio, tokens, B * 4);
+    memcpy(hio + B, pos, B * 4);
+    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    if ((rc = run_decode_step(m, B))) return rc;
+    if (argmax)
+        HIPCHK(hipMemcpyAsync(hio + 2 * B, m->d_tok, B * 4, hipMemcpyDeviceToHost, m->stream));
     if (logits)
         HIPCHK(hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)B * m->V * 4,
                               hipMemcpyDeviceToHost, m->stream));
@@ -895,16 +796,12 @@ const float *lm_forward(LMModel *m, int token, int pos)
     }
     if (check_tok_pos(m, &token, &pos, 1)) return NULL;
     int *hio = m->h_io;
-    if (use_persistent(m, 1)) {
-        if (run_persistent(m, token, pos, 1, 1, NULL)) return NULL;
-    } else {
-        hio[0] = token;
-        hio[1] = pos;
-        if (hipMemcpyAsync(m->d_tok, hio, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
-            hipMemcpyAsync(m->d_pos, hio + 1, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
-            return NULL;
-        if (run_decode_step(m, 1)) return NULL;
-    }
+    hio[0] = token;
+    hio[1] = pos;
+    if (hipMemcpyAsync(m->d_tok, hio, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
+        hipMemcpyAsync(m->d_pos, hio + 1, 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
+        return NULL;
+    if (run_decode_step(m, 1)) return NULL;
     if (hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
                        m->stream) != hipSuccess ||
         hipStreamSynchronize(m->stream) != hipSuccess) {
@@ -928,7 +825,6 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
             return LM_ERR_RANGE;
         }
     if (n_steps == 0) return LM_OK;
-    if (use_persistent(m, B)) return run_persistent(m, first_tokens[0], pos0[0], n_steps, 0, out_tokens);
     int *hio = m->h_io;
     memcpy(hio, first_tokens, B * 4);
     memcpy(hio + B, pos0, B * 4);
@@ -1137,11 +1033,6 @@ int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int 
     HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
     for (int f = 0; f < LM_KERN_COUNT && rc == LM_OK; f++) {
         const int per_step = (f == LM_KERN_CLS || f == LM_KERN_ARGMAX) ? 1 : m->L;
-        if (f == LM_KERN_WO && m->fuse_wo) {   /* part of the attention kernel */
-            if (launches_per_step) launches_per_step[f] = 0;
-            us_per_launch[f] = 0.f;
-            continue;
-        }
         if (launches_per_step) launches_per_step[f] = per_step;
         hipGraph_t g = NULL;
         hipGraphExec_t ge = NULL;
@@ -1190,7 +1081,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     if (rc) return rc;
     for (int b = 0; b < B; b++)
         if (pos[b] + steps + 1 > m->max_seq) return LM_ERR_RANGE;
-    /* kernels of one step: 5 per layer (Wo none when fused), then cls, argmax */
+    /* kernels of one step: 5 per layer, then cls, argmax */
     const int nk = 5 * m->L + 2;
     hipEvent_t *ev = (hipEvent_t *)calloc(2 * (size_t)nk, sizeof(hipEvent_t));
     int *kfam = (int *)calloc((size_t)nk, sizeof(int));
@@ -1211,7 +1102,6 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
         int k = 0;
         for (int l = 0; l < m->L && rc == LM_OK; l++)
             for (int f = 0; f < 5 && rc == LM_OK; f++) {
-                if (fams[f] == LM_KERN_WO && m->fuse_wo) continue;
                 kfam[k] = fams[f];
                 lmk_time_next(ev[2 * k], ev[2 * k + 1]);
                 rc = enqueue_kernel(m, B, fams[f], l, NULL);
@@ -1234,9 +1124,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
-            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX
-                                       ? 1
-                                       : (f == LM_KERN_WO && m->fuse_wo ? 0 : m->L);
+            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1 : m->L;
     }
     for (int i = 0; ev && i < 2 * nk; i++)
         if (ev[i]) hipEventDestroy(ev[i]);
@@ -1254,7 +1142,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
 int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16_t *W, float *C,
                      LMArgPartHost *part)
 {
-    if (M < 1 || N < 1 || K < 32 || K % 32 || !A || !W || !C) return LM_ERR_INVALID;
+    if (M < 1 || N < 1 || K < 64 || K % 64 || !A || !W || !C) return LM_ERR_INVALID;
     int rc = lm_init();
     if (rc) return rc;
     const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2;
@@ -1293,9 +1181,9 @@ int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16
 int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, const uint16_t *W,
                            float *parts)
 {
-    if (M < 1 || M > 4096 || N < 1 || K < 32 || K % 32 || !A || !W || !parts) return LM_ERR_INVALID;
+    if (M < 1 || M > 4096 || N < 1 || K < 64 || K % 64 || !A || !W || !parts) return LM_ERR_INVALID;
     if (nsplit == 0) nsplit = lmk_pick_split(M, N, K);
-    if (nsplit < 1 || nsplit > LMK_MAX_SPLIT || K % ((M > 64 ? 64 : 16) * nsplit)) return LM_ERR_INVALID;
+    if (nsplit < 1 || nsplit > LMK_MAX_SPLIT || K % (64 * nsplit)) return LM_ERR_INVALID;
     int rc = lm_init();
     if (rc) return rc;
     const size_t asz = (size_t)M * K * 2, wsz = (size_t)N * K * 2;
@@ -1319,7 +1207,7 @@ int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, c
 
 int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t *W, uint16_t *g)
 {
-    if (M < 1 || N < 2 * LMK_GATE_BLOCK || N % (2 * LMK_GATE_BLOCK) || K < 32 || K % 32 || !A || !W || !g)
+    if (M < 1 || N < 2 * LMK_GATE_BLOCK || N % (2 * LMK_GATE_BLOCK) || K < 64 || K % 64 || !A || !W || !g)
         return LM_ERR_INVALID;
     int rc = lm_init();
     if (rc) return rc;
@@ -1347,6 +1235,6 @@ int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t
 
 int lm_gemm_split_count(int M, int N, int K)
 {
-    if (M < 1 || N < 1 || K < 32 || K % 32) return LM_ERR_INVALID;
+    if (M < 1 || N < 1 || K < 64 || K % 64) return LM_ERR_INVALID;
     return lmk_pick_split(M, N, K);
 }

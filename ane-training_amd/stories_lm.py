@@ -31,10 +31,8 @@ LM_ERR_NOT_INIT = -10
 LM_DTYPE_F32 = 0
 LM_DTYPE_F16 = 1
 
-LM_OPT_DECODE_PATH = 1
 LM_OPT_USE_GRAPH = 2
 LM_OPT_KV_F32 = 3
-LM_OPT_FUSE_ATTN_WO = 4
 # kernel families of a decode step (LM_KERN_* in stories_lm.h)
 KERN_NAMES = ("qkv", "attn", "wo", "w13", "w2", "cls", "argmax")
 
@@ -410,9 +408,9 @@ def gemm_split_count(M: int, N: int, K: int) -> int:
 
 
 def selftest_gemm_split(A16: np.ndarray, W16: np.ndarray, nsplit: int = 0) -> np.ndarray:
-    """Partials [n, M, N] of the K-split GEMM (skinny kernel for M <= 64, tiled
-    up to 4096 rows); A16, W16 are uint16 fp16 bits [M, K], [N, K]; nsplit 0 =
-    the runtime's choice."""
+    """Partials [n, M, N] of the K-split GEMM (the tiled kernel, up to 4096
+    rows); A16, W16 are uint16 fp16 bits [M, K], [N, K]; nsplit 0 = the
+    runtime's choice."""
     A16 = np.ascontiguousarray(A16, dtype=np.uint16)
     W16 = np.ascontiguousarray(W16, dtype=np.uint16)
     M, K = A16.shape

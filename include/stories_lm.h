@@ -204,26 +204,13 @@ int lm_timer_begin(LMModel *m);
 /* Record a stop event, wait for it, return elapsed ms since lm_timer_begin. */
 int lm_timer_end(LMModel *m, float *ms);
 
-/* Execution knobs.  LM_OPT_DECODE_PATH selects the B=1 decode step: 0 = auto
- * (currently the chain), 1 = chain of per-op kernels replayed as captured
- * graphs, 2 = persistent kernel: one cooperative launch runs all requested
- * steps, work-groups hand activations over through tagged words in memory
- * (LM_ERR_UNSUPPORTED when it is not built for the model's shape).
- * LM_OPT_USE_GRAPH: 1 (default) replays captured hipGraphs, 0 launches
- * kernels directly (debugging / per-kernel timing). */
-#define LM_OPT_DECODE_PATH 1
+/* Execution knobs.  LM_OPT_USE_GRAPH: 1 (default) replays captured hipGraphs,
+ * 0 launches kernels directly (debugging / per-kernel timing). */
 #define LM_OPT_USE_GRAPH   2
 /* LM_OPT_KV_F32: 1 stores the K/V cache in fp32 (the reference forward keeps
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
-/* LM_OPT_FUSE_ATTN_WO: 1 runs the batch 1-4 chain's attention and Wo as one
- * kernel per layer, each head adding its share of the Wo product to the
- * residual (where the shape allows it: D = H*hd with a Wo head block of D x hd
- * fp16 that fits in LDS, e.g. Stories; otherwise LM_ERR_UNSUPPORTED).  0 (the
- * default) keeps two kernels, which is faster on MI355X: the fused kernel has
- * one work-group per head to stream all of Wo. */
-#define LM_OPT_FUSE_ATTN_WO 4
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------
@@ -273,16 +260,15 @@ int lm_selftest_reduce(const float *in64, float *out4);
 typedef struct { float val; int idx; } LMArgPartHost;
 
 /* Run one MFMA GEMM C = A W^T (fp32 accumulation) on caller data through the
- * same kernels the prefill and batched decode use (M <= 64: decode kernel,
- * else the LDS-tiled kernel): A [M, K] fp16 bits (a_f32 = 0) or fp32 (a_f32 =
- * 1, rounded to fp16 on load), W [N, K] fp16 bits, C [M, N] fp32, part (may be
- * NULL) [M, ceil(N/32)] per-32-column argmax partials.  K % 32 == 0. */
+ * LDS-tiled kernel the prefill and batched decode use (the tile the runtime
+ * picks for M rows): A [M, K] fp16 bits (a_f32 = 0) or fp32 (a_f32 = 1,
+ * rounded to fp16 on load), W [N, K] fp16 bits, C [M, N] fp32, part (may be
+ * NULL) [M, ceil(N/32)] per-32-column argmax partials.  K % 64 == 0. */
 int lm_selftest_gemm(int M, int N, int K, int a_f32, const void *A, const uint16_t *W,
                      float *C, LMArgPartHost *part);
 
-/* Run the K-split GEMM the forward uses for narrow projections (the skinny
- * kernel for M <= 64 rows, the tiled kernel up to 4096 rows, where K must be a
- * multiple of 64*nsplit): parts[s] [M, N] fp32 = A[:, s*K/n .. (s+1)*K/n)
+/* Run the K-split GEMM the forward uses for narrow projections (the tiled
+ * kernel, up to 4096 rows; K a multiple of 64*nsplit): parts[s] [M, N] fp32 = A[:, s*K/n .. (s+1)*K/n)
  * W[:, same]^T for s < n, n = nsplit, or the runtime's own choice when
  * nsplit == 0.  A [M, K] and W [N, K] fp16 bits; parts holds n*M*N floats (size
  * it with lm_gemm_split_count).  Returns n (> 0) or a negative status. */
@@ -294,7 +280,7 @@ int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, c
  * blocks of 16 (block j: W1 rows 16j .. 16j+15, then W3 rows 16j .. 16j+15),
  * h = A W^T in fp32, and g[m, 16j + c] = fp16(silu(h[m, 32j + c]) *
  * h[m, 32j + 16 + c]) for c < 16.  A [M, K] fp16 bits, g [M, N/2] fp16 bits;
- * N a multiple of 32, K of 32. */
+ * N a multiple of 32, K of 64. */
 int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t *W, uint16_t *g);
 
 /* The split count the runtime uses for an [M, K] x [N, K]^T GEMM (1: unsplit). */
@@ -302,8 +288,7 @@ int lm_gemm_split_count(int M, int N, int K);
 
 /* Kernel families of a decode step (index into lm_profile_decode's output). */
 #define LM_KERN_QKV    0   /* rmsnorm + QKV GEMV + RoPE + KV append          */
-#define LM_KERN_ATTN   1   /* causal attention over the KV cache (+ per-head
-                              Wo shares when LM_OPT_FUSE_ATTN_WO is on)      */
+#define LM_KERN_ATTN   1   /* causal attention over the KV cache              */
 #define LM_KERN_WO     2   /* Wo GEMV + residual (no launches when fused)   */
 #define LM_KERN_W13    3   /* rmsnorm + W1/W3 GEMV + SiLU gate              */
 #define LM_KERN_W2     4   /* W2 GEMV + residual                            */

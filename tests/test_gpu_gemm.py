@@ -7,10 +7,10 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (30, 96, 256), (32, 768, 768), (64, 2304, 768),
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (30, 96, 256), (32, 768, 768), (64, 2304, 768),
                                    (50, 200, 2048), (64, 768, 5632), (128, 128, 64), (256, 768, 768),
                                    (200, 2304, 768), (130, 32000, 768), (512, 4096, 2048),
-                                   (64, 32000, 768), (5, 20000, 256), (17, 300, 96)])
+                                   (64, 32000, 768), (5, 20000, 256), (17, 300, 128)])
 @pytest.mark.parametrize("a_f32", [False, True])
 def test_gemm_matches_numpy(lm, M, N, K, a_f32):
     rng = np.random.default_rng(M * 7 + N + K)
@@ -31,7 +31,7 @@ def test_gemm_matches_numpy(lm, M, N, K, a_f32):
 
 @pytest.mark.parametrize("M,N,K", [(64, 768, 768), (64, 768, 2048), (64, 2304, 768), (7, 768, 768),
                                    (32, 2048, 5632), (33, 200, 512), (200, 768, 768), (130, 200, 512),
-                                   (1000, 768, 2048), (20, 200, 96), (2048, 768, 2048), (1100, 700, 2048)])
+                                   (1000, 768, 2048), (20, 200, 128), (2048, 768, 2048), (1100, 700, 2048)])
 @pytest.mark.parametrize("nsplit", [0, 2])
 def test_gemm_split_partials(lm, M, N, K, nsplit):
     """Each K-split partial is the product over its own K-chunk."""
