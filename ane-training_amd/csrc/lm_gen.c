@@ -11,6 +11,14 @@
  * step; here the K/V cache carries it, so a step is one lm_forward, except
  * after a window shift (every position moves), where the window is prefilled
  * again.  Both give the logits of the same causal forward.
+ *
+ * Arithmetic: the first window (BOS + prompt) goes through lm_forward one
+ * position at a time, the fp32 decode chain whose logits follow the
+ * reference's fp32 forward to summation order, so the ids match the
+ * reference's until the first window shift.  A shift re-prefills the
+ * seq_len - 1 positions of the window through the fp16 MFMA prefill (logits within atol 2e-2
+ * + rtol 1e-2 of the reference): from there on an id can differ from the
+ * reference's only where two logits are that close.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "ane_gen.h"
@@ -185,10 +193,19 @@ static int text_add(Text *t, const char *piece)
     return 0;
 }
 
-/* Logits of the last of the ctx_len context tokens, by prefilling the window
- * into slot 0 (positions 0 .. ctx_len-1). */
-static int window_logits(ANEGenSession *g, int ctx_len)
+/* Logits of the last of the ctx_len context tokens with the window cached in
+ * slot 0 (positions 0 .. ctx_len-1): step by step through the fp32 decode
+ * chain (exact), or as one MFMA prefill of the window. */
+static int window_logits(ANEGenSession *g, int ctx_len, int exact)
 {
+    const int V = g->cfg.vocab_size < 0 ? -g->cfg.vocab_size : g->cfg.vocab_size;
+    if (exact) {
+        const float *lg = NULL;
+        for (int p = 0; p < ctx_len; p++)
+            if (!(lg = lm_forward(g->m, g->context[p], p))) return LM_ERR_HIP;
+        memcpy(g->logits, lg, (size_t)V * sizeof(float));
+        return LM_OK;
+    }
     const int slot = 0;
     return lm_prefill_batch(g->m, 1, &slot, g->context, ctx_len, LM_LOGITS_LAST, g->logits);
 }
@@ -234,9 +251,10 @@ ANEGenResult ane_gen_run(ANEGenSession *g, const char *prompt, const ANEGenConfi
     const double t0 = now_ms();
     int generated = 0;
     int stale = 1;   /* the cache does not hold the current window */
+    int shifted = 0; /* a window shift has happened */
     for (int gen = 0; gen < max_tokens; gen++) {
         if (stale) {
-            if (window_logits(g, ctx_len) != LM_OK) {
+            if (window_logits(g, ctx_len, !shifted) != LM_OK) {
                 result.stop_reason = ANE_GEN_STOP_ERROR;
                 break;
             }
@@ -258,6 +276,7 @@ ANEGenResult ane_gen_run(ANEGenSession *g, const char *prompt, const ANEGenConfi
             memmove(g->context + 1, g->context + 2, (size_t)(SEQ - 2) * sizeof(int));
             ctx_len = SEQ - 1;
             stale = 1;
+            shifted = 1;
         }
         g->context[ctx_len++] = next;
         generated++;

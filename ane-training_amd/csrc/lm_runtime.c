@@ -169,25 +169,60 @@ static void to_f32(const void *src, LMDType dt, size_t off, size_t n, float *dst
         lm_f16_to_f32((const uint16_t *)src + off, dst, n);
 }
 
-static int upload_weights(LMModel *m, const LMWeights *w)
+/* Where the host weights come from: one contiguous block per tensor
+ * (LMWeights) or per-layer pointer arrays (LMLayerWeights). */
+typedef struct {
+    LMDType dtype;
+    const void *embed, *rms_final, *wcls;   /* wcls NULL: tied */
+    const LMWeights *flat;
+    const LMLayerWeights *per;
+} WSrc;
+
+static const void *const *per_layer_array(const LMLayerWeights *w, int t)
+{
+    switch (t) {
+    case LMH_T_RMS_ATT: return w->rms_att_w;
+    case LMH_T_WQ: return w->wq;
+    case LMH_T_WK: return w->wk;
+    case LMH_T_WV: return w->wv;
+    case LMH_T_WO: return w->wo;
+    case LMH_T_RMS_FFN: return w->rms_ffn_w;
+    case LMH_T_W1: return w->w1;
+    case LMH_T_W2: return w->w2;
+    case LMH_T_W3: return w->w3;
+    default: return NULL;
+    }
+}
+
+/* Layer l's tensor t (n elements per layer) in the source's element type. */
+static const void *src_layer(const WSrc *ws, int t, size_t l, size_t n)
+{
+    if (ws->per) return per_layer_array(ws->per, t)[l];
+    const char *base = (const char *)lmh_weights_ptr(ws->flat, t);
+    return base + l * n * (ws->dtype == LM_DTYPE_F16 ? 2 : 4);
+}
+
+static int upload_weights(LMModel *m, const WSrc *w)
 {
     const size_t D = m->D, F = m->F, NQ = m->NQ, NKV = m->NKV, V = m->V, L = m->L;
     const size_t GB = LMK_GATE_BLOCK;
+    const LMDType dt = w->dtype;
     uint16_t *stage = (uint16_t *)malloc(m->layer_elems * 2);
     float *nf = (float *)malloc(L * D * 4);
     if (!stage || !nf) { free(stage); free(nf); return LM_ERR_OOM; }
     int rc = LM_OK;
     for (size_t l = 0; l < L && rc == LM_OK; l++) {
         uint16_t *p = stage;
-        to_f16(w->wq, w->dtype, l * NQ * D, NQ * D, p);              p += NQ * D;
-        to_f16(w->wk, w->dtype, l * NKV * D, NKV * D, p);            p += NKV * D;
-        to_f16(w->wv, w->dtype, l * NKV * D, NKV * D, p);            p += NKV * D;
-        to_f16(w->wo, w->dtype, l * D * NQ, D * NQ, p);              p += D * NQ;
+        to_f16(src_layer(w, LMH_T_WQ, l, NQ * D), dt, 0, NQ * D, p);    p += NQ * D;
+        to_f16(src_layer(w, LMH_T_WK, l, NKV * D), dt, 0, NKV * D, p);  p += NKV * D;
+        to_f16(src_layer(w, LMH_T_WV, l, NKV * D), dt, 0, NKV * D, p);  p += NKV * D;
+        to_f16(src_layer(w, LMH_T_WO, l, D * NQ), dt, 0, D * NQ, p);    p += D * NQ;
+        const void *w1 = src_layer(w, LMH_T_W1, l, F * D), *w3 = src_layer(w, LMH_T_W3, l, F * D);
         for (size_t j = 0; j < F / GB; j++) {
-            to_f16(w->w1, w->dtype, l * F * D + j * GB * D, GB * D, p); p += GB * D;
-            to_f16(w->w3, w->dtype, l * F * D + j * GB * D, GB * D, p); p += GB * D;
+            to_f16(w1, dt, j * GB * D, GB * D, p); p += GB * D;
+            to_f16(w3, dt, j * GB * D, GB * D, p); p += GB * D;
         }
-        to_f16(w->w2, w->dtype, l * D * F, D * F, p);
+        to_f16(src_layer(w, LMH_T_W2, l, D * F), dt, 0, D * F, p);
         if (hipMemcpy(m->d_layers + l * m->layer_elems, stage, m->layer_elems * 2,
                       hipMemcpyHostToDevice) != hipSuccess)
             rc = LM_ERR_HIP;
@@ -197,11 +232,11 @@ static int upload_weights(LMModel *m, const LMWeights *w)
         uint16_t *e16 = (uint16_t *)malloc(V * D * 2);
         if (!e16) rc = LM_ERR_OOM;
         if (rc == LM_OK) {
-            to_f16(w->token_embedding, w->dtype, 0, V * D, e16);
+            to_f16(w->embed, dt, 0, V * D, e16);
             if (hipMemcpy(m->d_embed, e16, V * D * 2, hipMemcpyHostToDevice) != hipSuccess)
                 rc = LM_ERR_HIP;
             if (rc == LM_OK && m->untied) {
-                to_f16(w->wcls, w->dtype, 0, V * D, e16);
+                to_f16(w->wcls, dt, 0, V * D, e16);
                 if (hipMemcpy(m->d_wcls, e16, V * D * 2, hipMemcpyHostToDevice) != hipSuccess)
                     rc = LM_ERR_HIP;
             }
@@ -209,12 +244,12 @@ static int upload_weights(LMModel *m, const LMWeights *w)
         free(e16);
     }
     if (rc == LM_OK) {
-        to_f32(w->rms_att_w, w->dtype, 0, L * D, nf);
+        for (size_t l = 0; l < L; l++) to_f32(src_layer(w, LMH_T_RMS_ATT, l, D), dt, 0, D, nf + l * D);
         if (hipMemcpy(m->d_rms_att, nf, L * D * 4, hipMemcpyHostToDevice) != hipSuccess) rc = LM_ERR_HIP;
-        to_f32(w->rms_ffn_w, w->dtype, 0, L * D, nf);
+        for (size_t l = 0; l < L; l++) to_f32(src_layer(w, LMH_T_RMS_FFN, l, D), dt, 0, D, nf + l * D);
         if (rc == LM_OK && hipMemcpy(m->d_rms_ffn, nf, L * D * 4, hipMemcpyHostToDevice) != hipSuccess)
             rc = LM_ERR_HIP;
-        to_f32(w->rms_final_w, w->dtype, 0, D, nf);
+        to_f32(w->rms_final, dt, 0, D, nf);
         if (rc == LM_OK && hipMemcpy(m->d_rms_final, nf, D * 4, hipMemcpyHostToDevice) != hipSuccess)
             rc = LM_ERR_HIP;
     }
@@ -306,7 +341,62 @@ static int supported_k(int k)
     return k == 256 || k == 512 || k == 768 || k == 1024 || k == 2048 || k == 5632;
 }
 
+static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, int max_seq,
+                             int *status);
+
 LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max_seq, int *status)
+{
+    int st = LM_OK;
+    if (!cfg || !w || max_batch < 1 || max_seq < 1 ||
+        (w->dtype != LM_DTYPE_F32 && w->dtype != LM_DTYPE_F16))
+        st = LM_ERR_INVALID;
+    for (int t = 0; t < LMH_NTENSORS - 1 && st == LM_OK; t++)
+        if (!lmh_weights_ptr(w, t)) {
+            fprintf(stderr, "stories_lm: weight tensor %d is NULL\n", t);
+            st = LM_ERR_INVALID;
+        }
+    if (st != LM_OK) {
+        if (status) *status = st;
+        fprintf(stderr, "stories_lm: lm_create failed: %s\n", lm_strerror(st));
+        return NULL;
+    }
+    const WSrc ws = {w->dtype, w->token_embedding, w->rms_final_w,
+                     lmh_weights_untied(w) ? w->wcls : NULL, w, NULL};
+    return create_model(cfg, &ws, max_batch, max_seq, status);
+}
+
+LMModel *lm_create_layers(const Config *cfg, const LMLayerWeights *w, int max_batch, int max_seq,
+                          int *status)
+{
+    int st = LM_OK;
+    if (!cfg || !w || max_batch < 1 || max_seq < 1 || cfg->n_layers < 1 ||
+        (w->dtype != LM_DTYPE_F32 && w->dtype != LM_DTYPE_F16) || !w->token_embedding ||
+        !w->rms_final_w)
+        st = LM_ERR_INVALID;
+    for (int t = LMH_T_RMS_ATT; t <= LMH_T_W3 && st == LM_OK; t++) {
+        const void *const *a = per_layer_array(w, t);
+        if (!a) {
+            fprintf(stderr, "stories_lm: per-layer weight array %d is NULL\n", t);
+            st = LM_ERR_INVALID;
+        }
+        for (int l = 0; a && l < cfg->n_layers && st == LM_OK; l++)
+            if (!a[l]) {
+                fprintf(stderr, "stories_lm: weight tensor %d of layer %d is NULL\n", t, l);
+                st = LM_ERR_INVALID;
+            }
+    }
+    if (st != LM_OK) {
+        if (status) *status = st;
+        fprintf(stderr, "stories_lm: lm_create_layers failed: %s\n", lm_strerror(st));
+        return NULL;
+    }
+    const WSrc ws = {w->dtype, w->token_embedding, w->rms_final_w,
+                     w->wcls && w->wcls != w->token_embedding ? w->wcls : NULL, NULL, w};
+    return create_model(cfg, &ws, max_batch, max_seq, status);
+}
+
+static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, int max_seq,
+                             int *status)
 {
     int st = LM_OK;
     LMModel *m = NULL;
@@ -315,24 +405,17 @@ LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch, int max
         st = (code);    \
         goto fail;      \
     } while (0)
-    if (!cfg || !w || max_batch < 1 || max_seq < 1) FAIL(LM_ERR_INVALID);
     if ((st = lm_init()) != LM_OK) goto fail;
     if ((st = lmh_check_config(cfg)) != LM_OK) {
         fprintf(stderr, "stories_lm: inconsistent Config\n");
         goto fail;
     }
-    if (w->dtype != LM_DTYPE_F32 && w->dtype != LM_DTYPE_F16) FAIL(LM_ERR_INVALID);
-    for (int t = 0; t < LMH_NTENSORS - 1; t++)
-        if (!lmh_weights_ptr(w, t)) {
-            fprintf(stderr, "stories_lm: weight tensor %d is NULL\n", t);
-            FAIL(LM_ERR_INVALID);
-        }
     m = (LMModel *)calloc(1, sizeof(LMModel));
     if (!m) FAIL(LM_ERR_OOM);
     m->cfg = *cfg;
     m->V = cfg->vocab_size < 0 ? -cfg->vocab_size : cfg->vocab_size;
     m->cfg.vocab_size = m->V;
-    m->untied = lmh_weights_untied(w);
+    m->untied = w->wcls != NULL;
     m->D = cfg->dim; m->F = cfg->hidden_dim; m->L = cfg->n_layers;
     m->H = cfg->n_heads; m->Hkv = cfg->n_kv_heads;
     m->hd = m->D / m->H;
@@ -874,20 +957,32 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
                        int S, int logits_mode, float *logits)
 {
     const int V = m->V;
+    unsigned char *seen = (unsigned char *)calloc((size_t)m->max_batch, 1);
+    if (!seen) return LM_ERR_OOM;
     for (int i = 0; i < nseq; i++) {
         if (slots[i] < 0 || slots[i] >= m->max_batch || pos0[i] < 0 || pos0[i] + S > m->max_seq) {
             fprintf(stderr, "stories_lm: prefill sequence %d: slot %d / positions %d..%d out of "
                     "range (max_batch %d, max_seq %d)\n", i, slots[i], pos0[i], pos0[i] + S - 1,
                     m->max_batch, m->max_seq);
+            free(seen);
             return LM_ERR_RANGE;
+        }
+        /* two sequences in one slot would write the same cache rows */
+        if (seen[slots[i]]++) {
+            fprintf(stderr, "stories_lm: prefill: slot %d given to more than one sequence\n",
+                    slots[i]);
+            free(seen);
+            return LM_ERR_INVALID;
         }
         for (int t = 0; t < S; t++)
             if (tokens[(size_t)i * S + t] < 0 || tokens[(size_t)i * S + t] >= V) {
                 fprintf(stderr, "stories_lm: prefill token %d out of range [0,%d)\n",
                         tokens[(size_t)i * S + t], V);
+                free(seen);
                 return LM_ERR_RANGE;
             }
     }
+    free(seen);
     const int cs = S >= PREFILL_ROWS ? 1 : PREFILL_ROWS / S;   /* sequences per chunk */
     const int chunk_rows = (nseq < cs ? nseq : cs) * S;
     int rc;

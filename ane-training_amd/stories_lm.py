@@ -54,6 +54,17 @@ class LMWeights(C.Structure):
         "w1", "w2", "w3", "rms_final_w", "wcls")]
 
 
+LAYER_TENSORS = ("rms_att_w", "wq", "wk", "wv", "wo", "rms_ffn_w", "w1", "w2", "w3")
+
+
+class LMLayerWeights(C.Structure):
+    """Per-layer pointer arrays, the layout of the reference's Model
+    (training/model.h:27-39)."""
+    _fields_ = ([("dtype", C.c_int), ("token_embedding", C.c_void_p)] +
+                [(n, C.POINTER(C.c_void_p)) for n in LAYER_TENSORS] +
+                [("rms_final_w", C.c_void_p), ("wcls", C.c_void_p)])
+
+
 class LMDeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32), ("compute_units", C.c_int),
                 ("clock_khz", C.c_int), ("l2_bytes", C.c_int), ("total_mem", C.c_size_t)]
@@ -214,6 +225,7 @@ def lib():
         "lm_init": (I, []),
         "lm_device_info": (I, [C.POINTER(LMDeviceInfo)]),
         "lm_create": (P, [C.POINTER(Config), C.POINTER(LMWeights), I, I, ip]),
+        "lm_create_layers": (P, [C.POINTER(Config), C.POINTER(LMLayerWeights), I, I, ip]),
         "lm_load_llama2c": (P, [C.c_char_p, I, I, ip]),
         "lm_free": (None, [P]),
         "lm_get_config": (I, [P, C.POINTER(Config)]),
@@ -325,6 +337,39 @@ def weights_view(cfg: Config, buf: np.ndarray, untied: bool) -> LMWeights:
     if rc:
         raise LMError(rc, "lm_weights_view")
     return w
+
+
+def split_layers(cfg: Config, buf: np.ndarray, untied: bool) -> dict:
+    """The tensors of a contiguous llama2.c-ordered buffer as separate arrays,
+    per-layer tensors as lists of per-layer copies (each its own allocation, as
+    the reference's model_load_weights mallocs them, training/model.h:129-147)."""
+    v = weights_view(cfg, buf, untied)
+    base = buf.ctypes.data
+    sizes = np.array(_tensor_sizes(cfg, untied), dtype=np.int64)
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    names = ("token_embedding",) + LAYER_TENSORS + ("rms_final_w", "wcls")
+    out = {}
+    L = cfg.n_layers
+    for i, n in enumerate(names):
+        ptr = getattr(v, n)
+        if n == "wcls" and not untied:
+            out[n] = None
+            continue
+        off = (ptr - base) // buf.itemsize
+        assert off == offs[i]
+        t = buf[off:off + sizes[i]]
+        out[n] = [t[j * (t.size // L):(j + 1) * (t.size // L)].copy() for j in range(L)] \
+            if n in LAYER_TENSORS else t.copy()
+    return out
+
+
+def _tensor_sizes(cfg: Config, untied: bool):
+    D, F, L = cfg.dim, cfg.hidden_dim, cfg.n_layers
+    V = abs(cfg.vocab_size)
+    hd = D // cfg.n_heads
+    NQ, NKV = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    return [V * D, L * D, L * NQ * D, L * NKV * D, L * NKV * D, L * D * NQ, L * D, L * F * D,
+            L * D * F, L * F * D, D] + ([V * D] if untied else [0])
 
 
 def f32_to_f16(a: np.ndarray) -> np.ndarray:
@@ -467,6 +512,32 @@ class Model:
         return cls(h, cfg)
 
     @classmethod
+    def create_layers(cls, cfg: Config, tensors: dict, max_batch: int, max_seq: int):
+        """lm_create_layers over per-layer arrays (split_layers' layout): every
+        per-layer tensor is a list of n_layers arrays, all uint16 (fp16 bits)
+        or all float32."""
+        dt = tensors["token_embedding"].dtype
+        code = {np.dtype(np.uint16): LM_DTYPE_F16, np.dtype(np.float32): LM_DTYPE_F32}[dt]
+        keep = []
+        w = LMLayerWeights()
+        w.dtype = code
+        w.token_embedding = tensors["token_embedding"].ctypes.data
+        for n in LAYER_TENSORS:
+            arrs = tensors[n]
+            assert len(arrs) == cfg.n_layers and all(a.dtype == dt and a.flags.c_contiguous for a in arrs)
+            ptrs = (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+            keep.append(ptrs)
+            setattr(w, n, C.cast(ptrs, C.POINTER(C.c_void_p)))
+        w.rms_final_w = tensors["rms_final_w"].ctypes.data
+        w.wcls = tensors["wcls"].ctypes.data if tensors.get("wcls") is not None else None
+        st = C.c_int(0)
+        h = lib().lm_create_layers(C.byref(cfg), C.byref(w), max_batch, max_seq, C.byref(st))
+        del keep
+        if not h:
+            raise LMError(st.value, "lm_create_layers")
+        return cls(h, cfg)
+
+    @classmethod
     def load_llama2c(cls, path: str, max_batch: int, max_seq: int):
         st = C.c_int(0)
         h = lib().lm_load_llama2c(path.encode(), max_batch, max_seq, C.byref(st))
@@ -526,7 +597,9 @@ class Model:
     def prefill_batch(self, tokens, slots=None, mode=LM_LOGITS_ALL, want_logits=True):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         nseq, S = tokens.shape
-        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.int32)
+        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.int32).ravel()
+        if sl is not None and sl.size != nseq:
+            raise ValueError(f"prefill_batch: {sl.size} slots for {nseq} sequences")
         rows = nseq * S if mode == LM_LOGITS_ALL else nseq
         logits = np.empty((rows, self.vocab), dtype=np.float32) if want_logits else None
         rc = lib().lm_prefill_batch(self._h, nseq, _ip(sl) if sl is not None else None, _ip(tokens),

@@ -12,11 +12,17 @@
  * Reference interfaces replaced (paths relative to the reference repository):
  *   Config                  training/model.h:19-21 (= Llama2Config,
  *                           training/stories_config.h:107-110)
- *   LMWeights               weight members of Model, training/model.h:27-39
+ *   LMWeights               weight members of Model, training/model.h:27-39,
+ *                           one contiguous block per tensor (llama2.c file order)
+ *   LMLayerWeights          the same members as per-layer pointer arrays, as
+ *                           Model holds them (float *wq[N_LAYERS], model.h:27-39;
+ *                           LayerWeights, training_dynamic/config.h:39-43)
  *   lm_init                 ane_init, libane/ane.h:97-100
  *   lm_create               model_load_weights + model_compile_kernels,
  *                           training/model.h:78-205; compile_fwd_kernels +
  *                           weight staging, training/training_dynamic/generate.m:251-277,386-392
+ *   lm_create_layers        model_compile_kernels(Model *) over an already
+ *                           loaded Model, training/model.h:169-205
  *   lm_load_llama2c         model_load_weights, training/model.h:78-164
  *   lm_forward              the per-token body of generate.m:437-487 (KV-cache
  *                           form of training/dashboard.py:205-267)
@@ -68,6 +74,24 @@ typedef struct {
     const void *wcls;
 } LMWeights;
 
+/* The same weights as per-layer pointers, the way the reference's Model holds
+ * them (training/model.h:27-39: float *wq[N_LAYERS] ..., each layer's tensor
+ * malloc'd on its own by model_load_weights, model.h:129-147): every per-layer
+ * member points at an array of n_layers pointers, entry l at layer l's tensor
+ * (rms_att_w[l] [dim], wq[l] [n_heads*hd, dim], wk[l] and wv[l]
+ * [n_kv_heads*hd, dim], wo[l] [dim, n_heads*hd], rms_ffn_w[l] [dim], w1[l] and
+ * w3[l] [hidden, dim], w2[l] [dim, hidden]), all of one element type. */
+typedef struct {
+    LMDType dtype;
+    const void *token_embedding;              /* [vocab, dim]            */
+    const void *const *rms_att_w;             /* [n_layers] -> [dim]     */
+    const void *const *wq, *const *wk, *const *wv, *const *wo;
+    const void *const *rms_ffn_w;
+    const void *const *w1, *const *w2, *const *w3;
+    const void *rms_final_w;                  /* [dim]                   */
+    const void *wcls;                         /* [vocab, dim]; NULL = tied */
+} LMLayerWeights;
+
 typedef struct LMModel LMModel;
 
 /* Status codes.  0 / -1 / -2 keep ane_init's meaning (libane/ane.h:99). */
@@ -117,6 +141,13 @@ int lm_device_info(LMDeviceInfo *out);
  * Returns NULL and sets *status (if non-NULL) on failure. */
 LMModel *lm_create(const Config *cfg, const LMWeights *w, int max_batch,
                    int max_seq, int *status);
+
+/* lm_create from per-layer weight pointers (LMLayerWeights): a caller holding
+ * a loaded Model passes its pointer arrays as they are, with no repacking.
+ * The result is identical to lm_create on the same values.  A NULL array or a
+ * NULL entry fails with LM_ERR_INVALID (checked before any device call). */
+LMModel *lm_create_layers(const Config *cfg, const LMLayerWeights *w, int max_batch,
+                          int max_seq, int *status);
 
 /* Read a llama2.c model file (fp32 values, header as Config, file order of
  * training/model.h:78-164, negative vocab_size = untied) and lm_create it.

@@ -29,7 +29,6 @@ struct OracleModel {
     float *w1T, *w2T, *w3T;
     float *wclsT;                 /* [D][V]                           */
     float *kc, *vc;               /* [L][max_seq][NKV]                */
-    float *buf;                   /* scratch                          */
 };
 
 /* ---------------------------------------------------------------- helpers */
@@ -215,10 +214,8 @@ OracleModel *oracle_create(const int *c, const float *w, int untied, int max_seq
     o->wclsT = (float *)malloc(v * d * 4);
     o->kc = (float *)calloc(l * (size_t)max_seq * nkv, 4);
     o->vc = (float *)calloc(l * (size_t)max_seq * nkv, 4);
-    o->buf = (float *)malloc(((size_t)max_seq > f ? (size_t)max_seq : f) * 4 * 4 + v * 4);
     if (!o->embed || !o->rms_att || !o->rms_ffn || !o->rms_final || !o->wqT || !o->wkT ||
-        !o->wvT || !o->woT || !o->w1T || !o->w2T || !o->w3T || !o->wclsT || !o->kc || !o->vc ||
-        !o->buf) {
+        !o->wvT || !o->woT || !o->w1T || !o->w2T || !o->w3T || !o->wclsT || !o->kc || !o->vc) {
         oracle_free(o);
         return NULL;
     }
@@ -253,7 +250,7 @@ void oracle_free(OracleModel *o)
     free(o->embed); free(o->rms_att); free(o->rms_ffn); free(o->rms_final);
     free(o->wqT); free(o->wkT); free(o->wvT); free(o->woT);
     free(o->w1T); free(o->w2T); free(o->w3T); free(o->wclsT);
-    free(o->kc); free(o->vc); free(o->buf);
+    free(o->kc); free(o->vc);
     free(o);
 }
 
@@ -264,7 +261,9 @@ static void round_kv(float *a, size_t n)
 
 /* The layer stack and classifier over S rows at positions pos0..pos0+S-1.
  * mode_full: attention over the S rows themselves (forward.h:127-128);
- * otherwise S == 1 and attention reads the cache (dashboard.py:236-251).
+ * otherwise the rows' K/V are appended to the cache at pos0.. and row t
+ * attends to cached positions 0..pos0+t (dashboard.py:236-251, one row at a
+ * time there; the same values and summation order for several rows).
  * last_only: the classifier of the last row only (generate.m:474-487). */
 static int forward_rows(OracleModel *o, const int *tokens, int S, int pos0, int mode_full,
                         int last_only, float *logits)
@@ -294,12 +293,20 @@ static int forward_rows(OracleModel *o, const int *tokens, int S, int pos0, int 
             oracle_attention(att, q, k, v, S, o->H, o->Hkv, hd);   /* :128 */
         } else {
             float *kc = o->kc + L * o->max_seq * NKV, *vc = o->vc + L * o->max_seq * NKV;
-            memcpy(kc + (size_t)pos0 * NKV, k, (size_t)NKV * 4);   /* dashboard.py:236-240 */
-            memcpy(vc + (size_t)pos0 * NKV, v, (size_t)NKV * 4);
-            const int grp = o->H / o->Hkv;
-            for (int h = 0; h < o->H; h++)                         /* dashboard.py:243-251 */
-                attend_row(att + h * hd, q + h * hd, kc + (h / grp) * hd, vc + (h / grp) * hd,
-                           NKV, pos0 + 1, hd, o->buf);
+            memcpy(kc + (size_t)pos0 * NKV, k, s * NKV * 4);       /* dashboard.py:236-240 */
+            memcpy(vc + (size_t)pos0 * NKV, v, s * NKV * 4);
+            const int grp = o->H / o->Hkv, H = o->H;
+            #pragma omp parallel
+            {
+                float *scores = (float *)malloc((size_t)(pos0 + S) * sizeof(float));
+                #pragma omp for collapse(2) schedule(dynamic, 4)
+                for (int h = 0; h < H; h++)                        /* dashboard.py:243-251 */
+                    for (int t = 0; t < S; t++)
+                        attend_row(att + (size_t)t * NQ + h * hd, q + (size_t)t * NQ + h * hd,
+                                   kc + (h / grp) * hd, vc + (h / grp) * hd, NKV, pos0 + t + 1,
+                                   hd, scores);
+                free(scores);
+            }
         }
         matmul_T(o->woT + L * D * NQ, att, o_out, S, NQ, D);      /* :134 */
         for (size_t i = 0; i < s * D; i++) x[i] += o_out[i];       /* :136 */
@@ -341,6 +348,16 @@ int oracle_decode_step(OracleModel *o, int token, int pos, float *logits)
     if (!o || !logits) return -3;
     if (token < 0 || token >= o->V || pos < 0 || pos >= o->max_seq) return -8;
     return forward_rows(o, &token, 1, pos, 0, 0, logits);
+}
+
+int oracle_forward_cached(OracleModel *o, const int *tokens, int S, int pos0, int last_only,
+                          float *logits)
+{
+    if (!o || !tokens || !logits || S < 1) return -3;
+    if (pos0 < 0 || pos0 + S > o->max_seq) return -8;
+    for (int t = 0; t < S; t++)
+        if (tokens[t] < 0 || tokens[t] >= o->V) return -8;
+    return forward_rows(o, tokens, S, pos0, 0, last_only, logits);
 }
 
 /* training/forward.h:174-183 */

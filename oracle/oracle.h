@@ -51,6 +51,14 @@ int oracle_forward_last(OracleModel *o, const int *tokens, int S, float *logits)
  * forward.h's arithmetic).  logits [vocab]. */
 int oracle_decode_step(OracleModel *o, int token, int pos, float *logits);
 
+/* Mode (ii) over S rows: tokens at positions pos0..pos0+S-1 append their K/V
+ * to the cache and attend to cached positions 0..pos0+t; positions < pos0 must
+ * have been filled before.  With pos0 = 0 the logits equal mode (i)'s bit for
+ * bit, and S = 1 is oracle_decode_step.  logits [S, vocab], or [vocab] with
+ * last_only. */
+int oracle_forward_cached(OracleModel *o, const int *tokens, int S, int pos0, int last_only,
+                          float *logits);
+
 /* Mean next-token cross-entropy over S-1 positions (training/forward.h:174-183). */
 float oracle_loss(const float *logits, const int *tokens, int S, int vocab);
 

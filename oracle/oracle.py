@@ -30,6 +30,7 @@ def lib():
             "oracle_forward_full": (I, [P, ip, I, fp]),
             "oracle_forward_last": (I, [P, ip, I, fp]),
             "oracle_decode_step": (I, [P, I, I, fp]),
+            "oracle_forward_cached": (I, [P, ip, I, I, I, fp]),
             "oracle_loss": (F, [fp, ip, I, I]),
             "oracle_argmax": (I, [fp, I]),
             "oracle_matmul": (None, [fp, fp, fp, I, I, I]),
@@ -103,6 +104,16 @@ class Oracle:
         rc = lib().oracle_decode_step(self._h, int(token), int(pos), _f(out))
         if rc:
             raise RuntimeError(f"oracle_decode_step: {rc}")
+        return out
+
+    def forward_cached(self, tokens, pos0: int = 0, last_only: bool = False) -> np.ndarray:
+        """Rows at positions pos0.. appended to the cache, each attending to
+        cached positions 0..its own: logits [S, vocab] (or [vocab])."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab if last_only else (t.size, self.vocab), dtype=np.float32)
+        rc = lib().oracle_forward_cached(self._h, _i(t), t.size, int(pos0), int(last_only), _f(out))
+        if rc:
+            raise RuntimeError(f"oracle_forward_cached: {rc}")
         return out
 
     def greedy(self, first_token: int, pos0: int, n_steps: int, want_logits=False):

@@ -13,8 +13,16 @@ to the device path are caught, and so GPU tests need no long CPU runs.
                    untied classifier): 256 greedy ids from token 1 at positions
                    0..255 with fp32 K/V and with binary16 K/V, and per step the
                    top-32 (logit, id) pairs plus logit sum / sum of squares.
+  scaled_c4.npz    config C4 (the scaled Llama-2 model: dim 2048, 16 layers, 16
+                   heads of 128, SwiGLU 5632, vocab 32000, seed 4): prompts 0
+                   and 31 of the 32 x 512 uniform prompts (seed 104), fp32 K/V
+                   (the reference forward): the prompt's last-row logits, then
+                   128 greedy decode steps at positions 512..639; per row the
+                   top-32 (logit, id) pairs, 256 fixed sampled columns, sum and
+                   sum of squares, and the 129 greedy ids.
 
-Run:  python tests/golden/make_fixtures.py   (about a minute on 8 cores)
+Run:  python tests/golden/make_fixtures.py [name ...]   (names: tiny, c0, c4;
+      about a minute for tiny + c0 and a few minutes for c4 on 8 cores)
 """
 import os
 import sys
@@ -65,8 +73,54 @@ def stories_c0():
     print("wrote stories_c0")
 
 
+SCALED = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
+              seq_len=640)
+C4_SEQS = (0, 31)
+NCOLS = 256
+
+
+def row_digest(lg, cols):
+    """top-32 ids/values, sampled columns, sum and sum of squares of logit rows."""
+    lg = np.atleast_2d(lg)
+    idx = np.argsort(-lg, axis=1, kind="stable")[:, :TOPK].astype(np.int32)
+    return dict(top_idx=idx, top_val=np.take_along_axis(lg, idx, axis=1).astype(np.float32),
+                cols_val=lg[:, cols].astype(np.float32), sum=lg.astype(np.float64).sum(1),
+                sumsq=(lg.astype(np.float64) ** 2).sum(1))
+
+
+def scaled_c4():
+    import time
+    cfg = S.make_config(**SCALED)
+    w32 = S.f16_to_f32(S.synth_weights_f16(cfg, 4, 0.02, True))
+    prompts = np.random.default_rng(104).integers(0, 32000, (32, 512)).astype(np.int32)
+    cols = np.sort(np.random.default_rng(4040).choice(32000, NCOLS, replace=False)).astype(np.int32)
+    out = dict(seed=np.int64(4), prompt_seed=np.int64(104), seqs=np.array(C4_SEQS, np.int32), cols=cols,
+               n_steps=np.int32(128))
+    for b in C4_SEQS:
+        t0 = time.time()
+        o = O.Oracle(cfg7(SCALED), w32, True, 640)
+        rows = [o.forward_cached(prompts[b], 0, last_only=True)]
+        ids = [O.argmax(rows[0])]
+        for s in range(128):
+            rows.append(o.decode_step(ids[-1], 512 + s))
+            ids.append(O.argmax(rows[-1]))
+        o.close()
+        dg = row_digest(np.stack(rows), cols)
+        for k, v in dg.items():
+            out[f"{k}_{b}"] = v
+        out[f"ids_{b}"] = np.array(ids, np.int32)
+        print(f"c4 sequence {b}: {time.time() - t0:.1f} s", flush=True)
+    np.savez_compressed(os.path.join(HERE, "scaled_c4.npz"), **out)
+    print("wrote scaled_c4")
+
+
 if __name__ == "__main__":
-    tiny("mha", TINY, 11)
-    tiny("gqa", TINY_GQA, 12)
-    tiny("hd128", TINY_HD128, 13)
-    stories_c0()
+    which = set(sys.argv[1:]) or {"tiny", "c0", "c4"}
+    if "tiny" in which:
+        tiny("mha", TINY, 11)
+        tiny("gqa", TINY_GQA, 12)
+        tiny("hd128", TINY_HD128, 13)
+    if "c0" in which:
+        stories_c0()
+    if "c4" in which:
+        scaled_c4()

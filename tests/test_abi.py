@@ -5,6 +5,7 @@ import glob
 import os
 import re
 
+import numpy as np
 import pytest
 
 from conftest import ROOT
@@ -61,3 +62,33 @@ def test_null_arguments_rejected_before_device(lm):
     assert L.lm_generate_greedy(None, 1, None, None, 1, None) == lm.LM_ERR_INVALID
     assert not L.lm_forward(None, 0, 0)
     L.lm_free(None)
+
+
+def test_create_layers_rejects_null_entries_before_device(lm):
+    """lm_create_layers checks every per-layer pointer before any device call
+    (here: layer 1 of wq missing), and split_layers' per-layer copies hold the
+    contiguous buffer's values."""
+    from conftest import TINY_GQA
+    cfg = lm.make_config(**TINY_GQA)
+    w16 = lm.synth_weights_f16(cfg, 3, 0.02, True)
+    t = lm.split_layers(cfg, w16, True)
+    names = ("token_embedding",) + lm.LAYER_TENSORS + ("rms_final_w", "wcls")
+    flat = np.concatenate([np.concatenate(t[n]) if n in lm.LAYER_TENSORS else t[n] for n in names])
+    assert np.array_equal(flat, w16)
+    assert all(len(t[n]) == cfg.n_layers for n in lm.LAYER_TENSORS)
+    t["wq"][1] = None
+    w = lm.LMLayerWeights()
+    w.dtype = lm.LM_DTYPE_F16
+    w.token_embedding = t["token_embedding"].ctypes.data
+    keep = []
+    for n in lm.LAYER_TENSORS:
+        ptrs = (ctypes.c_void_p * cfg.n_layers)(*[a.ctypes.data if a is not None else None for a in t[n]])
+        keep.append(ptrs)
+        setattr(w, n, ctypes.cast(ptrs, ctypes.POINTER(ctypes.c_void_p)))
+    w.rms_final_w = t["rms_final_w"].ctypes.data
+    st = ctypes.c_int(99)
+    assert not lm.lib().lm_create_layers(ctypes.byref(cfg), ctypes.byref(w), 1, 16, ctypes.byref(st))
+    assert st.value == lm.LM_ERR_INVALID
+    w.wq = None
+    assert not lm.lib().lm_create_layers(ctypes.byref(cfg), ctypes.byref(w), 1, 16, ctypes.byref(st))
+    assert st.value == lm.LM_ERR_INVALID

@@ -116,6 +116,13 @@ def test_host_validation_errors(lm):
     assert e.value.status == lm.LM_ERR_RANGE
     with pytest.raises(lm.LMError):
         m.forward(-1, 0)
+    toks = np.zeros((2, 4), np.int32)
+    with pytest.raises(lm.LMError) as e:
+        m.prefill_batch(toks, slots=[1, 1])       # one slot for two sequences
+    assert e.value.status == lm.LM_ERR_INVALID
+    with pytest.raises(ValueError):
+        m.prefill_batch(toks, slots=[0])          # fewer slots than sequences
+    m.prefill_batch(toks, slots=[1, 0])           # still usable
     m.close()
 
 
@@ -196,3 +203,24 @@ def test_profile_chain_times_every_family(lm):
     row = m.forward(1, 0)
     assert np.all(np.isfinite(row))
     m.close()
+
+
+@pytest.mark.parametrize("untied", [True, False])
+@pytest.mark.parametrize("f32", [False, True])
+def test_create_layers_equals_create(lm, untied, f32):
+    """lm_create_layers over separately allocated per-layer tensors (the
+    reference Model's layout) builds the same model as lm_create over the
+    contiguous buffer: decode logits and prefill logits bit for bit."""
+    _say(f"[create layers untied={untied} f32={f32}]")
+    d = TINY_GQA
+    cfg = lm.make_config(**d)
+    w16 = lm.synth_weights_f16(cfg, 26, 0.02, untied)
+    w = lm.f16_to_f32(w16) if f32 else w16
+    m1 = lm.Model.create(cfg, w, untied, 2, 64)
+    m2 = lm.Model.create_layers(cfg, lm.split_layers(cfg, w, untied), 2, 64)
+    toks = np.random.default_rng(26).integers(0, d["vocab_size"], 24).astype(np.int32)
+    for p, t in enumerate(toks[:12]):
+        assert np.array_equal(m1.forward(int(t), p), m2.forward(int(t), p))
+    assert np.array_equal(m1.prefill(toks, slot=1), m2.prefill(toks, slot=1))
+    m1.close()
+    m2.close()

@@ -34,6 +34,24 @@ def test_full_forward_equals_kv_decode_bitwise(lm, orc, d, kv16):
     assert np.array_equal(full, rows)
 
 
+@pytest.mark.parametrize("d", [TINY_GQA, TINY_HD128], ids=["gqa", "hd128"])
+@pytest.mark.parametrize("kv16", [False, True])
+def test_cached_rows_equal_full_forward_bitwise(lm, orc, d, kv16):
+    """The cache-appending multi-row forward in chunks (positions 0..12, then
+    13..32, then one row) equals the full forward and the one-row decode."""
+    w = _weights(lm, d, 8)
+    toks = np.random.default_rng(8).integers(0, d["vocab_size"], 34)
+    full = orc.Oracle(cfg7(d), w, True, 64, kv_f16=kv16).forward_full(toks)
+    o = orc.Oracle(cfg7(d), w, True, 64, kv_f16=kv16)
+    rows = np.concatenate([o.forward_cached(toks[:13]), o.forward_cached(toks[13:33], 13),
+                           o.forward_cached(toks[33:], 33)])
+    assert np.array_equal(full, rows)
+    o2 = orc.Oracle(cfg7(d), w, True, 64, kv_f16=kv16)
+    last = o2.forward_cached(toks[:20], 0, last_only=True)
+    assert np.array_equal(last, full[19])
+    assert np.array_equal(o2.decode_step(int(toks[20]), 20), full[20])
+
+
 def test_forward_last_is_last_row_of_full(lm, orc):
     """The window-recompute mode (classifier on the last row only) gives the
     full forward's last row bit for bit."""

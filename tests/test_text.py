@@ -220,3 +220,34 @@ def test_sampler_argument_errors():
         S.sample_temperature(np.zeros(4, np.float32), 0.0, S.Rng(1))
     with pytest.raises(S.LMError):
         S.sample_topp(np.zeros(4, np.float32), -1.0, 0.9, S.Rng(1))
+
+
+@pytest.mark.parametrize("n,vectors,draws", [(7, 30, 100), (300, 12, 150), (32000, 3, 25)])
+def test_samplers_draw_for_draw_against_reference(n, vectors, draws):
+    """The product samplers pick the same ids as the reference's
+    sample_temperature / sample_topp (generate.m:138-209, restated with libc
+    expf and srand48/drand48 in tests/ref_samplers.py) on the same logits and
+    the same seeded stream: thousands of draws over temperatures, nucleus
+    sizes, tied and peaked logits.  At the full vocabulary the logits are
+    peaked (a nucleus of a few hundred ids): the reference's selection sort
+    costs O(vocab x nucleus) per draw."""
+    import ref_samplers as R
+    rng = np.random.default_rng(n)
+    for v in range(vectors):
+        scale = 8.0 if n > 1000 else (0.5, 3.0, 8.0)[v % 3]
+        logits = (rng.standard_normal(n) * scale).astype(np.float32)
+        if v % 4 == 1:                        # ties: the sort must keep the reference's order
+            logits[rng.integers(0, n, max(2, min(n // 5, 40)))] = logits.max()
+        temp = (0.5, 0.8, 1.0, 1.3)[v % 4]
+        topp = (0.9, 0.5, 0.99, 0.75)[(v // 2) % 4]
+        seed = 1000 * n + v
+        probs = R.softmax_t(logits, temp)
+        nuc = R.nucleus(probs, topp)
+        R.srand48(seed)
+        want_t = [R.draw_temperature(probs) for _ in range(draws)]
+        want_p = [R.draw_topp(probs, nuc) for _ in range(draws)]
+        r = S.Rng(seed)
+        got_t = [S.sample_temperature(logits, temp, r) for _ in range(draws)]
+        got_p = [S.sample_topp(logits, temp, topp, r) for _ in range(draws)]
+        assert got_t == want_t, (n, v)
+        assert got_p == want_p, (n, v)
