@@ -154,6 +154,12 @@ int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W,
 int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
                 const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn);
 
+/* ---- allocation-free entry point (k_noalloc.hip) -------------------------- */
+
+/* Look up, once for the current device, the device address of the static
+ * argmax-partials scratch of lm_gemm_argmax_noalloc (called by lm_init). */
+int lmk_noalloc_setup(void);
+
 /* ---- diagnostics kernels (k_decode.hip) ---------------------------------- */
 
 /* Wave-reduction self-check: out[0..3] = sums computed with the production

@@ -114,6 +114,11 @@ int lm_init(void)
         g_init_status = LM_ERR_NO_DEVICE;
         return g_init_status;
     }
+    if (lmk_noalloc_setup() != hipSuccess) {
+        fprintf(stderr, "stories_lm: lookup of the static scratch's device address failed\n");
+        g_init_status = LM_ERR_HIP;
+        return g_init_status;
+    }
     g_init_status = LM_OK;
     return LM_OK;
 }

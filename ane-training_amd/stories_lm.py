@@ -252,6 +252,7 @@ def lib():
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
         "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
         "lm_gemm_split_count": (I, [I, I, I]),
+        "lm_gemm_argmax_noalloc": (I, [I, I, I, P, P, P, P, P]),
         "lm_selftest_gemm_gate": (I, [I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16),
                                       C.POINTER(C.c_uint16)]),
         "lm_tokenizer_load": (P, [C.c_char_p, I, ip]),
@@ -442,6 +443,13 @@ def selftest_gemm(A: np.ndarray, W16: np.ndarray, want_parts: bool = False):
     if want_parts:
         return out, parts[..., 0].view(np.float32), parts[..., 1]
     return out
+
+
+def gemm_argmax_noalloc(M: int, N: int, K: int, dA: int, dW: int, dC, dIds: int, stream=None) -> int:
+    """lm_gemm_argmax_noalloc on device addresses (ints; dC may be None):
+    queues C = A W^T and the per-row argmax on `stream`, allocating nothing.
+    Returns the status code."""
+    return int(lib().lm_gemm_argmax_noalloc(M, N, K, dA, dW, dC, dIds, stream))
 
 
 def gemm_split_count(M: int, N: int, K: int) -> int:

@@ -314,6 +314,20 @@ int lm_selftest_gemm_split(int M, int N, int K, int nsplit, const uint16_t *A, c
  * N a multiple of 32, K of 64. */
 int lm_selftest_gemm_gate(int M, int N, int K, const uint16_t *A, const uint16_t *W, uint16_t *g);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): the GEMM and argmax of lm_selftest_gemm on the caller's device
+ * buffers, allocating nothing.  C = A W^T (fp32 accumulation; A [M, K] and W
+ * [N, K] fp16 bits, C [M, N] fp32, all device pointers; C may be NULL) and
+ * ids[m] = the lowest column of row m's maximum (device int[M]), queued on
+ * `stream` (a hipStream_t; NULL = the null stream) without waiting.  The
+ * argmax partials live in a static 512 KiB device array per GPU, so M *
+ * ceil(N / 32) may not exceed 65536 (LM_ERR_RANGE beyond, nothing queued);
+ * K % 64 == 0.  Calls that overlap on one GPU share that array and race.
+ * lm_init must have succeeded (LM_ERR_NOT_INIT otherwise). */
+int lm_gemm_argmax_noalloc(int M, int N, int K, const uint16_t *A, const uint16_t *W, float *C,
+                           int *ids, void *stream);
+
 /* The split count the runtime uses for an [M, K] x [N, K]^T GEMM (1: unsplit). */
 int lm_gemm_split_count(int M, int N, int K);
 
