@@ -1113,63 +1113,6 @@ int lm_selftest_reduce(const float *in64, float *out4)
     return LM_OK;
 }
 
-/* Diagnostics: mean device time per launch of each decode kernel family.  For
- * family f `reps` rounds of its per-step launches (every layer for the
- * per-layer kernels) run between two hipEvents on the handle's stream, as one
- * captured graph (or launched directly when graphs are off); positions pos[b]
- * are held fixed (the argmax kernel's advance of pos is undone before the
- * timed run). */
-int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
-                      float *us_per_launch, int *launches_per_step)
-{
-    if (!m || !tokens || !pos || !us_per_launch || B < 1 || reps < 1) return LM_ERR_INVALID;
-    if (B > m->max_batch) return LM_ERR_RANGE;
-    if (B > MAX_GEMV_B) return LM_ERR_UNSUPPORTED;
-    int rc = check_tok_pos(m, tokens, pos, B);
-    if (rc) return rc;
-    int *hio = m->h_io;
-    memcpy(hio, tokens, B * 4);
-    memcpy(hio + B, pos, B * 4);
-    HIPCHK(hipMemcpyAsync(m->d_tok, hio, B * 4, hipMemcpyHostToDevice, m->stream));
-    for (int f = 0; f < LM_KERN_COUNT && rc == LM_OK; f++) {
-        const int per_step = (f == LM_KERN_CLS || f == LM_KERN_ARGMAX) ? 1 : m->L;
-        if (launches_per_step) launches_per_step[f] = per_step;
-        hipGraph_t g = NULL;
-        hipGraphExec_t ge = NULL;
-        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
-        HIPCHK(hipStreamSynchronize(m->stream));
-        if (m->use_graph) {
-            HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-            for (int r = 0; r < reps && rc == LM_OK; r++)
-                for (int l = 0; l < per_step && rc == LM_OK; l++) rc = enqueue_kernel(m, B, f, l, NULL);
-            hipError_t e = hipStreamEndCapture(m->stream, &g);
-            if (rc == LM_OK && e != hipSuccess) rc = LM_ERR_HIP;
-            if (rc == LM_OK && hipGraphInstantiateWithFlags(&ge, g, 0) != hipSuccess) rc = LM_ERR_HIP;
-        }
-        float ms = 0.f;
-        for (int it = 0; it < 2 && rc == LM_OK; it++) {   /* warm-up run, timed run */
-            if (f == LM_KERN_ARGMAX &&
-                hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
-                rc = LM_ERR_HIP;
-            if (rc == LM_OK && hipEventRecord(m->ev0, m->stream) != hipSuccess) rc = LM_ERR_HIP;
-            if (rc == LM_OK && ge && hipGraphLaunch(ge, m->stream) != hipSuccess) rc = LM_ERR_HIP;
-            for (int r = 0; !ge && r < reps && rc == LM_OK; r++)
-                for (int l = 0; l < per_step && rc == LM_OK; l++) rc = enqueue_kernel(m, B, f, l, NULL);
-            if (rc == LM_OK && (hipEventRecord(m->ev1, m->stream) != hipSuccess ||
-                                hipEventSynchronize(m->ev1) != hipSuccess ||
-                                hipEventElapsedTime(&ms, m->ev0, m->ev1) != hipSuccess))
-                rc = LM_ERR_HIP;
-        }
-        if (ge) hipGraphExecDestroy(ge);
-        if (g) hipGraphDestroy(g);
-        us_per_launch[f] = ms * 1e3f / (float)(reps * per_step);
-    }
-    if (rc == LM_OK)
-        HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
-    HIPCHK(hipStreamSynchronize(m->stream));
-    return rc;
-}
-
 int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int steps,
                      float *us_per_launch, int *launches_per_step)
 {
@@ -1181,7 +1124,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     if (rc) return rc;
     for (int b = 0; b < B; b++)
         if (pos[b] + steps + 1 > m->max_seq) return LM_ERR_RANGE;
-    /* kernels of one step: 5 per layer, then cls, argmax */
+    /* kernels of one step: 5 per layer, then the classifier and the argmax */
     const int nk = 5 * m->L + 2;
     hipEvent_t *ev = (hipEvent_t *)calloc(2 * (size_t)nk, sizeof(hipEvent_t));
     int *kfam = (int *)calloc((size_t)nk, sizeof(int));

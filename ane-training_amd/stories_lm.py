@@ -247,7 +247,6 @@ def lib():
         "lm_f16_to_f32": (None, [C.POINTER(C.c_uint16), fp, C.c_size_t]),
         "lm_rope_table": (I, [I, I, fp, fp]),
         "lm_selftest_reduce": (I, [fp, fp]),
-        "lm_profile_decode": (I, [P, I, ip, ip, I, fp, ip]),
         "lm_profile_chain": (I, [P, I, ip, ip, I, fp, ip]),
         "lm_selftest_gemm": (I, [I, I, I, I, P, C.POINTER(C.c_uint16), fp, P]),
         "lm_selftest_gemm_split": (I, [I, I, I, I, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), fp]),
@@ -637,18 +636,6 @@ class Model:
 
     def timer_begin(self):
         self._check(lib().lm_timer_begin(self._h), "lm_timer_begin")
-
-    def profile_decode(self, tokens, pos, reps=32):
-        """Mean device microseconds per launch of each decode kernel family
-        (graph of `reps` rounds of that family's launches, timed with hipEvents).
-        Returns (us_per_launch, launches_per_step), dicts keyed by KERN_NAMES."""
-        t = np.ascontiguousarray(tokens, dtype=np.int32)
-        p = np.ascontiguousarray(pos, dtype=np.int32)
-        us = np.zeros(len(KERN_NAMES), dtype=np.float32)
-        n = np.zeros(len(KERN_NAMES), dtype=np.int32)
-        rc = lib().lm_profile_decode(self._h, t.size, _ip(t), _ip(p), reps, _fp(us), _ip(n))
-        self._check(rc, "lm_profile_decode")
-        return dict(zip(KERN_NAMES, us.tolist())), dict(zip(KERN_NAMES, n.tolist()))
 
     def profile_chain(self, tokens, pos, steps=8):
         """Mean device microseconds per launch of each decode kernel family in

@@ -331,33 +331,25 @@ int lm_gemm_argmax_noalloc(int M, int N, int K, const uint16_t *A, const uint16_
 /* The split count the runtime uses for an [M, K] x [N, K]^T GEMM (1: unsplit). */
 int lm_gemm_split_count(int M, int N, int K);
 
-/* Kernel families of a decode step (index into lm_profile_decode's output). */
+/* Kernel families of a decode step (index into lm_profile_chain's output). */
 #define LM_KERN_QKV    0   /* rmsnorm + QKV GEMV + RoPE + KV append          */
 #define LM_KERN_ATTN   1   /* causal attention over the KV cache              */
-#define LM_KERN_WO     2   /* Wo GEMV + residual (no launches when fused)   */
+#define LM_KERN_WO     2   /* Wo GEMV + residual                            */
 #define LM_KERN_W13    3   /* rmsnorm + W1/W3 GEMV + SiLU gate              */
 #define LM_KERN_W2     4   /* W2 GEMV + residual                            */
-#define LM_KERN_CLS    5   /* final rmsnorm + classifier + argmax partials  */
+#define LM_KERN_CLS    5   /* final rmsnorm + classifier + argmax partials   */
 #define LM_KERN_ARGMAX 6   /* argmax reduction + greedy loop state          */
 #define LM_KERN_COUNT  7
-
-/* Mean device microseconds per launch of each decode kernel family for B rows
- * at tokens[b], positions pos[b]: the launches of one family (each layer for
- * the per-layer families) run `reps` times between hipEvents on the handle's
- * stream, as one captured graph (directly when LM_OPT_USE_GRAPH is 0).  launches_per_step[k] (may be
- * NULL) = launches of family k in one decode step.  Leaves the KV cache
- * entries at pos[b] and the activations overwritten. */
-int lm_profile_decode(LMModel *m, int B, const int *tokens, const int *pos, int reps,
-                      float *us_per_launch, int *launches_per_step);
 
 /* Mean device microseconds per launch of each decode kernel family inside the
  * real decode chain: `steps` greedy decode steps of B rows from tokens[b] at
  * positions pos[b] (advancing as a decode does), launched directly, every
  * kernel timed by events at its own dispatch's start and end (the kernel plus
  * a dispatch overhead a kernel trace leaves out; no kernel measures under
- * about 3.9 us).  One untimed step runs first.  launches_per_step as in
- * lm_profile_decode.  Needs pos[b] + steps + 1 <= max_seq; leaves the KV cache
- * at those positions and the activations overwritten. */
+ * about 3.9 us).  One untimed step runs first.  launches_per_step[k] (may
+ * be NULL) = launches of family k in one decode step.  Needs pos[b] + steps +
+ * 1 <= max_seq; leaves the KV cache at those positions and the activations
+ * overwritten. */
 int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int steps,
                      float *us_per_launch, int *launches_per_step);
 
