@@ -57,6 +57,8 @@ extern "C" void lmk_time_next(hipEvent_t start, hipEvent_t stop)
 
 #define WG 256
 #define NWAVE (WG / 64)
+/* rows of the tagged hand-off buffers (the batch 1-4 chain) */
+#define MAX_TAG_B 4
 
 /* ---- prologues ---------------------------------------------------------- */
 
@@ -217,13 +219,43 @@ __device__ __forceinline__ void pair_reduce(const float acc[NB], float r0[NB], f
 
 /* ---- QKV + RoPE + KV append ------------------------------------------------ */
 
+/* Hand-off words of the fused QKV + attention kernel: 64-bit words {value
+ * bits, tag}, stored and loaded as relaxed agent-scope atomics, so a reader
+ * that sees the current tag sees that launch's value (each word carries its
+ * own proof of freshness; no ordering between words is assumed).  q, k and v
+ * of row b: tq[b*NQ + i], tk[b*NKV + i], tv[b*NKV + i] (k and v as the cache
+ * stores them).  The tag of a launch is epoch * n_layers + layer + 1, epoch the
+ * decode-step count the argmax kernel advances: never 0 (the buffers' initial
+ * contents) and never repeated within 2^32 launches. */
+struct QkvTagged {
+    unsigned long long *tq, *tk, *tv;
+    const unsigned *epoch;
+    int layer, n_layers;
+    int *err;                       /* set when a hand-off wait gives up */
+};
+
+__device__ __forceinline__ unsigned qkv_tag(const QkvTagged &t)
+{
+    return *t.epoch * (unsigned)t.n_layers + (unsigned)t.layer + 1u;
+}
+
+__device__ __forceinline__ void tag_store(unsigned long long *w, float v, unsigned tag)
+{
+    const unsigned long long word =
+        ((unsigned long long)tag << 32) | (unsigned long long)__builtin_bit_cast(unsigned, v);
+    __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Rows of [Wq; Wk; Wv] . rmsnorm(x[b]) for the row pairs of this work-group,
+ * RoPE'd and stored (q fp32, k/v into the cache); with tg, also as tagged
+ * hand-off words. */
 template <int D, int NB, typename KT>
-__global__ void __launch_bounds__(WG) k_qkv_rope(
+__device__ __forceinline__ void qkv_rows(
     float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
     const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV, int hd,
     const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
     int B, float *__restrict__ q, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq,
-    int npairs)
+    int npairs, const QkvTagged *tg)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
@@ -256,6 +288,7 @@ __global__ void __launch_bounds__(WG) k_qkv_rope(
     const int lg = __builtin_ctz((unsigned)hd);
     const int Hkv = NKV >> lg;
     const int h = rr >> lg, d = rr & (hd - 1);
+    const unsigned tag = tg ? qkv_tag(*tg) : 0u;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         if (b >= B) break;
@@ -264,18 +297,43 @@ __global__ void __launch_bounds__(WG) k_qkv_rope(
             const float o0 = fmaf(a, c, -(e * sn));  /* forward.h:64 */
             const float o1 = fmaf(a, sn, e * c);     /* forward.h:65 */
             if (r < NQ) {
-                *(float2 *)(q + (size_t)b * NQ + r) = make_float2(o0, o1);
+                if (tg) {
+                    tag_store(tg->tq + (size_t)b * NQ + r, o0, tag);
+                    tag_store(tg->tq + (size_t)b * NQ + r + 1, o1, tag);
+                } else {
+                    *(float2 *)(q + (size_t)b * NQ + r) = make_float2(o0, o1);
+                }
             } else {
                 KT *dst = kc + (((size_t)b * Hkv + h) * max_seq + ps[b]) * hd + d;
                 dst[0] = kv_pack<KT>(o0);
                 dst[1] = kv_pack<KT>(o1);
+                if (tg) {
+                    tag_store(tg->tk + (size_t)b * NKV + rr, kv_round<KT>(o0), tag);
+                    tag_store(tg->tk + (size_t)b * NKV + rr + 1, kv_round<KT>(o1), tag);
+                }
             }
         } else {
             KT *dst = vc + (((size_t)b * Hkv + h) * max_seq + ps[b]) * hd + d;
             dst[0] = kv_pack<KT>(r0[b]);
             dst[1] = kv_pack<KT>(r1[b]);
+            if (tg) {
+                tag_store(tg->tv + (size_t)b * NKV + rr, kv_round<KT>(r0[b]), tag);
+                tag_store(tg->tv + (size_t)b * NKV + rr + 1, kv_round<KT>(r1[b]), tag);
+            }
         }
     }
+}
+
+template <int D, int NB, typename KT>
+__global__ void __launch_bounds__(WG) k_qkv_rope(
+    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
+    const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV, int hd,
+    const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
+    int B, float *__restrict__ q, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq,
+    int npairs)
+{
+    qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, hd, rc, rs, pos, B, q, kc, vc, max_seq, npairs,
+                        nullptr);
 }
 
 /* ---- decode attention ------------------------------------------------------- */
@@ -328,7 +386,7 @@ template <int HD, typename KT>
 __device__ __forceinline__ void attn_head(
     const float *__restrict__ q, const KT *__restrict__ kc, const KT *__restrict__ vc,
     const int *__restrict__ pos, const int *__restrict__ slot, int H, int Hkv, int max_seq,
-    float *oh, const QkvPart<KT> *qp = nullptr)
+    float *oh, int h, int b, const QkvPart<KT> *qp = nullptr, const QkvTagged *qt = nullptr)
 {
     /* positions per tile: 32 (measured against 64: the four waves share short
      * contexts more evenly).  Two tiles fit the registers except at hd 128 with
@@ -344,12 +402,12 @@ __device__ __forceinline__ void attn_head(
     __shared__ __attribute__((aligned(16))) float so[NWAVE][HD];
     __shared__ __attribute__((aligned(16))) float sqkv[3][HD];   /* q, k, v of a split QKV */
     __shared__ float scur;                                        /* its current score */
-    const int h = blockIdx.x, b = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ctx = pos[b] + 1;
-    /* positions read from the cache: all of them, or with qp all but the
+    /* positions read from the cache: all of them, or with qp / qt all but the
      * current one, which is added from LDS at the end */
-    const int vis = qp ? ctx - 1 : ctx;
+    const bool cur = qp || qt;
+    const int vis = cur ? ctx - 1 : ctx;
     const int ntiles = (vis + TILE - 1) / TILE;
     const int dq = lane % G, pp = lane / G;
     const int cs = slot ? slot[b] : b;
@@ -359,7 +417,7 @@ __device__ __forceinline__ void attn_head(
     /* scores in log2 units: exp(x) = exp2(x * log2 e), the hardware exp2 */
     const float scale = 1.4426950408889634f / sqrtf((float)HD);
     float qf[8];
-    if (!qp) {
+    if (!cur) {
         const float *qr = q + (size_t)b * H * HD + h * HD + dq * 8;
         const float4 a = *(const float4 *)qr, c = *(const float4 *)(qr + 4);
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
@@ -377,7 +435,7 @@ __device__ __forceinline__ void attn_head(
     constexpr bool EARLY = HD == 64;
     Raw kr[NP], vr[NP];
     Raw kr1[NP], vr1[NP];            /* the wave's next tile (DB) */
-    if (EARLY) {
+    if (EARLY || qt) {   /* also at hd 128 when q waits for the QKV work-groups */
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const int p = min(wv * TILE + pp + PP * i, max_seq - 1);
@@ -431,6 +489,33 @@ __device__ __forceinline__ void attn_head(
                 dst[3] = kv_pack<KT>(acc.w);
             }
         }
+    }
+    if (qt) {
+        /* q, k, v of the current position from the tagged hand-off words the
+         * QKV work-groups of this launch store (k, v as the cache holds
+         * them), after the first K/V tile's loads are in flight: each thread
+         * polls its words until they carry this launch's tag (bounded: a wait
+         * that gives up sets qt->err, and the kernel still ends) */
+        const unsigned tag = qkv_tag(*qt);
+        const int g = small_div(h, small_div(H, Hkv));
+        for (int t = threadIdx.x; t < 3 * HD; t += WG) {
+            const int vec = t / HD, e = t % HD;
+            const unsigned long long *w =
+                vec == 0 ? qt->tq + (size_t)b * H * HD + h * HD + e
+                         : (vec == 1 ? qt->tk : qt->tv) + (size_t)b * Hkv * HD + g * HD + e;
+            unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int spin = 0; (unsigned)(v >> 32) != tag; spin++) {
+                if (spin == (1 << 20)) {
+                    __hip_atomic_store(qt->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sqkv[vec][e] = __builtin_bit_cast(float, (unsigned)v);
+        }
+    }
+    if (cur) {
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 8; j++) qf[j] = sqkv[0][dq * 8 + j];
@@ -510,7 +595,7 @@ __device__ __forceinline__ void attn_head(
                 kv_raw_load(V + (size_t)p * HD, tv[i]);
             }
         };
-        if (!EARLY) fetch(wv, kr, vr);
+        if (!EARLY && !qt) fetch(wv, kr, vr);
         if constexpr (DB) {
             /* kr holds the wave's first tile and kr1 its second (both in
              * flight); the first tile is consumed outside the loop, which keeps
@@ -549,7 +634,7 @@ __device__ __forceinline__ void attn_head(
     __syncthreads();
     if (threadIdx.x < HD) {
         const int d = threadIdx.x;
-        float M = qp ? scur : -INFINITY;
+        float M = cur ? scur : -INFINITY;
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) M = fmaxf(M, sm[w]);
         float L = 0.f, acc = 0.f;
@@ -559,7 +644,7 @@ __device__ __forceinline__ void attn_head(
             L = fmaf(sl[w], f, L);
             acc = fmaf(so[w][d], f, acc);
         }
-        if (qp) {   /* the current position, after the cached ones */
+        if (cur) {   /* the current position, after the cached ones */
             const float f = __builtin_amdgcn_exp2f(scur - M);
             L += f;
             acc = fmaf(kv_round<KT>(sqkv[2][d]), f, acc);
@@ -578,7 +663,7 @@ __global__ void __launch_bounds__(WG) k_attn_decode(
     float *__restrict__ out, u16 *__restrict__ out16)
 {
     __shared__ float oh[HD];
-    attn_head<HD, KT>(q, kc, vc, pos, slot, H, Hkv, max_seq, oh);
+    attn_head<HD, KT>(q, kc, vc, pos, slot, H, Hkv, max_seq, oh, blockIdx.x, blockIdx.y);
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     if (d < HD) {
         if (out16) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
@@ -598,9 +683,38 @@ __global__ void __launch_bounds__(WG) k_attn_decode_part(
 {
     __shared__ float oh[HD];
     const QkvPart<KT> qp = {part, sstride, ns, NQ, NKV, rc, rs, kc, vc};
-    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, &qp);
+    attn_head<HD, KT>(nullptr, kc, vc, pos, slot, H, Hkv, max_seq, oh, blockIdx.x, blockIdx.y, &qp);
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     if (d < HD) out16[(size_t)b * H * HD + h * HD + d] = f2h(oh[d]);
+}
+
+/* ---- QKV + attention in one launch (batch 1-4 decode) ----------------------- */
+
+/* Work-groups 0 .. nprod-1 are the QKV GEMV of k_qkv_rope (which also stores
+ * q, k, v as tagged hand-off words); work-group nprod + b*H + h then runs the
+ * attention of head h, row b: it loads its first cached K/V tile, waits for
+ * the current position's q, k, v words of this launch, and writes the head
+ * output to out[b, h*HD ..] (fp32).  The attention work-groups come after every
+ * QKV work-group in dispatch order and only wait for them, so the waits end
+ * however many work-groups the device holds at once. */
+template <int D, int NB, typename KT, int HD>
+__global__ void __launch_bounds__(WG) k_qkv_attn(
+    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
+    const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV,
+    const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
+    int B, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq, int npairs, int nprod, int H,
+    QkvTagged tg, float *__restrict__ out)
+{
+    if ((int)blockIdx.x < nprod) {
+        qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, HD, rc, rs, pos, B, nullptr, kc, vc,
+                            max_seq, npairs, &tg);
+        return;
+    }
+    __shared__ float oh[HD];
+    const int a = blockIdx.x - nprod;
+    const int h = a % H, b = a / H;
+    attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
+    if ((int)threadIdx.x < HD) out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
 }
 
 /* ---- Wo + residual ---------------------------------------------------------- */
@@ -773,7 +887,7 @@ __global__ void __launch_bounds__(WG) k_cls(
  * and pos[b] += 1 (device-resident greedy loop state). */
 __global__ void __launch_bounds__(WG) k_argmax_final(
     const LMArgPart *__restrict__ part, int nblk, int *__restrict__ tok, int *__restrict__ pos,
-    int *__restrict__ hist, int hist_stride)
+    int *__restrict__ hist, int hist_stride, unsigned *__restrict__ epoch)
 {
     __shared__ float sv[NWAVE];
     __shared__ int si[NWAVE];
@@ -803,6 +917,7 @@ __global__ void __launch_bounds__(WG) k_argmax_final(
             hist[(size_t)b * hist_stride + p + 1] = id;
             pos[b] = p + 1;
         }
+        if (epoch && b == 0) *epoch += 1u;   /* the next step's hand-off tags */
     }
 }
 
@@ -873,6 +988,36 @@ extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const 
                                rms_w, wqkv, NQ, NKV, hd, rope_cos, rope_sin, pos, B, q,
                                (u16 *)kc, (u16 *)vc, max_seq, npairs);
     }));
+    return hipGetLastError();
+}
+
+extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
+                            const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
+                            const float *rope_cos, const float *rope_sin, const int *pos, int B,
+                            void *kc, void *vc, int kv_f32, int max_seq, int H,
+                            unsigned long long *tagged, const unsigned *epoch, int layer,
+                            int n_layers, int *err, float *out)
+{
+    if (B < 1 || B > 4 || NQ != D || H < 1 || NQ != H * hd || NKV % hd || H % (NKV / hd) ||
+        (emb && !tok) || !tagged || !epoch || !err || !out || (hd != 64 && hd != 128))
+        return hipErrorInvalidValue;
+    const int npairs = (NQ + 2 * NKV) / 2;
+    const int nprod = (npairs + NWAVE - 1) / NWAVE;
+    dim3 grid(nprod + H * B);
+    const QkvTagged tg = {tagged, tagged + (size_t)MAX_TAG_B * NQ,
+                          tagged + (size_t)MAX_TAG_B * (NQ + NKV), epoch, layer, n_layers, err};
+#define LAUNCH_QA(HD_, KT_)                                                                        \
+    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv, NQ,   \
+            NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H, tg,  \
+            out)
+    DISPATCH_D(D, DISPATCH_NB(B, {
+        if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
+        if (hd == 64 && kv_f32) LAUNCH_QA(64, float);
+        else if (hd == 64) LAUNCH_QA(64, u16);
+        else if (kv_f32) LAUNCH_QA(128, float);
+        else LAUNCH_QA(128, u16);
+    }));
+#undef LAUNCH_QA
     return hipGetLastError();
 }
 
@@ -971,11 +1116,11 @@ extern "C" int lmk_cls(hipStream_t s, const float *x, const float *rms_w, const 
 }
 
 extern "C" int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B, int *tok,
-                                int *pos, int *hist, int hist_stride)
+                                int *pos, int *hist, int hist_stride, unsigned *epoch)
 {
     if (B < 1 || nblk < 1 || !tok || (hist && !pos)) return hipErrorInvalidValue;
     DLAUNCH(k_argmax_final, dim3(B), dim3(WG), 0, s, part, nblk, tok, pos, hist,
-                       hist_stride);
+                       hist_stride, epoch);
     return hipGetLastError();
 }
 

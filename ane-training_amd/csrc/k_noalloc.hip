@@ -73,7 +73,7 @@ extern "C" int lm_gemm_argmax_noalloc(int M, int N, int K, const uint16_t *A, co
     ep.ldc = N;
     ep.part = g_scratch[dev];
     int e = lmk_gemm(s, A, K, W, M, N, K, LMK_EPI_ARGMAX, &ep);
-    if (e == 0) e = lmk_argmax_final(s, g_scratch[dev], nblk, M, ids, nullptr, nullptr, 0);
+    if (e == 0) e = lmk_argmax_final(s, g_scratch[dev], nblk, M, ids, nullptr, nullptr, 0, nullptr);
     if (e != 0) {
         fprintf(stderr, "stories_lm: lm_gemm_argmax_noalloc: launch failed: %s\n",
                 hipGetErrorString((hipError_t)e));

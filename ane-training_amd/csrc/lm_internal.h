@@ -56,6 +56,19 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rope_cos, const float *rope_sin, const int *pos,
                  int B, float *q, void *kc, void *vc, int kv_f32, int max_seq);
 
+/* lmk_qkv_rope and the attention of every (head, row) in one launch: the
+ * QKV work-groups hand q, k, v of the current position to the attention
+ * work-groups through tagged words (`tagged`: 4 * (NQ + 2 * NKV) 64-bit words,
+ * zero at allocation), tagged with *epoch * n_layers + layer + 1; the head
+ * outputs go to out[b, h*hd ..] (fp32).  A hand-off wait that gives up sets
+ * *err (the kernel still ends).  B <= 4, hd 64 or 128. */
+int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
+                 const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
+                 const float *rope_cos, const float *rope_sin, const int *pos, int B,
+                 void *kc, void *vc, int kv_f32, int max_seq, int H,
+                 unsigned long long *tagged, const unsigned *epoch, int layer,
+                 int n_layers, int *err, float *out);
+
 /* Causal attention, one work-group per (head, row): out[b, h*hd ..] =
  * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V over cache slot slot[b] (slot
  * NULL: slot b).  Serves decode rows and prefill rows alike. */
@@ -85,9 +98,10 @@ int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
 
 /* Reduce the argmax partials of each row b: tok[b] = argmax; when hist != NULL,
  * hist[b*hist_stride + pos[b] + 1] = tok[b] and pos[b] += 1 (device-resident
- * greedy loop state). */
+ * greedy loop state); with epoch, *epoch += 1 (the decode-step count that tags
+ * lmk_qkv_attn's hand-off words). */
 int lmk_argmax_final(hipStream_t s, const LMArgPart *part, int nblk, int B,
-                     int *tok, int *pos, int *hist, int hist_stride);
+                     int *tok, int *pos, int *hist, int hist_stride, unsigned *epoch);
 
 /* ---- prefill attention (k_attn.hip) ----------------------------------------
  * Rows come in nseq whole sequences of S consecutive rows (consecutive

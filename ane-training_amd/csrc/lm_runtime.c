@@ -61,6 +61,13 @@ struct LMModel {
     int *d_rtok, *d_rpos, *d_rslot;   /* prefill rows: token, position, slot */
     /* per-slot greedy state */
     int *d_tok, *d_pos, *d_hist, *d_slot_id;
+    /* batch 1-4 chain: QKV and attention in one launch (fuse_qa), handing q, k,
+     * v over through tagged words; the decode-step count that tags them; the
+     * flag a hand-off wait that gives up sets */
+    int fuse_qa;
+    unsigned long long *d_tagged;
+    unsigned *d_epoch;
+    int *d_err;
     /* pinned host staging */
     float *h_logits;
     int *h_io;
@@ -469,6 +476,14 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
+    const size_t ntag = (size_t)MAX_GEMV_B * (NQ + 2 * NKV);
+    if ((st = dev_alloc((void **)&m->d_tagged, ntag * 8))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_epoch, 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
+    if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_epoch, 0, 4) != hipSuccess ||
+        hipMemset(m->d_err, 0, 4) != hipSuccess)
+        FAIL(LM_ERR_HIP);
+    m->fuse_qa = 1;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
 
@@ -555,7 +570,7 @@ void lm_free(LMModel *m)
     free_rows(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id};
+                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_tagged, m->d_epoch, m->d_err};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_logits) hipHostFree(m->h_logits);
@@ -579,6 +594,12 @@ int lm_set_option(LMModel *m, int option, int value)
     switch (option) {
     case LM_OPT_USE_GRAPH:
         m->use_graph = value ? 1 : 0;
+        return LM_OK;
+    case LM_OPT_FUSE_QKV_ATTN:
+        if ((value ? 1 : 0) == m->fuse_qa) return LM_OK;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        drop_graphs(m);
+        m->fuse_qa = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_KV_F32:
         if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
@@ -615,14 +636,22 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
     void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
     switch (fam) {
     case LM_KERN_QKV:
-        KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
-                          m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
-                          m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
-                          m->max_seq));
+        if (m->fuse_qa)   /* with the attention of every head */
+            KCHK(lmk_qkv_attn(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
+                              m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
+                              m->d_rope_cos, m->d_rope_sin, m->d_pos, B, kc, vc, m->kv_f32,
+                              m->max_seq, m->H, m->d_tagged, m->d_epoch, l, m->L, m->d_err,
+                              m->d_attn));
+        else
+            KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
+                              m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
+                              m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
+                              m->max_seq));
         break;
-    case LM_KERN_ATTN:
-        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
-                             m->hd, m->max_seq, m->d_attn, NULL));
+    case LM_KERN_ATTN:   /* none when fused into the QKV launch */
+        if (!m->fuse_qa)
+            KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
+                                 m->hd, m->max_seq, m->d_attn, NULL));
         break;
     case LM_KERN_WO:
         KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
@@ -638,7 +667,7 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
         break;
     case LM_KERN_ARGMAX:
         KCHK(lmk_argmax_final(s, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
-                              m->max_seq + 1));
+                              m->max_seq + 1, m->d_epoch));
         break;
     default:
         return LM_ERR_INVALID;
@@ -789,7 +818,7 @@ static int enqueue_decode_gemm(LMModel *m, int B, float *logits)
     int rc = enqueue_rows(m, B, 1, m->d_tok, m->d_pos, m->d_slot_id, logits, 1);
     if (rc) return rc;
     KCHK(lmk_argmax_final(m->stream, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
-                          m->max_seq + 1));
+                          m->max_seq + 1, NULL));
     return LM_OK;
 }
 
@@ -838,6 +867,26 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
 
 static int run_decode_step(LMModel *m, int B) { return run_decode_steps(m, B, 1); }
 
+/* The hand-off flag of the fused QKV + attention launches: queued to the host
+ * with the results of a call, checked once the stream has synchronised. */
+static int *err_slot(LMModel *m) { return m->h_io + 4 * (size_t)m->max_batch; }
+
+static int queue_err_read(LMModel *m)
+{
+    return hipMemcpyAsync(err_slot(m), m->d_err, 4, hipMemcpyDeviceToHost, m->stream) == hipSuccess
+               ? LM_OK
+               : LM_ERR_HIP;
+}
+
+static int check_err(LMModel *m)
+{
+    if (!*err_slot(m)) return LM_OK;
+    fprintf(stderr, "stories_lm: a QKV -> attention hand-off wait gave up (results invalid)\n");
+    *err_slot(m) = 0;
+    HIPCHK(hipMemset(m->d_err, 0, 4));
+    return LM_ERR_HIP;
+}
+
 static int check_tok_pos(const LMModel *m, const int *tokens, const int *pos, int B)
 {
     for (int b = 0; b < B; b++) {
@@ -870,7 +919,9 @@ int lm_forward_batch(LMModel *m, const int *tokens, const int *pos, int B, float
     if (logits)
         HIPCHK(hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)B * m->V * 4,
                               hipMemcpyDeviceToHost, m->stream));
+    if ((rc = queue_err_read(m))) return rc;
     HIPCHK(hipStreamSynchronize(m->stream));
+    if ((rc = check_err(m))) return rc;
     if (argmax) memcpy(argmax, hio + 2 * B, B * 4);
     if (logits) memcpy(logits, m->h_logits, (size_t)B * m->V * 4);
     return LM_OK;
@@ -892,10 +943,11 @@ const float *lm_forward(LMModel *m, int token, int pos)
     if (run_decode_step(m, 1)) return NULL;
     if (hipMemcpyAsync(m->h_logits, m->d_logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
                        m->stream) != hipSuccess ||
-        hipStreamSynchronize(m->stream) != hipSuccess) {
+        queue_err_read(m) != LM_OK || hipStreamSynchronize(m->stream) != hipSuccess) {
         fprintf(stderr, "stories_lm: lm_forward: HIP error\n");
         return NULL;
     }
+    if (check_err(m)) return NULL;
     return m->h_logits;
 }
 
@@ -927,11 +979,17 @@ int lm_generate_greedy(LMModel *m, int B, const int *first_tokens, const int *po
     int *h = (int *)malloc((size_t)B * stride * 4);
     if (!h) return LM_ERR_OOM;
     hipError_t e = hipMemcpyAsync(h, m->d_hist, (size_t)B * stride * 4, hipMemcpyDeviceToHost, m->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(err_slot(m), m->d_err, 4, hipMemcpyDeviceToHost, m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) {
         free(h);
         fprintf(stderr, "stories_lm: lm_generate_greedy: %s\n", hipGetErrorString(e));
         return LM_ERR_HIP;
+    }
+    if ((rc = check_err(m))) {
+        free(h);
+        return rc;
     }
     for (int t = 0; t < n_steps; t++)
         for (int b = 0; b < B; b++) out_tokens[(size_t)t * B + b] = h[b * stride + pos0[b] + 1 + t];
@@ -1145,6 +1203,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
         int k = 0;
         for (int l = 0; l < m->L && rc == LM_OK; l++)
             for (int f = 0; f < 5 && rc == LM_OK; f++) {
+                if (fams[f] == LM_KERN_ATTN && m->fuse_qa) continue;   /* inside the QKV launch */
                 kfam[k] = fams[f];
                 lmk_time_next(ev[2 * k], ev[2 * k + 1]);
                 rc = enqueue_kernel(m, B, fams[f], l, NULL);
@@ -1167,7 +1226,9 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
-            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1 : m->L;
+            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX
+                                       ? 1
+                                       : (f == LM_KERN_ATTN && m->fuse_qa ? 0 : m->L);
     }
     for (int i = 0; ev && i < 2 * nk; i++)
         if (ev[i]) hipEventDestroy(ev[i]);

@@ -296,6 +296,8 @@ def main():
     ap.add_argument("--steps", type=int, default=32, help="timed 256-token C0 sequences")
     ap.add_argument("--warmup", type=int, default=2, help="untimed 256-token C0 sequences")
     ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="launch the decode attention apart from the QKV GEMV (A/B)")
     ap.add_argument("--kv16", action="store_true",
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
@@ -327,6 +329,8 @@ def main():
         m.set_option(S.LM_OPT_KV_F32, 1)
     if args.direct:
         m.set_option(S.LM_OPT_USE_GRAPH, 0)
+    if args.no_fuse:
+        m.set_option(S.LM_OPT_FUSE_QKV_ATTN, 0)
 
     for _ in range(args.warmup):
         m.generate_greedy([1], [0], SEQ)
@@ -353,8 +357,10 @@ def main():
         # kernel timed by hipEvents at its own dispatch's start and end
         us, launches = m.profile_chain([1], [0], SEQ - 2)
     m.close()
-    if launches is None:   # the chain's launch counts: one per layer, classifier and argmax once
-        launches = {k: (1 if k in ("cls", "argmax") else cfg.n_layers) for k in algo}
+    if launches is None:   # the chain's launch counts: one per layer (attention inside the
+        # QKV launch), classifier and argmax once
+        launches = {k: (1 if k in ("cls", "argmax") else 0 if k == "attn" else cfg.n_layers)
+                    for k in algo}
     step_bytes = sum(algo[k] * launches[k] for k in algo)
     step_gbs = step_bytes / (us_tok * 1e-6) / 1e9
     out = {
@@ -376,15 +382,19 @@ def main():
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1),
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
     }
+    if launches.get("attn") == 0:   # attention runs inside the QKV launch
+        algo["qkv"] += algo.pop("attn")
+        launches.pop("attn")
     if chain_timing:
-        dom = "attn"   # largest in the kernel trace; event times cannot rank the layer kernels
+        # the fused QKV + attention launch is the largest kernel of the step
+        dom = "qkv" if "attn" not in algo else "attn"
         dur_us = us[dom]
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
         out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                            "traffic": None, "bytes_per_launch": int(algo[dom]),
                            "launch_us": round(dur_us, 3)}
-        out["kernel_us_per_launch"] = {k: round(v, 3) for k, v in us.items()}
+        out["kernel_us_per_launch"] = {k: round(v, 3) for k, v in us.items() if launches.get(k)}
     if not args.no_extra:
         out["configs"] = bench_extra(S, w16, direct=args.direct)
         ra = reference_algorithm_gpu(S, cfg, w16, ids)

@@ -205,11 +205,14 @@ LONG_HD128 = dict(dim=512, hidden_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2,
 
 @pytest.mark.parametrize("name,d", [("hd64", LONG_HD64), ("hd128", LONG_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-def test_long_context_decode_chain(lm, orc, name, d, kv):
-    """620 steps of the B=1 decode chain (k_attn_decode over up to 620 cached
-    positions, GQA) against the reference forward at every step."""
-    _say(f"[long decode chain {name} kv{kv}]")
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_long_context_decode_chain(lm, orc, name, d, kv, fuse):
+    """620 steps of the B=1 decode chain (the attention over up to 620 cached
+    positions, GQA, in the QKV launch or its own) against the reference
+    forward at every step."""
+    _say(f"[long decode chain {name} kv{kv} fuse{fuse}]")
     m, w32 = make(lm, d, 61, 1, 640, kv == 32)
+    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     toks = np.random.default_rng(61).integers(0, d["vocab_size"], LONG).astype(np.int32)
     got = np.stack([m.forward(int(t), p) for p, t in enumerate(toks)])
     m.close()

@@ -46,10 +46,13 @@ def test_dpp_wave_reductions(lm):
 
 @pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-def test_tiny_decode_steps_match_oracle(lm, name, d, kv):
-    _say(f"[tiny decode {name} kv{kv}]")
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_tiny_decode_steps_match_oracle(lm, name, d, kv, fuse):
+    """fuse: QKV and attention in one launch (tagged hand-off words) or two."""
+    _say(f"[tiny decode {name} kv{kv} fuse{fuse}]")
     fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
+    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     got = np.stack([m.forward(int(t), p) for p, t in enumerate(fx["tokens"])])
     np.testing.assert_allclose(got, fx[f"logits_kv{kv}"], **TIGHT)
     np.testing.assert_allclose(got, fx["logits_kv32"], **NORTH_STAR)
@@ -59,13 +62,15 @@ def test_tiny_decode_steps_match_oracle(lm, name, d, kv):
 
 
 @pytest.mark.parametrize("B", [2, 3, 4])
-def test_tiny_batch_decode_matches_oracle(lm, orc, B):
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_tiny_batch_decode_matches_oracle(lm, orc, B, fuse):
     """B slots in one batched step, first in lock-step, then at different
     positions (slot b advances every b+1 steps; a repeated (token, pos) step
     rewrites the same cache entry)."""
-    _say(f"[tiny batch decode B={B}]")
+    _say(f"[tiny batch decode B={B} fuse{fuse}]")
     d = TINY
     m, w16 = make(lm, d, 21, B, 64, True)
+    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     w32 = lm.f16_to_f32(w16)
     seqs = np.random.default_rng(B).integers(0, d["vocab_size"], (B, 40)).astype(np.int32)
     orcs = [orc.Oracle(cfg7(d), w32, True, 64) for _ in range(B)]
@@ -184,16 +189,18 @@ def test_graph_replay_equals_direct_launches(lm):
     m2.close()
 
 
-def test_profile_chain_times_every_family(lm):
+@pytest.mark.parametrize("fuse", [1, 0])
+def test_profile_chain_times_every_family(lm, fuse):
     """lm_profile_chain: every kernel of real decode steps timed at its own
     dispatch; positive durations, the launch counts of a step, and the range
     check on the positions it advances through."""
-    _say("[profile chain]")
+    _say(f"[profile chain fuse{fuse}]")
     d = TINY
     m, _ = make(lm, d, 25, 1, 64, True)
+    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     us, n = m.profile_chain([1], [20], 6)
     L = d["n_layers"]
-    assert n == {"qkv": L, "attn": L, "wo": L, "w13": L, "w2": L, "cls": 1, "argmax": 1}
+    assert n == {"qkv": L, "attn": 0 if fuse else L, "wo": L, "w13": L, "w2": L, "cls": 1, "argmax": 1}
     for k in us:
         assert (us[k] > 0) == (n[k] > 0), k
         assert us[k] < 1e4, k
