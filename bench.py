@@ -282,6 +282,27 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
     return out
 
 
+def calibration_copy(mbytes):
+    """One device-to-device copy of mbytes MiB (hipMemcpy, the runtime's copy
+    kernel): the known-size reference that scales rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters to bytes."""
+    import ctypes
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    hip = ctypes.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    n = int(mbytes) << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), n) or hip.hipMalloc(ctypes.byref(b), n):
+        raise SystemExit("calibration copy: hipMalloc failed")
+    rc = hip.hipMemset(a, 0, ctypes.c_size_t(n)) or hip.hipMemcpy(b, a, n, 3) or hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    if rc:
+        raise SystemExit("calibration copy failed")
+
+
 def under_profiler():
     """True inside rocprofv3 (its preloaded tool library and ROCPROF* variables):
     event-bracketed dispatches (lm_profile_chain) are then not used."""
@@ -305,6 +326,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip configs C1-C4")
     ap.add_argument("--no-chain-timing", action="store_true",
                     help="skip the per-kernel event timing (automatic under a profiler)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="first copy this many MiB device to device (counter calibration)")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"],
                     help="run just this config of C1-C4 (for profiling) and print its entry")
     args = ap.parse_args()
@@ -319,6 +342,8 @@ def main():
     rc = S.init()
     if rc:
         raise SystemExit(f"lm_init: {S.strerror(rc)}")
+    if args.calib_copy_mb:
+        calibration_copy(args.calib_copy_mb)
     cfg = S.make_config(**S.STORIES_110M)
     w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
     if args.only:
