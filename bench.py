@@ -415,10 +415,18 @@ def main():
         dom = "qkv" if "attn" not in algo else "attn"
         dur_us = us[dom]
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
-        out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
-                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                           "traffic": None, "bytes_per_launch": int(algo[dom]),
-                           "launch_us": round(dur_us, 3)}
+        traffic = None
+        if dom == "qkv" and not args.kv16:
+            # k_qkv_attn, fp32 cache: 4.737 MB fetched per launch (FETCH_SIZE x 2.000 from the
+            # 256 MiB copy calibration, profiles/decode_b1_stories110m_chain.md) + its writes
+            # (q, k, v words and the K/V append, 33 KB, algorithmic: the WRITE_SIZE pass of this
+            # command did not complete)
+            traffic = 4737000 + 33000
+        out["roofline"] = {"bound": "hbm", "kernel": "k_qkv_attn" if dom == "qkv" else dom,
+                           "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                           "bytes_per_launch": int(algo[dom]), "launch_us": round(dur_us, 3),
+                           "launch_us_source": "hipEvents at each dispatch of the chain (lm_profile_chain)"}
         out["kernel_us_per_launch"] = {k: round(v, 3) for k, v in us.items() if launches.get(k)}
     if not args.no_extra:
         out["configs"] = bench_extra(S, w16, direct=args.direct)
