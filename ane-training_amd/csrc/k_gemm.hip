@@ -1026,6 +1026,13 @@ extern "C" int lmk_pick_split(int M, int N, int K)
         best = ns;
         if (K / ns <= 512) break;
     }
+    if (M <= 64) {
+        /* decode rows: more splits (k-chunks of at least 128) until the grid
+         * holds a work-group per CU */
+        const long tiles = (N + 63) / 64;
+        for (int ns = best + 1; ns <= cap && tiles * best < 256; ns++)
+            if (K % (BKH * ns) == 0 && K / ns >= 128) best = ns;
+    }
     return best;
 }
 
