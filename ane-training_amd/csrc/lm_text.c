@@ -198,6 +198,31 @@ double lm_rng_next(LMRng *r)
     return (double)r->x / 281474976710656.0;   /* 2^48 */
 }
 
+/* ---- loss -------------------------------------------------------------------- */
+
+/* Mean next-token cross-entropy of S logit rows (training/forward.h:174-183):
+ * for t < S-1, -(logits[t, tokens[t+1]] - max_t - log(sum_i exp(logits[t, i] -
+ * max_t))), averaged over S-1; sums in the reference's order, in fp32. */
+int lm_mean_ce(const float *logits, const int *tokens, int S, int V, float *loss)
+{
+    if (!logits || !tokens || !loss || S < 2 || V < 1) return LM_ERR_INVALID;
+    for (int t = 1; t < S; t++)
+        if (tokens[t] < 0 || tokens[t] >= V) return LM_ERR_RANGE;
+    float total = 0.f;
+    for (int t = 0; t < S - 1; t++) {
+        const float *row = logits + (size_t)t * V;
+        float mx = -1e9f;
+        for (int i = 0; i < V; i++)
+            if (row[i] > mx) mx = row[i];
+        float sm = 0.f;
+        for (int i = 0; i < V; i++) sm += expf(row[i] - mx);
+        const float log_prob = row[tokens[t + 1]] - mx - logf(sm);
+        total -= log_prob;
+    }
+    *loss = total / (S - 1);
+    return LM_OK;
+}
+
 /* ---- samplers --------------------------------------------------------------- */
 
 int lm_sample_argmax(const float *logits, int n)

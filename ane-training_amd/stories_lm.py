@@ -181,6 +181,17 @@ class Tokenizer:
         return out[:n].tolist()
 
 
+def mean_ce(logits, tokens) -> float:
+    """Mean next-token cross-entropy of [S, V] logit rows (training/forward.h:174-183)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    out = C.c_float(0.0)
+    rc = lib().lm_mean_ce(_fp(lg), _ip(t), t.size, lg.shape[-1], C.byref(out))
+    if rc:
+        raise LMError(rc, "lm_mean_ce")
+    return float(out.value)
+
+
 def sample_argmax(logits) -> int:
     x = np.ascontiguousarray(logits, dtype=np.float32)
     return lib().lm_sample_argmax(_fp(x), x.size)
@@ -263,6 +274,7 @@ def lib():
         "lm_rng_seed": (None, [C.POINTER(Rng), C.c_uint64]),
         "lm_rng_next": (C.c_double, [C.POINTER(Rng)]),
         "lm_sample_argmax": (I, [fp, I]),
+        "lm_mean_ce": (I, [fp, ip, I, I, fp]),
         "lm_sample_temperature": (I, [fp, I, F, C.POINTER(Rng)]),
         "lm_sample_topp": (I, [fp, I, F, F, C.POINTER(Rng)]),
         "lm_load_blzt": (P, [C.c_char_p, I, I, ip]),

@@ -386,6 +386,12 @@ typedef struct { uint64_t x; } LMRng;
 void lm_rng_seed(LMRng *r, uint64_t seed);
 double lm_rng_next(LMRng *r);
 
+/* Mean next-token cross-entropy over S logit rows [S, V] (host, e.g. from
+ * lm_prefill): *loss = -(1/(S-1)) sum_{t<S-1} log softmax(logits[t])[tokens[t+1]],
+ * with the reference's arithmetic (model_forward's loss, training/forward.h:
+ * 174-183).  LM_ERR_INVALID for S < 2, LM_ERR_RANGE for a token outside [0, V). */
+int lm_mean_ce(const float *logits, const int *tokens, int S, int V, float *loss);
+
 /* Samplers over n host logits (generate.m:129-209): argmax (lowest index on
  * ties); temperature softmax then one draw; nucleus (top-p) over the
  * temperature softmax.  Return the token, or a negative status. */

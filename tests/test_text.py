@@ -251,3 +251,25 @@ def test_samplers_draw_for_draw_against_reference(n, vectors, draws):
         got_p = [S.sample_topp(logits, temp, topp, r) for _ in range(draws)]
         assert got_t == want_t, (n, v)
         assert got_p == want_p, (n, v)
+
+
+def test_mean_ce_matches_reference_loss(orc):
+    """lm_mean_ce (model_forward's loss, training/forward.h:174-183) equals the
+    oracle's restatement bit for bit, and the closed forms: uniform logits give
+    log V; a row that puts all mass on the next token gives 0."""
+    rng = np.random.default_rng(3)
+    S_, V = 17, 300
+    logits = (rng.standard_normal((S_, V)) * 3).astype(np.float32)
+    toks = rng.integers(0, V, S_).astype(np.int32)
+    assert S.mean_ce(logits, toks) == orc.loss(logits, toks)
+    assert abs(S.mean_ce(np.zeros((5, V), np.float32), toks[:5]) - np.log(V)) < 1e-5
+    peaked = np.full((4, V), -1e4, np.float32)
+    for t in range(3):
+        peaked[t, toks[t + 1]] = 0.0
+    assert abs(S.mean_ce(peaked, toks[:4])) < 1e-6
+    with pytest.raises(S.LMError):
+        S.mean_ce(logits[:1], toks[:1])
+    bad = toks.copy()
+    bad[3] = V
+    with pytest.raises(S.LMError):
+        S.mean_ce(logits, bad)
