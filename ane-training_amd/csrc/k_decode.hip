@@ -229,6 +229,7 @@ __device__ __forceinline__ void pair_reduce(const float acc[NB], float r0[NB], f
  * contents) and never repeated within 2^32 launches. */
 struct QkvTagged {
     unsigned long long *tq, *tk, *tv;
+    unsigned long long *ta;         /* head outputs [b*NQ + h*hd + d] (Wo in the launch) */
     const unsigned *epoch;
     int layer, n_layers;
     int *err;                       /* set when a hand-off wait gives up */
@@ -246,6 +247,57 @@ __device__ __forceinline__ void tag_store(unsigned long long *w, float v, unsign
     __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* Poll one tagged word until it carries `tag` (bounded: a wait that gives up
+ * sets *err and returns the word's value as it is).  A wait also stops early
+ * once *err is set, so that after one wait has given up the rest of the
+ * launch, and the launches queued behind it, end within microseconds; the
+ * host reads the flag after the step and reports the failure. */
+__device__ __forceinline__ float tag_wait(const unsigned long long *w, unsigned tag, int *err)
+{
+    unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int spin = 0; (unsigned)(v >> 32) != tag; spin++) {
+        if ((spin & 255) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            break;
+        if (spin == (1 << 20)) {
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return __builtin_bit_cast(float, (unsigned)v);
+}
+
+__device__ __forceinline__ unsigned long long tag_peek(const unsigned long long *w)
+{
+    return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* The value of a word already read as v, or, when v carries another tag, of
+ * the wait on it: a thread reads all its words first and waits only on those
+ * not yet written, so its reads overlap instead of following one another. */
+__device__ __forceinline__ float tag_take(unsigned long long v, const unsigned long long *w,
+                                          unsigned tag, int *err)
+{
+    return (unsigned)(v >> 32) == tag ? __builtin_bit_cast(float, (unsigned)v) : tag_wait(w, tag, err);
+}
+
+/* dst[i] = value of w[i] for i < n, this work-group's threads taking
+ * i = threadIdx.x + j * WG, eight reads in flight per thread. */
+__device__ __forceinline__ void tag_wait_span(const unsigned long long *w, int n, unsigned tag,
+                                              int *err, float *dst)
+{
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * WG) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            v[j] = i0 + j * WG < n ? tag_peek(w + i0 + j * WG) : 0ull;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (i0 + j * WG < n) dst[i0 + j * WG] = tag_take(v[j], w + i0 + j * WG, tag, err);
+    }
+}
+
 /* Rows of [Wq; Wk; Wv] . rmsnorm(x[b]) for the row pairs of this work-group,
  * RoPE'd and stored (q fp32, k/v into the cache); with tg, also as tagged
  * hand-off words. */
@@ -255,7 +307,7 @@ __device__ __forceinline__ void qkv_rows(
     const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV, int hd,
     const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
     int B, float *__restrict__ q, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq,
-    int npairs, const QkvTagged *tg)
+    int npairs, const QkvTagged *tg, bool store_x = true)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
@@ -278,7 +330,7 @@ __device__ __forceinline__ void qkv_rows(
         cr[b] = rot ? rc[ti] : 1.f;
         sr[b] = rot ? rs[ti] : 0.f;
     }
-    norm_to_lds<D, NB>(in, B, x, emb != nullptr, xs);
+    norm_to_lds<D, NB>(in, B, x, emb != nullptr && store_x, xs);
     if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
@@ -498,21 +550,20 @@ __device__ __forceinline__ void attn_head(
          * that gives up sets qt->err, and the kernel still ends) */
         const unsigned tag = qkv_tag(*qt);
         const int g = small_div(h, small_div(H, Hkv));
-        for (int t = threadIdx.x; t < 3 * HD; t += WG) {
-            const int vec = t / HD, e = t % HD;
-            const unsigned long long *w =
-                vec == 0 ? qt->tq + (size_t)b * H * HD + h * HD + e
-                         : (vec == 1 ? qt->tk : qt->tv) + (size_t)b * Hkv * HD + g * HD + e;
-            unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int spin = 0; (unsigned)(v >> 32) != tag; spin++) {
-                if (spin == (1 << 20)) {
-                    __hip_atomic_store(qt->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            sqkv[vec][e] = __builtin_bit_cast(float, (unsigned)v);
+        constexpr int NT = (3 * HD + WG - 1) / WG;
+        const unsigned long long *wp[NT];
+        unsigned long long v[NT];
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int t = threadIdx.x + j * WG, vec = t / HD, e = t % HD;
+            wp[j] = vec == 0 ? qt->tq + (size_t)b * H * HD + h * HD + e
+                             : (vec == 1 ? qt->tk : qt->tv) + (size_t)b * Hkv * HD + g * HD + e;
+            v[j] = t < 3 * HD ? tag_peek(wp[j]) : 0ull;
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int t = threadIdx.x + j * WG;
+            if (t < 3 * HD) sqkv[t / HD][t % HD] = tag_take(v[j], wp[j], tag, qt->err);
         }
     }
     if (cur) {
@@ -697,24 +748,73 @@ __global__ void __launch_bounds__(WG) k_attn_decode_part(
  * output to out[b, h*HD ..] (fp32).  The attention work-groups come after every
  * QKV work-group in dispatch order and only wait for them, so the waits end
  * however many work-groups the device holds at once. */
-template <int D, int NB, typename KT, int HD>
+/* With Wo (WO): work-groups nprod + H*B .. then take the Wo GEMV + residual of
+ * k_wo_residual, a row pair per wave: their Wo rows are loaded at once, the
+ * head outputs arrive as tagged words from the attention work-groups (which
+ * then store no fp32 output), and x[b, r] += Wo[r, :] . attn[b].  In layer 0
+ * (emb) the residual starts from the embedding row and the QKV work-groups
+ * leave x alone, so each element of x has one writer in the launch. */
+template <int D, int NB, typename KT, int HD, bool WO>
 __global__ void __launch_bounds__(WG) k_qkv_attn(
     float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
     const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV,
     const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
     int B, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq, int npairs, int nprod, int H,
-    QkvTagged tg, float *__restrict__ out)
+    QkvTagged tg, float *__restrict__ out, const u16 *__restrict__ Wo)
 {
     if ((int)blockIdx.x < nprod) {
         qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, HD, rc, rs, pos, B, nullptr, kc, vc,
-                            max_seq, npairs, &tg);
+                            max_seq, npairs, &tg, !WO);
         return;
     }
-    __shared__ float oh[HD];
     const int a = blockIdx.x - nprod;
-    const int h = a % H, b = a / H;
-    attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
-    if ((int)threadIdx.x < HD) out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
+    if (!WO || a < H * B) {
+        __shared__ float oh[HD];
+        const int h = a % H, b = a / H;
+        attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
+        if ((int)threadIdx.x < HD) {
+            if constexpr (WO)
+                tag_store(tg.ta + (size_t)b * NQ + h * HD + threadIdx.x, oh[threadIdx.x], qkv_tag(tg));
+            else
+                out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
+        }
+        return;
+    }
+    if constexpr (WO) {
+        __shared__ __attribute__((aligned(16))) float xs[NB * D];
+        const int p = (a - H * B) * NWAVE + (threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
+        const int wpairs = D / 2;
+        const int r = 2 * min(p, wpairs - 1);
+        uint4 wv[D / 256];
+        hw_load<D>(Wo + (size_t)(r + half) * D, hl, wv);
+        float2 xo[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= B) {
+                xo[b] = make_float2(0.f, 0.f);
+            } else if (emb) {
+                const u16 *er = emb + (size_t)tok[b] * D + r;
+                xo[b] = make_float2(h2f(er[0]), h2f(er[1]));
+            } else {
+                xo[b] = *(const float2 *)(x + (size_t)b * D + r);
+            }
+        }
+        const unsigned tag = qkv_tag(tg);
+        tag_wait_span(tg.ta, B * D, tag, tg.err, xs);
+        __syncthreads();
+        if (p >= wpairs) return;
+        float acc[NB], r0[NB], r1[NB];
+        hw_dot<D, NB>(wv, xs, hl, acc);
+        pair_reduce<NB>(acc, r0, r1);
+        if (lane == 0) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                if (b >= B) break;
+                *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
+            }
+        }
+    }
 }
 
 /* ---- Wo + residual ---------------------------------------------------------- */
@@ -996,27 +1096,35 @@ extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const 
                             const float *rope_cos, const float *rope_sin, const int *pos, int B,
                             void *kc, void *vc, int kv_f32, int max_seq, int H,
                             unsigned long long *tagged, const unsigned *epoch, int layer,
-                            int n_layers, int *err, float *out)
+                            int n_layers, int *err, float *out, const uint16_t *wo)
 {
     if (B < 1 || B > 4 || NQ != D || H < 1 || NQ != H * hd || NKV % hd || H % (NKV / hd) ||
-        (emb && !tok) || !tagged || !epoch || !err || !out || (hd != 64 && hd != 128))
+        (emb && !tok) || !tagged || !epoch || !err || (!out && !wo) || (hd != 64 && hd != 128))
         return hipErrorInvalidValue;
     const int npairs = (NQ + 2 * NKV) / 2;
     const int nprod = (npairs + NWAVE - 1) / NWAVE;
-    dim3 grid(nprod + H * B);
+    const int nwo = wo ? (D / 2 + NWAVE - 1) / NWAVE : 0;
+    dim3 grid(nprod + H * B + nwo);
     const QkvTagged tg = {tagged, tagged + (size_t)MAX_TAG_B * NQ,
-                          tagged + (size_t)MAX_TAG_B * (NQ + NKV), epoch, layer, n_layers, err};
-#define LAUNCH_QA(HD_, KT_)                                                                        \
-    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv, NQ,   \
-            NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H, tg,  \
-            out)
+                          tagged + (size_t)MAX_TAG_B * (NQ + NKV),
+                          tagged + (size_t)MAX_TAG_B * (NQ + 2 * NKV), epoch, layer, n_layers, err};
+#define LAUNCH_QA(HD_, KT_, WO_)                                                                   \
+    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv,  \
+            NQ, NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H,  \
+            tg, out, (const u16 *)wo)
+#define LAUNCH_QA2(HD_, KT_)                  \
+    do {                                      \
+        if (wo) LAUNCH_QA(HD_, KT_, true);    \
+        else LAUNCH_QA(HD_, KT_, false);      \
+    } while (0)
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        if (hd == 64 && kv_f32) LAUNCH_QA(64, float);
-        else if (hd == 64) LAUNCH_QA(64, u16);
-        else if (kv_f32) LAUNCH_QA(128, float);
-        else LAUNCH_QA(128, u16);
+        if (hd == 64 && kv_f32) LAUNCH_QA2(64, float);
+        else if (hd == 64) LAUNCH_QA2(64, u16);
+        else if (kv_f32) LAUNCH_QA2(128, float);
+        else LAUNCH_QA2(128, u16);
     }));
+#undef LAUNCH_QA2
 #undef LAUNCH_QA
     return hipGetLastError();
 }

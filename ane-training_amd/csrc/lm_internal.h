@@ -58,16 +58,18 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 
 /* lmk_qkv_rope and the attention of every (head, row) in one launch: the
  * QKV work-groups hand q, k, v of the current position to the attention
- * work-groups through tagged words (`tagged`: 4 * (NQ + 2 * NKV) 64-bit words,
- * zero at allocation), tagged with *epoch * n_layers + layer + 1; the head
- * outputs go to out[b, h*hd ..] (fp32).  A hand-off wait that gives up sets
- * *err (the kernel still ends).  B <= 4, hd 64 or 128. */
+ * work-groups through tagged words (`tagged`: 4 * (2 * NQ + 2 * NKV) 64-bit
+ * words, zero at allocation), tagged with *epoch * n_layers + layer + 1; the
+ * head outputs go to out[b, h*hd ..] (fp32), or, with wo (the layer's Wo [D,
+ * NQ]), on through tagged words to Wo work-groups in the same launch that add
+ * Wo . attn to x (lmk_wo_residual's work; out unused).  A hand-off wait that
+ * gives up sets *err (the kernel still ends).  B <= 4, hd 64 or 128. */
 int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                  const float *rope_cos, const float *rope_sin, const int *pos, int B,
                  void *kc, void *vc, int kv_f32, int max_seq, int H,
                  unsigned long long *tagged, const unsigned *epoch, int layer,
-                 int n_layers, int *err, float *out);
+                 int n_layers, int *err, float *out, const uint16_t *wo);
 
 /* Causal attention, one work-group per (head, row): out[b, h*hd ..] =
  * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V over cache slot slot[b] (slot

@@ -41,8 +41,19 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # Published reference figure for this metric: Stories-110M B=1 greedy decode on
 # the ANE (libane, fp16), M3 Pro: 41.7 tok/s (full 256-window recompute).
+LIB_FUSE_DEFAULT = 2     # LM_OPT_FUSE_QKV_ATTN after lm_load / lm_create
 REF_TOK_S = 41.7
 SEQ = 256
+
+
+def qkv_launch_writes(cfg, kvb, with_wo):
+    """Bytes the fused QKV launch writes for one row: the q, k, v hand-off words
+    (8 bytes each) and the K/V append; then either the fp32 head outputs, or
+    (with Wo inside) the head-output words and the updated residual row."""
+    hd = cfg.dim // cfg.n_heads
+    nq, nkv = cfg.dim, cfg.n_kv_heads * hd
+    w = 8 * (nq + 2 * nkv) + 2 * nkv * kvb
+    return w + (8 * nq + 4 * cfg.dim if with_wo else 4 * nq)
 
 
 def algorithmic_bytes(cfg, B, mean_ctx, kv_bytes=2, logits=False):
@@ -317,8 +328,8 @@ def main():
     ap.add_argument("--steps", type=int, default=32, help="timed 256-token C0 sequences")
     ap.add_argument("--warmup", type=int, default=2, help="untimed 256-token C0 sequences")
     ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
-    ap.add_argument("--no-fuse", action="store_true",
-                    help="launch the decode attention apart from the QKV GEMV (A/B)")
+    ap.add_argument("--fuse", type=int, choices=[0, 1, 2], default=None,
+                    help="LM_OPT_FUSE_QKV_ATTN for the C0 chain (A/B; default: the library's)")
     ap.add_argument("--kv16", action="store_true",
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
@@ -354,8 +365,8 @@ def main():
         m.set_option(S.LM_OPT_KV_F32, 1)
     if args.direct:
         m.set_option(S.LM_OPT_USE_GRAPH, 0)
-    if args.no_fuse:
-        m.set_option(S.LM_OPT_FUSE_QKV_ATTN, 0)
+    if args.fuse is not None:
+        m.set_option(S.LM_OPT_FUSE_QKV_ATTN, args.fuse)
 
     for _ in range(args.warmup):
         m.generate_greedy([1], [0], SEQ)
@@ -382,10 +393,16 @@ def main():
         # kernel timed by hipEvents at its own dispatch's start and end
         us, launches = m.profile_chain([1], [0], SEQ - 2)
     m.close()
-    if launches is None:   # the chain's launch counts: one per layer (attention inside the
-        # QKV launch), classifier and argmax once
-        launches = {k: (1 if k in ("cls", "argmax") else 0 if k == "attn" else cfg.n_layers)
+    if launches is None:   # the chain's launch counts: one per layer, attention (and Wo at
+        # level 2) inside the QKV launch, classifier and argmax once
+        fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
+        inside = {"attn": fz >= 1, "wo": fz == 2}
+        launches = {k: (1 if k in ("cls", "argmax") else 0 if inside.get(k) else cfg.n_layers)
                     for k in algo}
+    for k in ("attn", "wo"):        # families that run inside the QKV launch
+        if launches.get(k) == 0:
+            algo["qkv"] += algo.pop(k)
+            launches.pop(k)
     step_bytes = sum(algo[k] * launches[k] for k in algo)
     step_gbs = step_bytes / (us_tok * 1e-6) / 1e9
     out = {
@@ -407,9 +424,6 @@ def main():
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1),
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
     }
-    if launches.get("attn") == 0:   # attention runs inside the QKV launch
-        algo["qkv"] += algo.pop("attn")
-        launches.pop("attn")
     if chain_timing:
         # the fused QKV + attention launch is the largest kernel of the step
         dom = "qkv" if "attn" not in algo else "attn"
@@ -417,11 +431,12 @@ def main():
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
         traffic = None
         if dom == "qkv" and not args.kv16:
-            # k_qkv_attn, fp32 cache: 4.737 MB fetched per launch (FETCH_SIZE x 2.000 from the
-            # 256 MiB copy calibration, profiles/decode_b1_stories110m_chain.md) + its writes
-            # (q, k, v words and the K/V append, 33 KB, algorithmic: the WRITE_SIZE pass of this
-            # command did not complete)
-            traffic = 4737000 + 33000
+            # fp32 cache, from FETCH_SIZE (x 2.000, the 256 MiB copy calibration) with QKV +
+            # attention fused and Wo launched apart (profiles/decode_b1_stories110m_chain.md):
+            # 4.737 MB per k_qkv_attn launch, 1.234 MB per k_wo_residual launch (their sum
+            # when Wo runs inside the launch too) + the launch's writes, taken as algorithmic
+            traffic = 4737000 + (1234000 if "wo" not in algo else 0) + qkv_launch_writes(
+                cfg, kvb, "wo" not in algo)
         out["roofline"] = {"bound": "hbm", "kernel": "k_qkv_attn" if dom == "qkv" else dom,
                            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

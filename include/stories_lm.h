@@ -242,10 +242,11 @@ int lm_timer_end(LMModel *m, float *ms);
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
-/* LM_OPT_FUSE_QKV_ATTN: 1 (default) runs the batch 1-4 chain's QKV GEMV and
- * the attention of every head as one launch per layer (the QKV work-groups
- * hand q, k, v to the attention work-groups through tagged words in memory);
- * 0 launches them separately. */
+/* LM_OPT_FUSE_QKV_ATTN: 2 (default) runs the batch 1-4 chain's QKV GEMV, the
+ * attention of every head and the Wo GEMV + residual as one launch per layer
+ * (the QKV work-groups hand q, k, v to the attention work-groups, and those
+ * the head outputs to the Wo work-groups, through tagged words in memory);
+ * 1 launches Wo apart; 0 launches each of the three apart. */
 #define LM_OPT_FUSE_QKV_ATTN 5
 int lm_set_option(LMModel *m, int option, int value);
 

@@ -205,7 +205,7 @@ LONG_HD128 = dict(dim=512, hidden_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2,
 
 @pytest.mark.parametrize("name,d", [("hd64", LONG_HD64), ("hd128", LONG_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-@pytest.mark.parametrize("fuse", [1, 0])
+@pytest.mark.parametrize("fuse", [2, 1, 0])
 def test_long_context_decode_chain(lm, orc, name, d, kv, fuse):
     """620 steps of the B=1 decode chain (the attention over up to 620 cached
     positions, GQA, in the QKV launch or its own) against the reference
