@@ -4,9 +4,11 @@
  * K-split QKV GEMM of 5..64 rows, k_attn_decode_part, which first sums q, k, v
  * from the GEMM's partials, rotates and appends them).
  *
- * One decode step of one layer is five launches, shaped after the reference's
+ * One decode step of one layer is five stages, shaped after the reference's
  * fused forward programs (training/training_dynamic/mil_dynamic.h:56-288) and
- * cut only where every output needs the whole of the previous vector:
+ * cut only where every output needs the whole of the previous vector.  They
+ * run as five launches, or (k_qkv_attn) as roles of the work-groups of one
+ * launch that hand their results on through tagged words in memory:
  *   qkv_rope   rmsnorm prologue (forward.h:46-53) + [Wq;Wk;Wv] GEMV
  *              (forward.h:122-124) + interleaved RoPE (forward.h:55-70) + KV
  *              append; layer 0 also gathers the embedding row (forward.h:108-110)
@@ -57,8 +59,6 @@ extern "C" void lmk_time_next(hipEvent_t start, hipEvent_t stop)
 
 #define WG 256
 #define NWAVE (WG / 64)
-/* rows of the tagged hand-off buffers (the batch 1-4 chain) */
-#define MAX_TAG_B 4
 
 /* ---- prologues ---------------------------------------------------------- */
 
@@ -229,7 +229,12 @@ __device__ __forceinline__ void pair_reduce(const float acc[NB], float r0[NB], f
  * contents) and never repeated within 2^32 launches. */
 struct QkvTagged {
     unsigned long long *tq, *tk, *tv;
-    unsigned long long *ta;         /* head outputs [b*NQ + h*hd + d] (Wo in the launch) */
+    unsigned long long *ta;         /* head outputs [b*NQ + h*hd + d] (Wo in the launch), in
+                                     * LM_TA_COPIES copies LM_TAG_B*NQ words apart */
+    unsigned long long *tx;         /* x after Wo [b*D + i] (FFN in the launch), in
+                                     * LM_TX_COPIES copies LM_TAG_B*D apart */
+    unsigned long long *tgt;        /* gate g [b*F + i] (FFN in the launch), copies
+                                     * LM_TAG_B*F apart */
     const unsigned *epoch;
     int layer, n_layers;
     int *err;                       /* set when a hand-off wait gives up */
@@ -262,7 +267,7 @@ __device__ __forceinline__ float tag_wait(const unsigned long long *w, unsigned 
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(LM_TAG_SLEEP);
         v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return __builtin_bit_cast(float, (unsigned)v);
@@ -280,6 +285,26 @@ __device__ __forceinline__ float tag_take(unsigned long long v, const unsigned l
                                           unsigned tag, int *err)
 {
     return (unsigned)(v >> 32) == tag ? __builtin_bit_cast(float, (unsigned)v) : tag_wait(w, tag, err);
+}
+
+/* Before a work-group reads a span of words: one thread polls the span's last
+ * word (most often the last written) while the others wait at the barrier, so
+ * that a waiting work-group keeps one poll in flight instead of one per
+ * thread.  A hint only: each word is still checked by its reader. */
+#ifndef LM_TAG_DOORBELL
+#define LM_TAG_DOORBELL 7
+#endif
+#ifndef LM_DOORBELL_SPREAD
+#define LM_DOORBELL_SPREAD 1
+#endif
+__device__ __forceinline__ void tag_doorbell(const unsigned long long *w, int n, int k, unsigned tag,
+                                             int *err)
+{
+    /* the k-th reader of a copy polls the last word of the k-th 128-byte line
+     * (wrapping), so that the readers of one copy poll different lines */
+    const int i = LM_DOORBELL_SPREAD ? (k * 16 + 15) % n : n - 1;
+    if (threadIdx.x == 0) (void)tag_wait(w + i, tag, err);
+    __syncthreads();
 }
 
 /* dst[i] = value of w[i] for i < n, this work-group's threads taking
@@ -741,78 +766,257 @@ __global__ void __launch_bounds__(WG) k_attn_decode_part(
 
 /* ---- QKV + attention in one launch (batch 1-4 decode) ----------------------- */
 
-/* Work-groups 0 .. nprod-1 are the QKV GEMV of k_qkv_rope (which also stores
- * q, k, v as tagged hand-off words); work-group nprod + b*H + h then runs the
- * attention of head h, row b: it loads its first cached K/V tile, waits for
- * the current position's q, k, v words of this launch, and writes the head
- * output to out[b, h*HD ..] (fp32).  The attention work-groups come after every
- * QKV work-group in dispatch order and only wait for them, so the waits end
- * however many work-groups the device holds at once. */
-/* With Wo (WO): work-groups nprod + H*B .. then take the Wo GEMV + residual of
- * k_wo_residual, a row pair per wave: their Wo rows are loaded at once, the
- * head outputs arrive as tagged words from the attention work-groups (which
- * then store no fp32 output), and x[b, r] += Wo[r, :] . attn[b].  In layer 0
- * (emb) the residual starts from the embedding row and the QKV work-groups
- * leave x alone, so each element of x has one writer in the launch. */
-template <int D, int NB, typename KT, int HD, bool WO>
-__global__ void __launch_bounds__(WG) k_qkv_attn(
-    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
-    const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV,
-    const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
-    int B, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq, int npairs, int nprod, int H,
-    QkvTagged tg, float *__restrict__ out, const u16 *__restrict__ Wo)
+/* Wo role of k_qkv_attn, work-group a of the role, a row pair per wave:
+ * x'[b, r..r+1] = (layer 0: the embedding row, else x) + Wo[r..r+1, :] . attn[b],
+ * the head outputs taken from copy a % LM_TA_COPIES of their tagged words.
+ * Without the FFN in the launch (F == 0) x' goes to x; with it, to every copy
+ * of the tagged words tx (x is then written by the W2 role). */
+template <int D, int NB, int F>
+__device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__restrict__ emb,
+                                        const int *__restrict__ tok, const u16 *__restrict__ Wo,
+                                        int B, int NQ, const QkvTagged &tg, int a, float *xs)
 {
-    if ((int)blockIdx.x < nprod) {
-        qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, HD, rc, rs, pos, B, nullptr, kc, vc,
-                            max_seq, npairs, &tg, !WO);
-        return;
-    }
-    const int a = blockIdx.x - nprod;
-    if (!WO || a < H * B) {
-        __shared__ float oh[HD];
-        const int h = a % H, b = a / H;
-        attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
-        if ((int)threadIdx.x < HD) {
-            if constexpr (WO)
-                tag_store(tg.ta + (size_t)b * NQ + h * HD + threadIdx.x, oh[threadIdx.x], qkv_tag(tg));
-            else
-                out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
-        }
-        return;
-    }
-    if constexpr (WO) {
-        __shared__ __attribute__((aligned(16))) float xs[NB * D];
-        const int p = (a - H * B) * NWAVE + (threadIdx.x >> 6);
-        const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
-        const int wpairs = D / 2;
-        const int r = 2 * min(p, wpairs - 1);
-        uint4 wv[D / 256];
-        hw_load<D>(Wo + (size_t)(r + half) * D, hl, wv);
-        float2 xo[NB];
+    const int p = a * NWAVE + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
+    const int wpairs = D / 2;
+    const int r = 2 * min(p, wpairs - 1);
+    uint4 wv[D / 256];
+    hw_load<D>(Wo + (size_t)(r + half) * D, hl, wv);
+    float2 xo[NB];
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if (b >= B) {
-                xo[b] = make_float2(0.f, 0.f);
-            } else if (emb) {
-                const u16 *er = emb + (size_t)tok[b] * D + r;
-                xo[b] = make_float2(h2f(er[0]), h2f(er[1]));
-            } else {
-                xo[b] = *(const float2 *)(x + (size_t)b * D + r);
-            }
+    for (int b = 0; b < NB; b++) {
+        if (b >= B) {
+            xo[b] = make_float2(0.f, 0.f);
+        } else if (emb) {
+            const u16 *er = emb + (size_t)tok[b] * D + r;
+            xo[b] = make_float2(h2f(er[0]), h2f(er[1]));
+        } else {
+            xo[b] = *(const float2 *)(x + (size_t)b * D + r);
         }
-        const unsigned tag = qkv_tag(tg);
-        tag_wait_span(tg.ta, B * D, tag, tg.err, xs);
-        __syncthreads();
-        if (p >= wpairs) return;
-        float acc[NB], r0[NB], r1[NB];
-        hw_dot<D, NB>(wv, xs, hl, acc);
-        pair_reduce<NB>(acc, r0, r1);
+    }
+    const unsigned tag = qkv_tag(tg);
+    const unsigned long long *tac = tg.ta + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * NQ;
+    if (LM_TAG_DOORBELL & 1) tag_doorbell(tac, B * D, a / LM_TA_COPIES, tag, tg.err);
+    tag_wait_span(tac, B * D, tag, tg.err, xs);
+    __syncthreads();
+    if (p >= wpairs) return;
+    float acc[NB], r0[NB], r1[NB];
+    hw_dot<D, NB>(wv, xs, hl, acc);
+    pair_reduce<NB>(acc, r0, r1);
+    if constexpr (F == 0) {
         if (lane == 0) {
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 if (b >= B) break;
                 *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
             }
+        }
+    } else if (lane < LM_TX_COPIES) {
+        unsigned long long *dst = tg.tx + (size_t)lane * LM_TAG_B * D + r;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= B) break;
+            tag_store(dst + (size_t)b * D, xo[b].x + r0[b], tag);
+            tag_store(dst + (size_t)b * D + 1, xo[b].y + r1[b], tag);
+        }
+    }
+}
+
+/* W1/W3 role of k_qkv_attn (the FFN in the launch), work-group a of the role,
+ * one hidden unit i per wave as in k_ffn13: x' from copy a % LM_TX_COPIES of
+ * its tagged words, normalised in LDS exactly as norm_to_lds does, then
+ * g[b, i] = silu(W1[i] . xn) * (W3[i] . xn) stored to every copy of the tagged
+ * words tgt.  (One unit per wave measured faster than two or four: more
+ * work-groups load the weights.) */
+template <int D, int NB, int F>
+__device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const u16 *__restrict__ W13,
+                                         int B, const QkvTagged &tg, int a, float *xs)
+{
+    constexpr int PER = D / WG;
+    __shared__ float red[NB][NWAVE];
+    const int tid = threadIdx.x, wv_ = tid >> 6;
+    const int i0 = a * NWAVE + wv_;
+    const int i = min(i0, F - 1);
+    const int lane = tid & 63, half = lane >> 5, hl = lane & 31;
+    constexpr int GB = LMK_GATE_BLOCK;
+    const size_t row = (size_t)(i / GB) * (2 * GB) + half * GB + (i % GB);
+    uint4 wv[D / 256];
+    hw_load<D>(W13 + row * D, hl, wv);
+    float w[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) w[j] = rms_w[tid + j * WG];
+    const unsigned tag = qkv_tag(tg);
+    /* each thread's words are the elements tid + j*WG of each row, which are
+     * also the ones it normalises: no barrier between the two */
+    const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D;
+    if (LM_TAG_DOORBELL & 2) tag_doorbell(txc, B * D, a / LM_TX_COPIES, tag, tg.err);
+    tag_wait_span(txc, B * D, tag, tg.err, xs);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float ss = 0.f;
+        if (b < B) {
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const float v = xs[b * D + tid + j * WG];
+                ss = fmaf(v, v, ss);
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[b][wv_] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < NWAVE; k++) tot += red[b][k];
+        const float scale = 1.0f / sqrtf(tot / D + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            float *e = xs + b * D + tid + j * WG;
+            *e = b < B ? *e * scale * w[j] : 0.f;
+        }
+    }
+    __syncthreads();
+    if (i0 >= F) return;
+    float acc[NB], h1[NB], h3[NB];
+    hw_dot<D, NB>(wv, xs, hl, acc);
+    pair_reduce<NB>(acc, h1, h3);
+    if (lane < LM_TA_COPIES) {
+        unsigned long long *dst = tg.tgt + (size_t)lane * LM_TAG_B * F + i;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= B) break;
+            const float silu = h1[b] / (1.0f + expf(-h1[b]));  /* forward.h:101 */
+            tag_store(dst + (size_t)b * F, silu * h3[b], tag);  /* forward.h:151 */
+        }
+    }
+}
+
+/* W2 role of k_qkv_attn (the FFN in the launch), work-group a of the role, a
+ * row pair per wave as in k_w2_residual: x[b, r..r+1] = x'[b, r..r+1] +
+ * W2[r..r+1, :] . g[b], g from copy a % LM_TA_COPIES of its tagged words. */
+template <int D, int NB, int F>
+__device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__restrict__ W2, int B,
+                                        const QkvTagged &tg, int a, float *xs)
+{
+    const int p = a * NWAVE + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
+    const int wpairs = D / 2;
+    const int r = 2 * min(p, wpairs - 1);
+    uint4 wv[F / 256];
+    hw_load<F>(W2 + (size_t)(r + half) * F, hl, wv);
+    const unsigned tag = qkv_tag(tg);
+    const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D + r;
+    const unsigned long long *tgc = tg.tgt + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * F;
+    if (LM_TAG_DOORBELL & 4) tag_doorbell(tgc, B * F, a / LM_TA_COPIES, tag, tg.err);
+    /* x' of this row pair (written before any gate word) with the gate */
+    unsigned long long v0[NB], v1[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        v0[b] = b < B ? tag_peek(txc + (size_t)b * D) : 0ull;
+        v1[b] = b < B ? tag_peek(txc + (size_t)b * D + 1) : 0ull;
+    }
+    tag_wait_span(tgc, B * F, tag, tg.err, xs);
+    for (int k = B * F + threadIdx.x; k < NB * F; k += WG) xs[k] = 0.f;
+    float2 xo[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        xo[b] = b < B ? make_float2(tag_take(v0[b], txc + (size_t)b * D, tag, tg.err),
+                                    tag_take(v1[b], txc + (size_t)b * D + 1, tag, tg.err))
+                      : make_float2(0.f, 0.f);
+    __syncthreads();
+    if (p >= wpairs) return;
+    float acc[NB], r0[NB], r1[NB];
+    hw_dot<F, NB>(wv, xs, hl, acc);
+    pair_reduce<NB>(acc, r0, r1);
+    if (lane == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (b >= B) break;
+            *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
+        }
+    }
+}
+
+/* The FFN operands of a layer run inside k_qkv_attn. */
+struct FfnArgs {
+    const float *rms_w;   /* rms_ffn gains [D] */
+    const u16 *w13;       /* W1/W3 rows interleaved in LMK_GATE_BLOCK blocks [2F, D] */
+    const u16 *w2;        /* [D, F] */
+};
+
+/* One launch of the batch 1-4 decode chain per layer; its work-groups take
+ * roles in this order, each role waiting only on roles before it:
+ *  - 0 .. nprod-1: the QKV GEMV of k_qkv_rope, also storing q, k, v as tagged
+ *    hand-off words;
+ *  - then one per (row b, head h): the attention of head h, row b, which loads
+ *    its first cached K/V tile, waits for the current position's q, k, v words
+ *    and hands the head output on (fp32 to out[b, h*HD ..] without WO, else
+ *    as tagged words, in LM_TA_COPIES copies);
+ *  - with WO, D/(2*NWAVE) work-groups of the Wo GEMV + residual (wo_role);
+ *  - with F > 0 (the layer's FFN in the launch too), F/NWAVE work-groups of the
+ *    W1/W3 gate (w13_role), then D/(2*NWAVE) of the W2 GEMV + residual
+ *    (w2_role).
+ * A role's work-groups come after every work-group it waits for in dispatch
+ * order, so the waits end however many work-groups the device holds at once.
+ * In layer 0 (emb) the residual starts from the embedding row and the QKV
+ * work-groups leave x alone, so each element of x has one writer in the
+ * launch; the QKV and Wo work-groups read x before they store any word, and x
+ * is written only after every word of every head, so no read of x in the
+ * launch sees the value written in it. */
+#ifndef LM_QA_WAVES
+#define LM_QA_WAVES 1
+#endif
+template <int D, int NB, typename KT, int HD, bool WO, int F>
+__global__ void __launch_bounds__(WG, LM_QA_WAVES) k_qkv_attn(
+    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
+    const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV,
+    const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
+    int B, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq, int npairs, int nprod, int H,
+    QkvTagged tg, float *__restrict__ out, const u16 *__restrict__ Wo, FfnArgs ffn)
+{
+    static_assert(F == 0 || WO, "the FFN roles take x' from the Wo role");
+    static_assert(LM_TA_COPIES <= 64 && LM_TX_COPIES <= 64, "a wave's lanes store the copies");
+    if ((int)blockIdx.x < nprod) {
+        qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, HD, rc, rs, pos, B, nullptr, kc, vc,
+                            max_seq, npairs, &tg, !WO);
+        return;
+    }
+    int a = blockIdx.x - nprod;
+    if (!WO || a < H * B) {
+        __shared__ float oh[HD];
+        const int h = a % H, b = a / H;
+        attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
+        if constexpr (WO) {
+            /* every copy of the head output, the work-group's threads taking
+             * (element, copy) pairs */
+            const unsigned tag = qkv_tag(tg);
+            for (int t = threadIdx.x; t < HD * LM_TA_COPIES; t += WG) {
+                const int e = t % HD, c = t / HD;
+                tag_store(tg.ta + (size_t)c * LM_TAG_B * NQ + (size_t)b * NQ + h * HD + e, oh[e], tag);
+            }
+        } else if ((int)threadIdx.x < HD) {
+            out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
+        }
+        return;
+    }
+    if constexpr (WO) {
+        /* the LDS rows of whichever of the Wo, W1/W3 and W2 roles this
+         * work-group takes */
+        constexpr int ROW = F > D ? F : D;
+        __shared__ __attribute__((aligned(16))) float xs[NB * ROW];
+        constexpr int NWO = (D / 2 + NWAVE - 1) / NWAVE;
+        a -= H * B;
+        if (F == 0 || a < NWO) {
+            wo_role<D, NB, F>(x, emb, tok, Wo, B, NQ, tg, a, xs);
+            return;
+        }
+        if constexpr (F > 0) {
+            constexpr int N13 = (F + NWAVE - 1) / NWAVE;
+            a -= NWO;
+            if (a < N13) w13_role<D, NB, F>(ffn.rms_w, ffn.w13, B, tg, a, xs);
+            else w2_role<D, NB, F>(x, ffn.w2, B, tg, a - N13, xs);
         }
     }
 }
@@ -1065,8 +1269,10 @@ __global__ void k_selftest_reduce(const float *in, float *out)
     default: return hipErrorInvalidValue;                             \
     }
 
-/* LDS budget of the GEMV kernels: NB rows of K fp32. */
-#define GEMV_LDS_OK(K_, NB_) ((size_t)(K_) * (NB_) * 4 <= 65536)
+/* LDS budget of the GEMV kernels: NB rows of K fp32 within the 160 KB a
+ * gfx950 work-group may hold (the compiler checks each kernel's whole static
+ * LDS against the same limit). */
+#define GEMV_LDS_OK(K_, NB_) ((size_t)(K_) * (NB_) * 4 <= 163840)
 
 extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                             const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV,
@@ -1091,40 +1297,73 @@ extern "C" int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const 
     return hipGetLastError();
 }
 
+/* (model width, hidden width) pairs the whole-layer launch is instantiated
+ * for; K_ and F_ name them in the body. */
+#define DISPATCH_DF(D, F, ...)                                                          \
+    do {                                                                                \
+        if ((D) == 256 && (F) == 512) { constexpr int K_ = 256, F_ = 512; __VA_ARGS__; }     \
+        else if ((D) == 512 && (F) == 1024) { constexpr int K_ = 512, F_ = 1024; __VA_ARGS__; } \
+        else if ((D) == 768 && (F) == 2048) { constexpr int K_ = 768, F_ = 2048; __VA_ARGS__; } \
+        else if ((D) == 1024 && (F) == 1024) { constexpr int K_ = 1024, F_ = 1024; __VA_ARGS__; } \
+        else if ((D) == 2048 && (F) == 5632) { constexpr int K_ = 2048, F_ = 5632; __VA_ARGS__; } \
+        else return hipErrorInvalidValue;                                               \
+    } while (0)
+
+extern "C" int lmk_layer_fusable(int D, int F, int B)
+{
+    if (B < 1 || B > 4) return 0;
+    DISPATCH_DF(D, F, DISPATCH_NB(B, {
+        return GEMV_LDS_OK(K_, NB_) && GEMV_LDS_OK(F_, NB_);
+    }));
+    return 0;
+}
+
 extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                             const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                             const float *rope_cos, const float *rope_sin, const int *pos, int B,
                             void *kc, void *vc, int kv_f32, int max_seq, int H,
                             unsigned long long *tagged, const unsigned *epoch, int layer,
-                            int n_layers, int *err, float *out, const uint16_t *wo)
+                            int n_layers, int *err, float *out, const uint16_t *wo,
+                            const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F)
 {
     if (B < 1 || B > 4 || NQ != D || H < 1 || NQ != H * hd || NKV % hd || H % (NKV / hd) ||
-        (emb && !tok) || !tagged || !epoch || !err || (!out && !wo) || (hd != 64 && hd != 128))
+        (emb && !tok) || !tagged || !epoch || !err || (!out && !wo) || (hd != 64 && hd != 128) ||
+        (w13 && (!wo || !w2 || !rms_ffn || F < 1 || F % LMK_GATE_BLOCK || !lmk_layer_fusable(D, F, B))))
         return hipErrorInvalidValue;
     const int npairs = (NQ + 2 * NKV) / 2;
     const int nprod = (npairs + NWAVE - 1) / NWAVE;
     const int nwo = wo ? (D / 2 + NWAVE - 1) / NWAVE : 0;
-    dim3 grid(nprod + H * B + nwo);
-    const QkvTagged tg = {tagged, tagged + (size_t)MAX_TAG_B * NQ,
-                          tagged + (size_t)MAX_TAG_B * (NQ + NKV),
-                          tagged + (size_t)MAX_TAG_B * (NQ + 2 * NKV), epoch, layer, n_layers, err};
-#define LAUNCH_QA(HD_, KT_, WO_)                                                                   \
-    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv,  \
-            NQ, NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H,  \
-            tg, out, (const u16 *)wo)
-#define LAUNCH_QA2(HD_, KT_)                  \
-    do {                                      \
-        if (wo) LAUNCH_QA(HD_, KT_, true);    \
-        else LAUNCH_QA(HD_, KT_, false);      \
+    dim3 grid(nprod + H * B + nwo);   /* with the FFN: + its roles' work-groups, below */
+    unsigned long long *ta = tagged + (size_t)LM_TAG_B * (NQ + 2 * NKV);
+    unsigned long long *tx = ta + (size_t)LM_TA_COPIES * LM_TAG_B * NQ;
+    unsigned long long *tgt = tx + (size_t)LM_TX_COPIES * LM_TAG_B * D;
+    const QkvTagged tg = {tagged, tagged + (size_t)LM_TAG_B * NQ, tagged + (size_t)LM_TAG_B * (NQ + NKV),
+                          ta, tx, tgt, epoch, layer, n_layers, err};
+    const FfnArgs ffn = {rms_ffn, (const u16 *)w13, (const u16 *)w2};
+#define LAUNCH_QA(HD_, KT_, WO_, F_)                                                                \
+    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_, F_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv, \
+            NQ, NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H,     \
+            tg, out, (const u16 *)wo, ffn)
+#define LAUNCH_QA_KV(WO_, F_)                                    \
+    do {                                                         \
+        if (hd == 64 && kv_f32) LAUNCH_QA(64, float, WO_, F_);   \
+        else if (hd == 64) LAUNCH_QA(64, u16, WO_, F_);          \
+        else if (kv_f32) LAUNCH_QA(128, float, WO_, F_);         \
+        else LAUNCH_QA(128, u16, WO_, F_);                       \
     } while (0)
-    DISPATCH_D(D, DISPATCH_NB(B, {
-        if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
-        if (hd == 64 && kv_f32) LAUNCH_QA2(64, float);
-        else if (hd == 64) LAUNCH_QA2(64, u16);
-        else if (kv_f32) LAUNCH_QA2(128, float);
-        else LAUNCH_QA2(128, u16);
-    }));
-#undef LAUNCH_QA2
+    if (w13) {
+        DISPATCH_DF(D, F, DISPATCH_NB(B, {
+            grid.x += (F_ + NWAVE - 1) / NWAVE + (K_ / 2 + NWAVE - 1) / NWAVE;
+            LAUNCH_QA_KV(true, F_);
+        }));
+    } else {
+        DISPATCH_D(D, DISPATCH_NB(B, {
+            if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
+            if (wo) LAUNCH_QA_KV(true, 0);
+            else LAUNCH_QA_KV(false, 0);
+        }));
+    }
+#undef LAUNCH_QA_KV
 #undef LAUNCH_QA
     return hipGetLastError();
 }

@@ -56,20 +56,47 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rope_cos, const float *rope_sin, const int *pos,
                  int B, float *q, void *kc, void *vc, int kv_f32, int max_seq);
 
+/* Tagged hand-off words of the batch 1-4 chain (LM_TAG_WORDS of them): q, k
+ * and v of up to LM_TAG_B rows, then LM_TA_COPIES copies of the head
+ * outputs, LM_TX_COPIES of x after Wo and LM_TA_COPIES of the FFN gate, each
+ * reading work-group taking one copy, so that the readers of one value spread
+ * over more memory channels. */
+#define LM_TAG_B 4
+#ifndef LM_TA_COPIES
+#define LM_TA_COPIES 4
+#endif
+#ifndef LM_TAG_SLEEP
+#define LM_TAG_SLEEP 1
+#endif
+#ifndef LM_TX_COPIES
+#define LM_TX_COPIES 4
+#endif
+#define LM_TAG_WORDS(NQ, NKV, D, F) \
+    ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * ((NQ) + (F)) + LM_TX_COPIES * (D)))
+
 /* lmk_qkv_rope and the attention of every (head, row) in one launch: the
  * QKV work-groups hand q, k, v of the current position to the attention
- * work-groups through tagged words (`tagged`: 4 * (2 * NQ + 2 * NKV) 64-bit
- * words, zero at allocation), tagged with *epoch * n_layers + layer + 1; the
- * head outputs go to out[b, h*hd ..] (fp32), or, with wo (the layer's Wo [D,
- * NQ]), on through tagged words to Wo work-groups in the same launch that add
- * Wo . attn to x (lmk_wo_residual's work; out unused).  A hand-off wait that
- * gives up sets *err (the kernel still ends).  B <= 4, hd 64 or 128. */
+ * work-groups through tagged words (`tagged`: LM_TAG_WORDS(NQ, NKV, D, F)
+ * 64-bit words, zero at allocation), tagged with *epoch * n_layers + layer +
+ * 1; the head outputs go to out[b, h*hd ..] (fp32), or, with wo (the layer's
+ * Wo [D, NQ]), on through tagged words to Wo work-groups in the same launch
+ * that add Wo . attn to x (lmk_wo_residual's work; out unused).  With w13 too
+ * (rms_ffn, w13 and w2 of the layer, hidden width F), the Wo work-groups hand
+ * x on through tagged words to W1/W3 work-groups (lmk_ffn13's work), and
+ * those the gate to W2 work-groups that write x (lmk_w2_residual's work): the
+ * whole layer in one launch.  A hand-off wait that gives up sets *err (the
+ * kernel still ends).  B <= 4, hd 64 or 128. */
 int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                  const float *rope_cos, const float *rope_sin, const int *pos, int B,
                  void *kc, void *vc, int kv_f32, int max_seq, int H,
                  unsigned long long *tagged, const unsigned *epoch, int layer,
-                 int n_layers, int *err, float *out, const uint16_t *wo);
+                 int n_layers, int *err, float *out, const uint16_t *wo,
+                 const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F);
+
+/* Whether the whole-layer form of lmk_qkv_attn (w13 given) is built for this
+ * model width, hidden width and batch. */
+int lmk_layer_fusable(int D, int F, int B);
 
 /* Causal attention, one work-group per (head, row): out[b, h*hd ..] =
  * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V over cache slot slot[b] (slot

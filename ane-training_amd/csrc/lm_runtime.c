@@ -61,10 +61,10 @@ struct LMModel {
     int *d_rtok, *d_rpos, *d_rslot;   /* prefill rows: token, position, slot */
     /* per-slot greedy state */
     int *d_tok, *d_pos, *d_hist, *d_slot_id;
-    /* batch 1-4 chain: QKV, attention (fuse_qa >= 1) and Wo (fuse_qa 2) in one
-     * launch, handing q, k, v and the head outputs over through tagged words;
-     * the decode-step count that tags them; the flag a hand-off wait that
-     * gives up sets */
+    /* batch 1-4 chain: QKV, attention (fuse_qa >= 1), Wo (>= 2) and the FFN
+     * (3) in one launch, handing q, k, v, the head outputs, x and the gate
+     * over through tagged words; the decode-step count that tags them; the
+     * flag a hand-off wait that gives up sets */
     int fuse_qa;
     unsigned long long *d_tagged;
     unsigned *d_epoch;
@@ -477,14 +477,14 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     if ((st = dev_alloc((void **)&m->d_pos, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_slot_id, NB * 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
-    const size_t ntag = (size_t)MAX_GEMV_B * (2 * NQ + 2 * NKV);
+    const size_t ntag = LM_TAG_WORDS(NQ, NKV, D, F);
     if ((st = dev_alloc((void **)&m->d_tagged, ntag * 8))) goto fail;
     if ((st = dev_alloc((void **)&m->d_epoch, 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
     if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_epoch, 0, 4) != hipSuccess ||
         hipMemset(m->d_err, 0, 4) != hipSuccess)
         FAIL(LM_ERR_HIP);
-    m->fuse_qa = 2;
+    m->fuse_qa = 3;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
 
@@ -597,7 +597,7 @@ int lm_set_option(LMModel *m, int option, int value)
         m->use_graph = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_FUSE_QKV_ATTN:
-        if (value < 0 || value > 2) return LM_ERR_INVALID;
+        if (value < 0 || value > 3) return LM_ERR_INVALID;
         if (value == m->fuse_qa) return LM_OK;
         HIPCHK(hipStreamSynchronize(m->stream));
         drop_graphs(m);
@@ -628,9 +628,27 @@ int lm_set_option(LMModel *m, int option, int value)
         }                                                                             \
     } while (0)
 
-/* Queue the kernel of family `fam` (LM_KERN_*) of layer l for rows 0..B-1. */
+/* The decode chain's fusion level for B rows: fuse_qa, except that the
+ * whole-layer launch (3) is built only for the (dim, hidden) pairs and batches
+ * lmk_layer_fusable names; level 2 runs elsewhere. */
+static int chain_level(const LMModel *m, int B)
+{
+    return m->fuse_qa == 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : m->fuse_qa;
+}
+
+/* Whether kernel family fam runs inside the QKV launch at fusion level lvl. */
+static int fam_inside(int fam, int lvl)
+{
+    return (fam == LM_KERN_ATTN && lvl >= 1) || (fam == LM_KERN_WO && lvl >= 2) ||
+           ((fam == LM_KERN_W13 || fam == LM_KERN_W2) && lvl >= 3);
+}
+
+/* Queue the kernel of family `fam` (LM_KERN_*) of layer l for rows 0..B-1
+ * (nothing for a family that runs inside the QKV launch). */
 static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
 {
+    const int lvl = chain_level(m, B);
+    if (fam_inside(fam, lvl)) return LM_OK;
     hipStream_t s = m->stream;
     const int D = m->D, F = m->F;
     const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
@@ -638,25 +656,26 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
     void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
     switch (fam) {
     case LM_KERN_QKV:
-        if (m->fuse_qa)   /* with the attention of every head (and Wo at level 2) */
+        if (lvl)   /* with the attention of every head (Wo from level 2, the FFN at 3) */
             KCHK(lmk_qkv_attn(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
                               m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
                               m->d_rope_cos, m->d_rope_sin, m->d_pos, B, kc, vc, m->kv_f32,
                               m->max_seq, m->H, m->d_tagged, m->d_epoch, l, m->L, m->d_err,
-                              m->d_attn, m->fuse_qa == 2 ? lw + m->off_wo : NULL));
+                              m->d_attn, lvl >= 2 ? lw + m->off_wo : NULL,
+                              m->d_rms_ffn + (size_t)l * D, lvl == 3 ? lw + m->off_w13 : NULL,
+                              lw + m->off_w2, F));
         else
             KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
                               m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
                               m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_q, kc, vc, m->kv_f32,
                               m->max_seq));
         break;
-    case LM_KERN_ATTN:   /* none when fused into the QKV launch */
-        if (!m->fuse_qa)
-            KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
-                                 m->hd, m->max_seq, m->d_attn, NULL));
+    case LM_KERN_ATTN:
+        KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, m->d_pos, NULL, B, m->H, m->Hkv,
+                             m->hd, m->max_seq, m->d_attn, NULL));
         break;
-    case LM_KERN_WO:   /* none when fused into the QKV launch */
-        if (m->fuse_qa != 2) KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
+    case LM_KERN_WO:
+        KCHK(lmk_wo_residual(s, m->d_attn, lw + m->off_wo, D, B, m->d_x));
         break;
     case LM_KERN_W13:
         KCHK(lmk_ffn13(s, m->d_x, m->d_rms_ffn + (size_t)l * D, lw + m->off_w13, D, F, B, m->d_g));
@@ -1205,8 +1224,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
         int k = 0;
         for (int l = 0; l < m->L && rc == LM_OK; l++)
             for (int f = 0; f < 5 && rc == LM_OK; f++) {
-                if ((fams[f] == LM_KERN_ATTN && m->fuse_qa) || (fams[f] == LM_KERN_WO && m->fuse_qa == 2))
-                    continue;   /* inside the QKV launch */
+                if (fam_inside(fams[f], chain_level(m, B))) continue;   /* inside the QKV launch */
                 kfam[k] = fams[f];
                 lmk_time_next(ev[2 * k], ev[2 * k + 1]);
                 rc = enqueue_kernel(m, B, fams[f], l, NULL);
@@ -1230,9 +1248,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
             launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1
-                                   : (f == LM_KERN_ATTN && m->fuse_qa) || (f == LM_KERN_WO && m->fuse_qa == 2)
-                                       ? 0
-                                       : m->L;
+                                   : fam_inside(f, chain_level(m, B)) ? 0 : m->L;
     }
     for (int i = 0; ev && i < 2 * nk; i++)
         if (ev[i]) hipEventDestroy(ev[i]);

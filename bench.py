@@ -41,19 +41,31 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # Published reference figure for this metric: Stories-110M B=1 greedy decode on
 # the ANE (libane, fp16), M3 Pro: 41.7 tok/s (full 256-window recompute).
-LIB_FUSE_DEFAULT = 2     # LM_OPT_FUSE_QKV_ATTN after lm_load / lm_create
+LIB_FUSE_DEFAULT = 3     # LM_OPT_FUSE_QKV_ATTN after lm_load / lm_create
 REF_TOK_S = 41.7
 SEQ = 256
 
 
-def qkv_launch_writes(cfg, kvb, with_wo):
+# FETCH_SIZE per launch of the C0 chain's kernels with QKV + attention in one launch and
+# the rest apart (bytes, the counter's KiB x 1024 x 2.000)
+C0_FETCH = {"qkv": 4737000, "wo": 1234000, "w13": 6382000, "w2": 3265000}
+TAG_COPIES = 8    # copies of each tagged word set that several work-groups read
+
+
+def qkv_launch_writes(cfg, kvb, folded):
     """Bytes the fused QKV launch writes for one row: the q, k, v hand-off words
-    (8 bytes each) and the K/V append; then either the fp32 head outputs, or
-    (with Wo inside) the head-output words and the updated residual row."""
+    (8 bytes each) and the K/V append; then the fp32 head outputs, or (Wo
+    inside) the head-output words in every copy and either x (3 KB) or (the
+    FFN inside too) the words of x and of the gate in every copy, then x."""
     hd = cfg.dim // cfg.n_heads
-    nq, nkv = cfg.dim, cfg.n_kv_heads * hd
+    nq, nkv, D, F = cfg.dim, cfg.n_kv_heads * hd, cfg.dim, cfg.hidden_dim
     w = 8 * (nq + 2 * nkv) + 2 * nkv * kvb
-    return w + (8 * nq + 4 * cfg.dim if with_wo else 4 * nq)
+    if "wo" not in folded:
+        return w + 4 * nq
+    w += 8 * TAG_COPIES * nq + 4 * D
+    if "w2" in folded:
+        w += 8 * TAG_COPIES * (D + F)
+    return w
 
 
 def algorithmic_bytes(cfg, B, mean_ctx, kv_bytes=2, logits=False):
@@ -328,7 +340,7 @@ def main():
     ap.add_argument("--steps", type=int, default=32, help="timed 256-token C0 sequences")
     ap.add_argument("--warmup", type=int, default=2, help="untimed 256-token C0 sequences")
     ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
-    ap.add_argument("--fuse", type=int, choices=[0, 1, 2], default=None,
+    ap.add_argument("--fuse", type=int, choices=[0, 1, 2, 3], default=None,
                     help="LM_OPT_FUSE_QKV_ATTN for the C0 chain (A/B; default: the library's)")
     ap.add_argument("--kv16", action="store_true",
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
@@ -393,14 +405,16 @@ def main():
         # kernel timed by hipEvents at its own dispatch's start and end
         us, launches = m.profile_chain([1], [0], SEQ - 2)
     m.close()
-    if launches is None:   # the chain's launch counts: one per layer, attention (and Wo at
-        # level 2) inside the QKV launch, classifier and argmax once
+    if launches is None:   # the chain's launch counts: one per layer, attention (Wo from
+        # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once
         fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
-        inside = {"attn": fz >= 1, "wo": fz == 2}
+        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz == 3, "w2": fz == 3}
         launches = {k: (1 if k in ("cls", "argmax") else 0 if inside.get(k) else cfg.n_layers)
                     for k in algo}
-    for k in ("attn", "wo"):        # families that run inside the QKV launch
+    folded = []
+    for k in ("attn", "wo", "w13", "w2"):    # families that run inside the QKV launch
         if launches.get(k) == 0:
+            folded.append(k)
             algo["qkv"] += algo.pop(k)
             launches.pop(k)
     step_bytes = sum(algo[k] * launches[k] for k in algo)
@@ -430,13 +444,12 @@ def main():
         dur_us = us[dom]
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
         traffic = None
-        if dom == "qkv" and not args.kv16:
-            # fp32 cache, from FETCH_SIZE (x 2.000, the 256 MiB copy calibration) with QKV +
-            # attention fused and Wo launched apart (profiles/decode_b1_stories110m_chain.md):
-            # 4.737 MB per k_qkv_attn launch, 1.234 MB per k_wo_residual launch (their sum
-            # when Wo runs inside the launch too) + the launch's writes, taken as algorithmic
-            traffic = 4737000 + (1234000 if "wo" not in algo else 0) + qkv_launch_writes(
-                cfg, kvb, "wo" not in algo)
+        if dom == "qkv" and not args.kv16 and "attn" in folded:
+            # fp32 cache: FETCH_SIZE (x 2.000, the 256 MiB copy calibration) of each part
+            # launched on its own, QKV + attention fused (profiles/decode_b1_stories110m_chain.md),
+            # summed over the parts this launch holds, + its writes, taken as algorithmic
+            traffic = sum(C0_FETCH[k] for k in ["qkv"] + folded if k != "attn") + \
+                qkv_launch_writes(cfg, kvb, folded)
         out["roofline"] = {"bound": "hbm", "kernel": "k_qkv_attn" if dom == "qkv" else dom,
                            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

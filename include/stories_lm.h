@@ -242,11 +242,13 @@ int lm_timer_end(LMModel *m, float *ms);
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
-/* LM_OPT_FUSE_QKV_ATTN: 2 (default) runs the batch 1-4 chain's QKV GEMV, the
- * attention of every head and the Wo GEMV + residual as one launch per layer
- * (the QKV work-groups hand q, k, v to the attention work-groups, and those
- * the head outputs to the Wo work-groups, through tagged words in memory);
- * 1 launches Wo apart; 0 launches each of the three apart. */
+/* LM_OPT_FUSE_QKV_ATTN: 3 (default) runs each layer of the batch 1-4 decode
+ * chain as one launch: QKV GEMV, the attention of every head, Wo + residual,
+ * W1/W3 + gate and W2 + residual, each set of work-groups handing its
+ * results to the next through tagged words in memory (where the whole-layer
+ * form is not built for the model's widths and batch, level 2 runs); 2 runs
+ * QKV, attention and Wo as one launch and the FFN as two; 1 also launches Wo
+ * apart; 0 launches all five apart. */
 #define LM_OPT_FUSE_QKV_ATTN 5
 int lm_set_option(LMModel *m, int option, int value);
 

@@ -195,6 +195,29 @@ def test_scaled_c4_full_shape(lm):
         check_trajectory(got, fx[f"ids_{b}"], tv[:, 0] - tv[:, 1], f"sequence {b}")
 
 
+# ---- the decode chain at the scaled model's widths ------------------------------
+
+SCALED_2L = dict(SCALED, n_layers=2, vocab_size=512, seq_len=32)
+
+
+@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("fuse", [3, 2])
+def test_wide_decode_chain_batches(lm, orc, B, fuse):
+    """The batch 1-4 decode chain at dim 2048, hidden 5632, head dim 128 (two
+    layers): B rows of different tokens, 6 steps, each row against the
+    reference forward over its own tokens (fp32 cache: TIGHT)."""
+    _say(f"[wide decode chain B={B} fuse{fuse}]")
+    d = SCALED_2L
+    m, w32 = make(lm, d, 71, B, 32, True)
+    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
+    toks = np.random.default_rng(71 + B).integers(0, d["vocab_size"], (B, 6)).astype(np.int32)
+    got = np.stack([m.forward_batch(toks[:, p], np.full(B, p, np.int32))[0] for p in range(6)], 1)
+    m.close()
+    for b in range(B):
+        ref = orc.Oracle(cfg7(d), w32, True, 32).forward_cached(toks[b])
+        np.testing.assert_allclose(got[b], ref, err_msg=f"row {b}", **TIGHT)
+
+
 # ---- long contexts: every tile loop of the decode attention --------------------
 
 LONG = 620     # cached positions reach 619: 20 tiles of 32, past two rounds of 4 waves x 2 tiles
@@ -205,11 +228,11 @@ LONG_HD128 = dict(dim=512, hidden_dim=1024, n_layers=2, n_heads=4, n_kv_heads=2,
 
 @pytest.mark.parametrize("name,d", [("hd64", LONG_HD64), ("hd128", LONG_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-@pytest.mark.parametrize("fuse", [2, 1, 0])
+@pytest.mark.parametrize("fuse", [3, 2, 1, 0])
 def test_long_context_decode_chain(lm, orc, name, d, kv, fuse):
     """620 steps of the B=1 decode chain (the attention over up to 620 cached
-    positions, GQA, in the QKV launch or its own) against the reference
-    forward at every step."""
+    positions, GQA, in the QKV launch or its own; fuse 3 runs the whole layer
+    in that launch) against the reference forward at every step."""
     _say(f"[long decode chain {name} kv{kv} fuse{fuse}]")
     m, w32 = make(lm, d, 61, 1, 640, kv == 32)
     m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
