@@ -1124,11 +1124,87 @@ __global__ void __launch_bounds__(WG) k_w2_residual(
 #define CLS_PAIRS_PER_WAVE 4
 #define CLS_ROWS_PER_WG (2 * CLS_PAIRS_PER_WAVE * NWAVE)
 
+/* The argmax reduction inside the classifier launch (k_cls with fold.tw): the
+ * classifier work-groups store the partial of row b, blk as two tagged words
+ * (value bits; index), tw[b*nblk + blk] and tw[(LM_TAG_B + b)*nblk + blk],
+ * tagged *epoch + 1; one more work-group, last in dispatch order, waits for
+ * them and does k_argmax_final's work. */
+struct ArgFold {
+    unsigned long long *tw;     /* 2 * LM_TAG_B * nblk words, zero at allocation */
+    unsigned *epoch;
+    int *tok, *pos, *hist;
+    int hist_stride;
+    int *err;
+};
+
+/* The reducer of k_cls with fold: rows 0..B-1 over nblk partials (lowest index
+ * on ties, the combine being commutative and associative, so any order gives
+ * k_argmax_final's result). */
+__device__ __forceinline__ void cls_argmax_fold(const ArgFold &f, int nblk, int B)
+{
+    __shared__ float sv[NWAVE];
+    __shared__ int si[NWAVE];
+    const unsigned tag = *f.epoch + 1u;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int b = 0; b < B; b++) {
+        const unsigned long long *wv_ = f.tw + (size_t)b * nblk;
+        const unsigned long long *wi_ = f.tw + (size_t)(LM_TAG_B + b) * nblk;
+        if (threadIdx.x == 0) (void)tag_wait(wi_ + nblk - 1, tag, f.err);   /* doorbell */
+        __syncthreads();
+        float v = -INFINITY;
+        int id = 0x7FFFFFFF;
+        for (int i0 = threadIdx.x; i0 < nblk; i0 += 4 * WG) {
+            unsigned long long pv[4], pi[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = i0 + j * WG;
+                pv[j] = i < nblk ? tag_peek(wv_ + i) : 0ull;
+                pi[j] = i < nblk ? tag_peek(wi_ + i) : 0ull;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = i0 + j * WG;
+                if (i < nblk) {
+                    const float pval = tag_take(pv[j], wv_ + i, tag, f.err);
+                    const int pidx = __builtin_bit_cast(int, tag_take(pi[j], wi_ + i, tag, f.err));
+                    argmax_combine(v, id, pval, pidx);
+                }
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(v, off, 64);
+            const int oi = __shfl_xor(id, off, 64);
+            argmax_combine(v, id, ov, oi);
+        }
+        if (lane == 0) { sv[wv] = v; si[wv] = id; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            v = sv[0];
+            id = si[0];
+            for (int w = 1; w < NWAVE; w++) argmax_combine(v, id, sv[w], si[w]);
+            if (id == 0x7FFFFFFF) id = 0;
+            f.tok[b] = id;
+            if (f.hist) {
+                const int p = f.pos[b];
+                f.hist[(size_t)b * f.hist_stride + p + 1] = id;
+                f.pos[b] = p + 1;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *f.epoch += 1u;   /* the next step's hand-off tags */
+}
+
 template <int D, int NB>
 __global__ void __launch_bounds__(WG) k_cls(
     const float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W,
-    int V, int B, float *__restrict__ logits, LMArgPart *__restrict__ part)
+    int V, int B, float *__restrict__ logits, LMArgPart *__restrict__ part, ArgFold fold)
 {
+    if (fold.tw && blockIdx.x == gridDim.x - 1) {
+        cls_argmax_fold(fold, gridDim.x - 1, B);
+        return;
+    }
+    const unsigned ftag = fold.tw ? *fold.epoch + 1u : 0u;
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     __shared__ float bvs[NB][NWAVE];
     __shared__ int bis[NB][NWAVE];
@@ -1182,7 +1258,14 @@ __global__ void __launch_bounds__(WG) k_cls(
         float v = bvs[b][0];
         int id = bis[b][0];
         for (int w = 1; w < NWAVE; w++) argmax_combine(v, id, bvs[b][w], bis[b][w]);
-        part[(size_t)b * gridDim.x + blockIdx.x] = LMArgPart{v, id};
+        if (fold.tw) {
+            const int nblk = gridDim.x - 1;
+            tag_store(fold.tw + (size_t)b * nblk + blockIdx.x, v, ftag);
+            tag_store(fold.tw + (size_t)(LM_TAG_B + b) * nblk + blockIdx.x,
+                      __builtin_bit_cast(float, id), ftag);
+        } else {
+            part[(size_t)b * gridDim.x + blockIdx.x] = LMArgPart{v, id};
+        }
     }
 }
 
@@ -1450,14 +1533,18 @@ extern "C" int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2
 extern "C" int lmk_cls_nblk(int V) { return (V + CLS_ROWS_PER_WG - 1) / CLS_ROWS_PER_WG; }
 
 extern "C" int lmk_cls(hipStream_t s, const float *x, const float *rms_w, const uint16_t *wcls, int D,
-                       int V, int B, float *logits, LMArgPart *part)
+                       int V, int B, float *logits, LMArgPart *part, unsigned long long *fold_tw,
+                       unsigned *epoch, int *tok, int *pos, int *hist, int hist_stride, int *err)
 {
-    if (B < 1 || B > 4 || V < 1 || !part) return hipErrorInvalidValue;
-    dim3 grid(lmk_cls_nblk(V));
+    if (B < 1 || B > 4 || V < 1 || (!part && !fold_tw) ||
+        (fold_tw && (!epoch || !tok || !err || (hist && !pos))))
+        return hipErrorInvalidValue;
+    dim3 grid(lmk_cls_nblk(V) + (fold_tw ? 1 : 0));
+    const ArgFold fold = {fold_tw, epoch, tok, pos, hist, hist_stride, err};
     DISPATCH_D(D, DISPATCH_NB(B, {
         if (!GEMV_LDS_OK(K_, NB_)) return hipErrorInvalidValue;
         DLAUNCH((k_cls<K_, NB_>), grid, dim3(WG), 0, s, x, rms_w, wcls, V, B, logits,
-                           part);
+                           part, fold);
     }));
     return hipGetLastError();
 }

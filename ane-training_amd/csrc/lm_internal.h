@@ -119,11 +119,16 @@ int lmk_w2_residual(hipStream_t s, const float *g, const uint16_t *w2, int D,
 
 /* xn = rmsnorm(x[b]) * w; logits[b, v] = Wcls[v] . xn (logits may be NULL);
  * argmax partials (lowest index on ties) to part[b * nblk + blk], nblk =
- * lmk_cls_nblk(V). */
+ * lmk_cls_nblk(V).  With fold_tw (2 * LM_TAG_B * nblk 64-bit words, zero at
+ * allocation) the partials go out as tagged words instead, and one more
+ * work-group of the launch reduces them as lmk_argmax_final does (tok, and
+ * with hist the history and positions), then advances *epoch; a hand-off wait
+ * that gives up sets *err. */
 int lmk_cls_nblk(int V);
 int lmk_cls(hipStream_t s, const float *x, const float *rms_w,
             const uint16_t *wcls, int D, int V, int B, float *logits,
-            LMArgPart *part);
+            LMArgPart *part, unsigned long long *fold_tw, unsigned *epoch, int *tok,
+            int *pos, int *hist, int hist_stride, int *err);
 
 /* Reduce the argmax partials of each row b: tok[b] = argmax; when hist != NULL,
  * hist[b*hist_stride + pos[b] + 1] = tok[b] and pos[b] += 1 (device-resident

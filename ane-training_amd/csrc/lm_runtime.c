@@ -67,6 +67,7 @@ struct LMModel {
      * flag a hand-off wait that gives up sets */
     int fuse_qa;
     unsigned long long *d_tagged;
+    unsigned long long *d_cls_tw;     /* the classifier's argmax partials as tagged words (level 3) */
     unsigned *d_epoch;
     int *d_err;
     /* pinned host staging */
@@ -479,10 +480,12 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     if ((st = dev_alloc((void **)&m->d_hist, (size_t)max_batch * (max_seq + 1) * 4))) goto fail;
     const size_t ntag = LM_TAG_WORDS(NQ, NKV, D, F);
     if ((st = dev_alloc((void **)&m->d_tagged, ntag * 8))) goto fail;
+    const size_t ncls = (size_t)2 * LM_TAG_B * m->cls_nblk;
+    if ((st = dev_alloc((void **)&m->d_cls_tw, ncls * 8))) goto fail;
     if ((st = dev_alloc((void **)&m->d_epoch, 4))) goto fail;
     if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
-    if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_epoch, 0, 4) != hipSuccess ||
-        hipMemset(m->d_err, 0, 4) != hipSuccess)
+    if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_cls_tw, 0, ncls * 8) != hipSuccess ||
+        hipMemset(m->d_epoch, 0, 4) != hipSuccess || hipMemset(m->d_err, 0, 4) != hipSuccess)
         FAIL(LM_ERR_HIP);
     m->fuse_qa = 3;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
@@ -571,7 +574,8 @@ void lm_free(LMModel *m)
     free_rows(m);
     void *dev[] = {m->d_layers, m->d_embed, m->untied ? m->d_wcls : NULL, m->d_rms_att,
                    m->d_rms_ffn, m->d_rms_final, m->d_rope_cos, m->d_rope_sin, m->d_kc,
-                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_tagged, m->d_epoch, m->d_err};
+                   m->d_vc, m->d_tok, m->d_pos, m->d_hist, m->d_slot_id, m->d_tagged, m->d_cls_tw, m->d_epoch,
+                   m->d_err};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
     if (m->h_logits) hipHostFree(m->h_logits);
@@ -636,11 +640,12 @@ static int chain_level(const LMModel *m, int B)
     return m->fuse_qa == 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : m->fuse_qa;
 }
 
-/* Whether kernel family fam runs inside the QKV launch at fusion level lvl. */
+/* Whether kernel family fam runs inside another family's launch at fusion
+ * level lvl (the QKV launch; at level 3 the argmax inside the classifier's). */
 static int fam_inside(int fam, int lvl)
 {
     return (fam == LM_KERN_ATTN && lvl >= 1) || (fam == LM_KERN_WO && lvl >= 2) ||
-           ((fam == LM_KERN_W13 || fam == LM_KERN_W2) && lvl >= 3);
+           ((fam == LM_KERN_W13 || fam == LM_KERN_W2 || fam == LM_KERN_ARGMAX) && lvl >= 3);
 }
 
 /* Queue the kernel of family `fam` (LM_KERN_*) of layer l for rows 0..B-1
@@ -684,7 +689,9 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
         KCHK(lmk_w2_residual(s, m->d_g, lw + m->off_w2, D, F, B, m->d_x));
         break;
     case LM_KERN_CLS:
-        KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax));
+        KCHK(lmk_cls(s, m->d_x, m->d_rms_final, m->d_wcls, D, m->V, B, logits, m->d_amax,
+                     lvl == 3 ? m->d_cls_tw : NULL, m->d_epoch, m->d_tok, m->d_pos, m->d_hist,
+                     m->max_seq + 1, m->d_err));
         break;
     case LM_KERN_ARGMAX:
         KCHK(lmk_argmax_final(s, m->d_amax, m->cls_nblk, B, m->d_tok, m->d_pos, m->d_hist,
@@ -1231,6 +1238,7 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
                 k++;
             }
         for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
+            if (fam_inside(f, chain_level(m, B))) continue;   /* inside the classifier launch */
             kfam[k] = f;
             lmk_time_next(ev[2 * k], ev[2 * k + 1]);
             rc = enqueue_kernel(m, B, f, 0, NULL);
@@ -1247,8 +1255,9 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
-            launches_per_step[f] = f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1
-                                   : fam_inside(f, chain_level(m, B)) ? 0 : m->L;
+            launches_per_step[f] = fam_inside(f, chain_level(m, B))              ? 0
+                                   : f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1
+                                                                             : m->L;
     }
     for (int i = 0; ev && i < 2 * nk; i++)
         if (ev[i]) hipEventDestroy(ev[i]);

@@ -408,9 +408,12 @@ def main():
     if launches is None:   # the chain's launch counts: one per layer, attention (Wo from
         # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once
         fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
-        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz == 3, "w2": fz == 3}
-        launches = {k: (1 if k in ("cls", "argmax") else 0 if inside.get(k) else cfg.n_layers)
+        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz == 3, "w2": fz == 3, "argmax": fz == 3}
+        launches = {k: (0 if inside.get(k) else 1 if k in ("cls", "argmax") else cfg.n_layers)
                     for k in algo}
+    if launches.get("argmax") == 0:   # the argmax runs inside the classifier launch
+        algo["cls"] += algo.pop("argmax")
+        launches.pop("argmax")
     folded = []
     for k in ("attn", "wo", "w13", "w2"):    # families that run inside the QKV launch
         if launches.get(k) == 0:

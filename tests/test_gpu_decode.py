@@ -203,7 +203,8 @@ def test_profile_chain_times_every_family(lm, fuse):
     us, n = m.profile_chain([1], [20], 6)
     L = d["n_layers"]
     assert n == {"qkv": L, "attn": 0 if fuse >= 1 else L, "wo": 0 if fuse >= 2 else L,
-                 "w13": 0 if fuse == 3 else L, "w2": 0 if fuse == 3 else L, "cls": 1, "argmax": 1}
+                 "w13": 0 if fuse == 3 else L, "w2": 0 if fuse == 3 else L, "cls": 1,
+                 "argmax": 0 if fuse == 3 else 1}
     for k in us:
         assert (us[k] > 0) == (n[k] > 0), k
         assert us[k] < 1e4, k
