@@ -34,6 +34,7 @@
     } while (0)
 
 #define MAX_GEMV_B 4
+#define PREFILL_GRAPHS 4   /* prefill chunk shapes kept captured */
 
 struct LMModel {
     Config cfg;                 /* vocab_size positive */
@@ -76,6 +77,14 @@ struct LMModel {
     /* captured decode graphs: [B][0] one step, [B][1] GRAPH_STEPS steps
      * (greedy feedback stays on the device) */
     hipGraphExec_t (*step_graph)[2];   /* [max_batch + 1][2]   */
+    /* captured prefill chunks (the layers and, with all logits, the
+     * classifier), by rows, rows per sequence and logits mode; replaced round
+     * robin */
+    struct {
+        int R, S, all;
+        hipGraphExec_t ge;
+    } pgraph[PREFILL_GRAPHS];
+    int pgraph_next;
     int use_graph;
 };
 
@@ -292,6 +301,11 @@ static int alloc_kv(LMModel *m)
 
 static void drop_graphs(LMModel *m)
 {
+    for (int i = 0; i < PREFILL_GRAPHS; i++)
+        if (m->pgraph[i].ge) {
+            hipGraphExecDestroy(m->pgraph[i].ge);
+            m->pgraph[i].ge = NULL;
+        }
     if (!m->step_graph) return;
     for (int b = 0; b <= m->max_batch; b++)
         for (int k = 0; k < 2; k++)
@@ -1044,6 +1058,43 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
  * every row's logits; LM_LOGITS_LAST: the last row of each sequence.  Host
  * `logits` (may be NULL) receives them in sequence order; the last chunk's
  * logits stay in d_logits. */
+/* The layers of a prefill chunk of R rows (sequences of S rows; tokens,
+ * positions and slots in d_rtok / d_rpos / d_rslot) and, with `all`, the
+ * classifier into d_logits: replayed from a captured graph of that shape
+ * (captured on first use) unless graphs are off. */
+static int run_rows(LMModel *m, int R, int S, int all)
+{
+    if (!m->use_graph)
+        return enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, all ? m->d_logits : NULL, all);
+    int k = 0;
+    while (k < PREFILL_GRAPHS &&
+           !(m->pgraph[k].ge && m->pgraph[k].R == R && m->pgraph[k].S == S && m->pgraph[k].all == all))
+        k++;
+    if (k == PREFILL_GRAPHS) {
+        k = m->pgraph_next;
+        m->pgraph_next = (k + 1) % PREFILL_GRAPHS;
+        if (m->pgraph[k].ge) {
+            hipGraphExecDestroy(m->pgraph[k].ge);
+            m->pgraph[k].ge = NULL;
+        }
+        hipGraph_t g;
+        HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot,
+                                    all ? m->d_logits : NULL, all);
+        hipError_t e = hipStreamEndCapture(m->stream, &g);
+        if (rc) return rc;
+        HIPCHK(e);
+        e = hipGraphInstantiateWithFlags(&m->pgraph[k].ge, g, 0);
+        hipGraphDestroy(g);
+        HIPCHK(e);
+        m->pgraph[k].R = R;
+        m->pgraph[k].S = S;
+        m->pgraph[k].all = all;
+    }
+    HIPCHK(hipGraphLaunch(m->pgraph[k].ge, m->stream));
+    return LM_OK;
+}
+
 static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, const int *tokens,
                        int S, int logits_mode, float *logits)
 {
@@ -1098,13 +1149,13 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
             break;
         }
         if (logits_mode == LM_LOGITS_ALL) {
-            rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, m->d_logits, 1);
+            rc = run_rows(m, R, S, 1);
             if (rc == LM_OK && logits &&
                 hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
                                hipMemcpyDeviceToHost, m->stream) != hipSuccess)
                 rc = LM_ERR_HIP;
         } else {
-            rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, NULL, 0);
+            rc = run_rows(m, R, S, 0);
             /* gather the last row of each sequence into d_attn (same row width) */
             if (rc == LM_OK &&
                 hipMemcpy2DAsync(m->d_attn, (size_t)m->D * 4, m->d_x + (size_t)(S - 1) * m->D,
