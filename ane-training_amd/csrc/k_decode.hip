@@ -545,6 +545,19 @@ __device__ __forceinline__ void attn_head(
             kv_raw_load(K + (size_t)p * HD, kr[i]);
             kv_raw_load(V + (size_t)p * HD, vr[i]);
         }
+        if constexpr (DB) {
+            /* waiting for the QKV work-groups of the same launch: the second
+             * tile too, so that no tile load follows the wait (a wave with one
+             * tile reads one tile of unused rows) */
+            if (qt) {
+#pragma unroll
+                for (int i = 0; i < NP; i++) {
+                    const int p = min((wv + NWAVE) * TILE + pp + PP * i, max_seq - 1);
+                    kv_raw_load(K + (size_t)p * HD, kr1[i]);
+                    kv_raw_load(V + (size_t)p * HD, vr1[i]);
+                }
+            }
+        }
         /* keeps the tile's loads ahead of the partials' (the scheduler would
          * otherwise issue them after the partials' sum, a second round trip) */
         __builtin_amdgcn_sched_barrier(0);
@@ -710,7 +723,7 @@ __device__ __forceinline__ void attn_head(
              * the loop's registers at two tiles (143 -> 109 VGPRs at hd 64).
              * The scheduling barriers keep each fetch ahead of the compute it
              * overlaps (the compiler would sink the loads to their first use). */
-            fetch(wv + NWAVE, kr1, vr1);
+            if (!qt) fetch(wv + NWAVE, kr1, vr1);
             __builtin_amdgcn_sched_barrier(0);
             if (wv < ntiles) {                                   /* wave-uniform */
                 consume(wv, kr, vr);
