@@ -267,7 +267,7 @@ __device__ __forceinline__ float tag_wait(const unsigned long long *w, unsigned 
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
-        __builtin_amdgcn_s_sleep(LM_TAG_SLEEP);
+        __builtin_amdgcn_s_sleep(1);
         v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return __builtin_bit_cast(float, (unsigned)v);
@@ -287,23 +287,16 @@ __device__ __forceinline__ float tag_take(unsigned long long v, const unsigned l
     return (unsigned)(v >> 32) == tag ? __builtin_bit_cast(float, (unsigned)v) : tag_wait(w, tag, err);
 }
 
-/* Before a work-group reads a span of words: one thread polls the span's last
- * word (most often the last written) while the others wait at the barrier, so
- * that a waiting work-group keeps one poll in flight instead of one per
- * thread.  A hint only: each word is still checked by its reader. */
-#ifndef LM_TAG_DOORBELL
-#define LM_TAG_DOORBELL 7
-#endif
-#ifndef LM_DOORBELL_SPREAD
-#define LM_DOORBELL_SPREAD 1
-#endif
+/* Before a work-group reads a span of words (the doorbell): one thread polls
+ * one word of the span while the others wait at the barrier, so that a waiting
+ * work-group keeps one poll in flight instead of one per thread; the k-th
+ * reader of a copy polls the last word of the copy's k-th 128-byte line
+ * (wrapping), so that the readers of one copy poll different lines.  A hint
+ * only: each word is still checked by its reader. */
 __device__ __forceinline__ void tag_doorbell(const unsigned long long *w, int n, int k, unsigned tag,
                                              int *err)
 {
-    /* the k-th reader of a copy polls the last word of the k-th 128-byte line
-     * (wrapping), so that the readers of one copy poll different lines */
-    const int i = LM_DOORBELL_SPREAD ? (k * 16 + 15) % n : n - 1;
-    if (threadIdx.x == 0) (void)tag_wait(w + i, tag, err);
+    if (threadIdx.x == 0) (void)tag_wait(w + (k * 16 + 15) % n, tag, err);
     __syncthreads();
 }
 
@@ -841,7 +834,7 @@ __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__rest
     }
     const unsigned tag = qkv_tag(tg);
     const unsigned long long *tac = tg.ta + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * NQ;
-    if (LM_TAG_DOORBELL & 1) tag_doorbell(tac, B * D, a / LM_TA_COPIES, tag, tg.err);
+    tag_doorbell(tac, B * D, a / LM_TA_COPIES, tag, tg.err);
     tag_wait_span(tac, B * D, tag, tg.err, xs);
     __syncthreads();
     if (p >= wpairs) return;
@@ -894,7 +887,7 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
     /* each thread's words are the elements tid + j*WG of each row, which are
      * also the ones it normalises: no barrier between the two */
     const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D;
-    if (LM_TAG_DOORBELL & 2) tag_doorbell(txc, B * D, a / LM_TX_COPIES, tag, tg.err);
+    tag_doorbell(txc, B * D, a / LM_TX_COPIES, tag, tg.err);
     tag_wait_span(txc, B * D, tag, tg.err, xs);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -954,7 +947,7 @@ __device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__rest
     const unsigned tag = qkv_tag(tg);
     const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D + r;
     const unsigned long long *tgc = tg.tgt + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * F;
-    if (LM_TAG_DOORBELL & 4) tag_doorbell(tgc, B * F, a / LM_TA_COPIES, tag, tg.err);
+    tag_doorbell(tgc, B * F, a / LM_TA_COPIES, tag, tg.err);
     /* x' of this row pair (written before any gate word) with the gate */
     unsigned long long v0[NB], v1[NB];
 #pragma unroll
@@ -1010,11 +1003,8 @@ struct FfnArgs {
  * launch; the QKV and Wo work-groups read x before they store any word, and x
  * is written only after every word of every head, so no read of x in the
  * launch sees the value written in it. */
-#ifndef LM_QA_WAVES
-#define LM_QA_WAVES 1
-#endif
 template <int D, int NB, typename KT, int HD, bool WO, int F>
-__global__ void __launch_bounds__(WG, LM_QA_WAVES) k_qkv_attn(
+__global__ void __launch_bounds__(WG) k_qkv_attn(
     float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
     const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV,
     const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,

@@ -65,9 +65,6 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 #ifndef LM_TA_COPIES
 #define LM_TA_COPIES 4
 #endif
-#ifndef LM_TAG_SLEEP
-#define LM_TAG_SLEEP 1
-#endif
 #ifndef LM_TX_COPIES
 #define LM_TX_COPIES 4
 #endif
