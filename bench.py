@@ -192,6 +192,28 @@ def reference_algorithm_gpu(S, cfg, w16, ids, n_tokens=48):
                       f"classifier) + logits to the host + host argmax, wall clock"}
 
 
+def c0_kv16(S, cfg, w16, ids, direct, seqs=8):
+    """C0 with the binary16 K/V cache (north_star's storage; the headline uses
+    the reference forward's fp32 K/V): tok/s over `seqs` timed 256-token greedy
+    sequences after one untimed, and the first step whose id differs from the
+    fp32-cache run (a near tie that the cache rounding flips), if any."""
+    m = S.Model.create(cfg, w16, True, 1, SEQ)
+    if direct:
+        m.set_option(S.LM_OPT_USE_GRAPH, 0)
+    got = m.generate_greedy([1], [0], SEQ)[:, 0]
+    m.sync()
+    m.timer_begin()
+    for _ in range(seqs):
+        m.generate_greedy([1], [0], SEQ)
+    ms = m.timer_end()
+    m.close()
+    diff = np.nonzero(np.asarray(got) != np.asarray(ids))[0]
+    return {"value": round(seqs * SEQ / (ms / 1e3), 1), "unit": "tok/s",
+            "us_per_token": round(ms * 1e3 / (seqs * SEQ), 3),
+            "first_id_differing_from_fp32_cache": int(diff[0]) if diff.size else None,
+            "sample": f"{seqs} timed 256-token greedy sequences from token id 1"}
+
+
 MFMA_PEAK_TFLOPS = 2500.0      # dense fp16
 
 
@@ -463,6 +485,8 @@ def main():
         out["configs"] = bench_extra(S, w16, direct=args.direct)
         ra = reference_algorithm_gpu(S, cfg, w16, ids)
         out["configs"]["c0_reference_algorithm"] = ra
+        if not args.kv16:
+            out["configs"]["c0_kv16"] = c0_kv16(S, cfg, w16, ids, args.direct)
         out["vs_baseline_same_algorithm"] = round(ra["value"] / REF_TOK_S, 1)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg.astuple(), w16, S, ids, args.cpu_seconds)
