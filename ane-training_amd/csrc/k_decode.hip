@@ -253,17 +253,20 @@ __device__ __forceinline__ void tag_store(unsigned long long *w, float v, unsign
 }
 
 /* Poll one tagged word until it carries `tag` (bounded: a wait that gives up
- * sets *err and returns the word's value as it is).  A wait also stops early
- * once *err is set, so that after one wait has given up the rest of the
- * launch, and the launches queued behind it, end within microseconds; the
- * host reads the flag after the step and reports the failure. */
+ * after err[1] polls sets err[0] and returns the word's value as it is).  A
+ * wait also stops early once err[0] is set, so that after one wait has given
+ * up the rest of the launch, and the launches queued behind it, end within
+ * microseconds; the host reads the flag after the step and reports the
+ * failure. */
 __device__ __forceinline__ float tag_wait(const unsigned long long *w, unsigned tag, int *err)
 {
     unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((unsigned)(v >> 32) == tag) return __builtin_bit_cast(float, (unsigned)v);
+    const int lim = err[1];
     for (int spin = 0; (unsigned)(v >> 32) != tag; spin++) {
         if ((spin & 255) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
             break;
-        if (spin == (1 << 20)) {
+        if (spin >= lim) {
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }

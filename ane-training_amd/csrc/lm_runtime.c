@@ -497,10 +497,14 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     const size_t ncls = (size_t)2 * LM_TAG_B * m->cls_nblk;
     if ((st = dev_alloc((void **)&m->d_cls_tw, ncls * 8))) goto fail;
     if ((st = dev_alloc((void **)&m->d_epoch, 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_err, 4))) goto fail;
+    if ((st = dev_alloc((void **)&m->d_err, 8))) goto fail;   /* flag, poll limit */
     if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_cls_tw, 0, ncls * 8) != hipSuccess ||
         hipMemset(m->d_epoch, 0, 4) != hipSuccess || hipMemset(m->d_err, 0, 4) != hipSuccess)
         FAIL(LM_ERR_HIP);
+    {
+        const int spins = LM_HANDOFF_SPINS;
+        if (hipMemcpy(m->d_err + 1, &spins, 4, hipMemcpyHostToDevice) != hipSuccess) FAIL(LM_ERR_HIP);
+    }
     m->fuse_qa = 3;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
@@ -620,6 +624,11 @@ int lm_set_option(LMModel *m, int option, int value)
         HIPCHK(hipStreamSynchronize(m->stream));
         drop_graphs(m);
         m->fuse_qa = value;
+        return LM_OK;
+    case LM_OPT_HANDOFF_SPINS:
+        if (value < 1) return LM_ERR_INVALID;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(hipMemcpy(m->d_err + 1, &value, 4, hipMemcpyHostToDevice));
         return LM_OK;
     case LM_OPT_KV_F32:
         if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
@@ -923,7 +932,7 @@ static int queue_err_read(LMModel *m)
 static int check_err(LMModel *m)
 {
     if (!*err_slot(m)) return LM_OK;
-    fprintf(stderr, "stories_lm: a QKV -> attention hand-off wait gave up (results invalid)\n");
+    fprintf(stderr, "stories_lm: a hand-off wait inside a fused launch gave up (results invalid)\n");
     *err_slot(m) = 0;
     HIPCHK(hipMemset(m->d_err, 0, 4));
     return LM_ERR_HIP;

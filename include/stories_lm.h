@@ -250,6 +250,10 @@ int lm_timer_end(LMModel *m, float *ms);
  * QKV, attention and Wo as one launch and the FFN as two; 1 also launches Wo
  * apart; 0 launches all five apart. */
 #define LM_OPT_FUSE_QKV_ATTN 5
+/* LM_OPT_HANDOFF_SPINS: polls after which a wait for a tagged hand-off word
+ * inside a fused launch gives up (default 1 << 20, about a second); the call
+ * then returns LM_ERR_HIP.  For tests of that path; >= 1. */
+#define LM_OPT_HANDOFF_SPINS 6
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------
