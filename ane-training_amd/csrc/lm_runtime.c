@@ -619,7 +619,7 @@ int lm_set_option(LMModel *m, int option, int value)
         m->use_graph = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_FUSE_QKV_ATTN:
-        if (value < 0 || value > 3) return LM_ERR_INVALID;
+        if (value < 0 || value > 4) return LM_ERR_INVALID;
         if (value == m->fuse_qa) return LM_OK;
         HIPCHK(hipStreamSynchronize(m->stream));
         drop_graphs(m);
@@ -655,12 +655,17 @@ int lm_set_option(LMModel *m, int option, int value)
         }                                                                             \
     } while (0)
 
-/* The decode chain's fusion level for B rows: fuse_qa, except that the
- * whole-layer launch (3) is built only for the (dim, hidden) pairs and batches
- * lmk_layer_fusable names; level 2 runs elsewhere. */
+/* The decode chain's fusion level for B rows: fuse_qa, where 3 takes the
+ * whole-layer launch for one row only (B = 2 and 4 ran faster at level 2:
+ * 203 and 281 us/step against 207 and 385) and 4 takes it for every batch;
+ * the whole-layer launch is built only for the (dim, hidden) pairs and
+ * batches lmk_layer_fusable names, and level 2 runs elsewhere. */
 static int chain_level(const LMModel *m, int B)
 {
-    return m->fuse_qa == 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : m->fuse_qa;
+    int lvl = m->fuse_qa;
+    if (lvl == 3 && B > 1) lvl = 2;
+    if (lvl == 4) lvl = 3;
+    return lvl == 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : lvl;
 }
 
 /* Whether kernel family fam runs inside another family's launch at fusion

@@ -362,7 +362,7 @@ def main():
     ap.add_argument("--steps", type=int, default=32, help="timed 256-token C0 sequences")
     ap.add_argument("--warmup", type=int, default=2, help="untimed 256-token C0 sequences")
     ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
-    ap.add_argument("--fuse", type=int, choices=[0, 1, 2, 3], default=None,
+    ap.add_argument("--fuse", type=int, choices=[0, 1, 2, 3, 4], default=None,
                     help="LM_OPT_FUSE_QKV_ATTN for the C0 chain (A/B; default: the library's)")
     ap.add_argument("--kv16", action="store_true",
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
@@ -430,7 +430,7 @@ def main():
     if launches is None:   # the chain's launch counts: one per layer, attention (Wo from
         # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once
         fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
-        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz == 3, "w2": fz == 3, "argmax": fz == 3}
+        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz >= 3, "w2": fz >= 3, "argmax": fz >= 3}
         launches = {k: (0 if inside.get(k) else 1 if k in ("cls", "argmax") else cfg.n_layers)
                     for k in algo}
     if launches.get("argmax") == 0:   # the argmax runs inside the classifier launch

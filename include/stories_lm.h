@@ -242,13 +242,15 @@ int lm_timer_end(LMModel *m, float *ms);
  * K and V in fp32, training/forward.h:118-128), 0 (default) in binary16.
  * Changing it reallocates and clears the cache of every slot. */
 #define LM_OPT_KV_F32      3
-/* LM_OPT_FUSE_QKV_ATTN: 3 (default) runs each layer of the batch 1-4 decode
+/* LM_OPT_FUSE_QKV_ATTN: 3 (default) runs each layer of the batch-1 decode
  * chain as one launch: QKV GEMV, the attention of every head, Wo + residual,
  * W1/W3 + gate and W2 + residual, each set of work-groups handing its
- * results to the next through tagged words in memory (where the whole-layer
- * form is not built for the model's widths and batch, level 2 runs); 2 runs
- * QKV, attention and Wo as one launch and the FFN as two; 1 also launches Wo
- * apart; 0 launches all five apart. */
+ * results to the next through tagged words in memory, and folds the argmax
+ * into the classifier's launch; batches of 2-4 run level 2 (faster there).
+ * 4 takes the whole-layer launch for every batch of 1-4.  Where the
+ * whole-layer form is not built for the model's widths and batch, level 2
+ * runs.  2 runs QKV, attention and Wo as one launch and the FFN as two; 1
+ * also launches Wo apart; 0 launches all five apart. */
 #define LM_OPT_FUSE_QKV_ATTN 5
 /* LM_OPT_HANDOFF_SPINS: polls after which a wait for a tagged hand-off word
  * inside a fused launch gives up (default 1 << 20, about a second); the call
