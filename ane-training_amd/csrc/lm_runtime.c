@@ -63,9 +63,10 @@ struct LMModel {
     /* per-slot greedy state */
     int *d_tok, *d_pos, *d_hist, *d_slot_id;
     /* batch 1-4 chain: QKV, attention (fuse_qa >= 1), Wo (>= 2) and the FFN
-     * (3) in one launch, handing q, k, v, the head outputs, x and the gate
-     * over through tagged words; the decode-step count that tags them; the
-     * flag a hand-off wait that gives up sets */
+     * (3 at one row, 4 at every batch; chain_level) in one launch, handing q,
+     * k, v, the head outputs, x and the gate over through tagged words; the
+     * decode-step count that tags them; the flag a hand-off wait that gives up
+     * sets, and the polls before one does */
     int fuse_qa;
     unsigned long long *d_tagged;
     unsigned long long *d_cls_tw;     /* the classifier's argmax partials as tagged words (level 3) */
