@@ -235,8 +235,6 @@ struct QkvTagged {
                                      * LM_TX_COPIES copies LM_TAG_B*D apart */
     unsigned long long *tgt;        /* gate g [b*F + i] (FFN in the launch), copies
                                      * LM_TAG_B*F apart */
-    unsigned long long *txx;        /* x after W2 [b*D + i] (whole-token launch), in
-                                     * LM_TXX_COPIES copies LM_TAG_B*D apart */
     const unsigned *epoch;
     int layer, n_layers;
     int *err;                       /* set when a hand-off wait gives up */
@@ -321,84 +319,25 @@ __device__ __forceinline__ void tag_wait_span(const unsigned long long *w, int n
     }
 }
 
-/* xs holds rows 0..B-1 of K raw values, element i of row b written by thread
- * (b*K + i) % WG (as tag_wait_span leaves them; K is a multiple of WG, so each
- * thread normalises the elements it wrote and needs no barrier first):
- * normalised in place exactly as norm_to_lds does (the same sums in the same
- * order), rows B..NB-1 set to zero; w holds the gains of this thread's
- * columns. */
-template <int K, int NB>
-__device__ __forceinline__ void norm_lds_inplace(float *xs, int B, const float (&w)[K / WG])
-{
-    constexpr int PER = K / WG;
-    __shared__ float red[NB][NWAVE];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float ss = 0.f;
-        if (b < B) {
-#pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const float v = xs[b * K + tid + j * WG];
-                ss = fmaf(v, v, ss);
-            }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) red[b][wv] = ss;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float tot = 0.f;
-#pragma unroll
-        for (int k = 0; k < NWAVE; k++) tot += red[b][k];
-        const float scale = 1.0f / sqrtf(tot / K + 1e-5f);
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            float *e = xs + b * K + tid + j * WG;
-            *e = b < B ? *e * scale * w[j] : 0.f;
-        }
-    }
-    __syncthreads();
-}
-
-/* Where the input rows of a QKV work-group of the whole-token launch come
- * from after layer 0: copy `words` of the tagged x that the previous layer's
- * W2 work-groups wrote with `tag`; `k` is this reader's index among the
- * copy's readers (its doorbell line).  words == NULL: not from words. */
-struct XWords {
-    const unsigned long long *words;
-    unsigned tag;
-    int k;
-};
-
 /* Rows of [Wq; Wk; Wv] . rmsnorm(x[b]) for the row pairs of this work-group,
  * RoPE'd and stored (q fp32, k/v into the cache); with tg, also as tagged
- * hand-off words.  wgi: the work-group's index among the QKV work-groups
- * (blockIdx.x when negative); xw: the input rows come from tagged words
- * instead of x. */
+ * hand-off words. */
 template <int D, int NB, typename KT>
 __device__ __forceinline__ void qkv_rows(
     float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok,
     const float *__restrict__ rms_w, const u16 *__restrict__ W, int NQ, int NKV, int hd,
     const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
     int B, float *__restrict__ q, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq,
-    int npairs, const QkvTagged *tg, bool store_x = true, int wgi = -1,
-    XWords xw = XWords{nullptr, 0u, 0})
+    int npairs, const QkvTagged *tg, bool store_x = true)
 {
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
-    const int p = (wgi < 0 ? (int)blockIdx.x : wgi) * NWAVE + (threadIdx.x >> 6);
+    const int p = blockIdx.x * NWAVE + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
     const int r = 2 * min(p, npairs - 1);
     uint4 wv[D / 256];
     hw_load<D>(W + (size_t)(r + half) * D, hl, wv);
     NormIn<D, NB> in;
-    if (xw.words) {
-#pragma unroll
-        for (int j = 0; j < D / WG; j++) in.w[j] = rms_w[threadIdx.x + j * WG];
-    } else {
-        norm_load<D, NB>(x, emb, tok, rms_w, B, in);
-    }
+    norm_load<D, NB>(x, emb, tok, rms_w, B, in);
     /* epilogue operands: position and rotation of this row pair per sequence */
     const int half_hd = hd >> 1;
     const bool rot = r < NQ + NKV;
@@ -412,13 +351,7 @@ __device__ __forceinline__ void qkv_rows(
         cr[b] = rot ? rc[ti] : 1.f;
         sr[b] = rot ? rs[ti] : 0.f;
     }
-    if (xw.words) {
-        tag_doorbell(xw.words, B * D, xw.k, xw.tag, tg->err);
-        tag_wait_span(xw.words, B * D, xw.tag, tg->err, xs);
-        norm_lds_inplace<D, NB>(xs, B, in.w);
-    } else {
-        norm_to_lds<D, NB>(in, B, x, emb != nullptr && store_x, xs);
-    }
+    norm_to_lds<D, NB>(in, B, x, emb != nullptr && store_x, xs);
     if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
@@ -882,8 +815,7 @@ __global__ void __launch_bounds__(WG) k_attn_decode_part(
 template <int D, int NB, int F>
 __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__restrict__ emb,
                                         const int *__restrict__ tok, const u16 *__restrict__ Wo,
-                                        int B, int NQ, const QkvTagged &tg, int a, float *xs,
-                                        XWords xw = XWords{nullptr, 0u, 0})
+                                        int B, int NQ, const QkvTagged &tg, int a, float *xs)
 {
     const int p = a * NWAVE + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
@@ -892,7 +824,6 @@ __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__rest
     uint4 wv[D / 256];
     hw_load<D>(Wo + (size_t)(r + half) * D, hl, wv);
     float2 xo[NB];
-    unsigned long long x0[NB], x1[NB];   /* the residual's words (xw) */
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         if (b >= B) {
@@ -900,9 +831,6 @@ __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__rest
         } else if (emb) {
             const u16 *er = emb + (size_t)tok[b] * D + r;
             xo[b] = make_float2(h2f(er[0]), h2f(er[1]));
-        } else if (xw.words) {
-            x0[b] = tag_peek(xw.words + (size_t)b * D + r);
-            x1[b] = tag_peek(xw.words + (size_t)b * D + r + 1);
         } else {
             xo[b] = *(const float2 *)(x + (size_t)b * D + r);
         }
@@ -911,15 +839,6 @@ __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__rest
     const unsigned long long *tac = tg.ta + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * NQ;
     tag_doorbell(tac, B * D, a / LM_TA_COPIES, tag, tg.err);
     tag_wait_span(tac, B * D, tag, tg.err, xs);
-    if (xw.words && !emb) {
-        /* every word of x was written before any head output this work-group
-         * has read, so these seldom wait */
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-            if (b < B)
-                xo[b] = make_float2(tag_take(x0[b], xw.words + (size_t)b * D + r, xw.tag, tg.err),
-                                    tag_take(x1[b], xw.words + (size_t)b * D + r + 1, xw.tag, tg.err));
-    }
     __syncthreads();
     if (p >= wpairs) return;
     float acc[NB], r0[NB], r1[NB];
@@ -955,6 +874,7 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
                                          int B, const QkvTagged &tg, int a, float *xs)
 {
     constexpr int PER = D / WG;
+    __shared__ float red[NB][NWAVE];
     const int tid = threadIdx.x, wv_ = tid >> 6;
     const int i0 = a * NWAVE + wv_;
     const int i = min(i0, F - 1);
@@ -972,7 +892,33 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
     const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D;
     tag_doorbell(txc, B * D, a / LM_TX_COPIES, tag, tg.err);
     tag_wait_span(txc, B * D, tag, tg.err, xs);
-    norm_lds_inplace<D, NB>(xs, B, w);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float ss = 0.f;
+        if (b < B) {
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const float v = xs[b * D + tid + j * WG];
+                ss = fmaf(v, v, ss);
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[b][wv_] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < NWAVE; k++) tot += red[b][k];
+        const float scale = 1.0f / sqrtf(tot / D + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            float *e = xs + b * D + tid + j * WG;
+            *e = b < B ? *e * scale * w[j] : 0.f;
+        }
+    }
+    __syncthreads();
     if (i0 >= F) return;
     float acc[NB], h1[NB], h3[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
@@ -993,8 +939,7 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
  * W2[r..r+1, :] . g[b], g from copy a % LM_TA_COPIES of its tagged words. */
 template <int D, int NB, int F>
 __device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__restrict__ W2, int B,
-                                        const QkvTagged &tg, int a, float *xs, bool x_words = false,
-                                        bool x_plain = true)
+                                        const QkvTagged &tg, int a, float *xs)
 {
     const int p = a * NWAVE + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
@@ -1026,47 +971,12 @@ __device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__rest
     float acc[NB], r0[NB], r1[NB];
     hw_dot<F, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
-    if (x_plain && lane == 0) {
+    if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
             *(float2 *)(x + (size_t)b * D + r) = make_float2(xo[b].x + r0[b], xo[b].y + r1[b]);
         }
-    }
-    if (x_words && lane < LM_TXX_COPIES) {
-        /* the whole-token launch: x on to the next layer (or the classifier)
-         * in every copy of its tagged words */
-        unsigned long long *dst = tg.txx + (size_t)lane * LM_TAG_B * D + r;
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            if (b >= B) break;
-            tag_store(dst + (size_t)b * D, xo[b].x + r0[b], tag);
-            tag_store(dst + (size_t)b * D + 1, xo[b].y + r1[b], tag);
-        }
-    }
-}
-
-/* Attention role of k_qkv_attn, work-group a of the role: head h = a % H of
- * row b = a / H, its output on as tagged words (WO: to the Wo role, in
- * LM_TA_COPIES copies) or to out[b, h*HD ..] (fp32). */
-template <int HD, typename KT, bool WO>
-__device__ __forceinline__ void attn_role(const KT *__restrict__ kc, const KT *__restrict__ vc,
-                                          const int *__restrict__ pos, int NQ, int NKV, int max_seq,
-                                          int H, const QkvTagged &tg, int a, float *__restrict__ out)
-{
-    __shared__ float oh[HD];
-    const int h = a % H, b = a / H;
-    attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
-    if constexpr (WO) {
-        /* every copy of the head output, the work-group's threads taking
-         * (element, copy) pairs */
-        const unsigned tag = qkv_tag(tg);
-        for (int t = threadIdx.x; t < HD * LM_TA_COPIES; t += WG) {
-            const int e = t % HD, c = t / HD;
-            tag_store(tg.ta + (size_t)c * LM_TAG_B * NQ + (size_t)b * NQ + h * HD + e, oh[e], tag);
-        }
-    } else if ((int)threadIdx.x < HD) {
-        out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
     }
 }
 
@@ -1113,7 +1023,20 @@ __global__ void __launch_bounds__(WG) k_qkv_attn(
     }
     int a = blockIdx.x - nprod;
     if (!WO || a < H * B) {
-        attn_role<HD, KT, WO>(kc, vc, pos, NQ, NKV, max_seq, H, tg, a, out);
+        __shared__ float oh[HD];
+        const int h = a % H, b = a / H;
+        attn_head<HD, KT>(nullptr, kc, vc, pos, nullptr, H, NKV / HD, max_seq, oh, h, b, nullptr, &tg);
+        if constexpr (WO) {
+            /* every copy of the head output, the work-group's threads taking
+             * (element, copy) pairs */
+            const unsigned tag = qkv_tag(tg);
+            for (int t = threadIdx.x; t < HD * LM_TA_COPIES; t += WG) {
+                const int e = t % HD, c = t / HD;
+                tag_store(tg.ta + (size_t)c * LM_TAG_B * NQ + (size_t)b * NQ + h * HD + e, oh[e], tag);
+            }
+        } else if ((int)threadIdx.x < HD) {
+            out[(size_t)b * H * HD + h * HD + threadIdx.x] = oh[threadIdx.x];
+        }
         return;
     }
     if constexpr (WO) {
@@ -1310,22 +1233,21 @@ __device__ __forceinline__ void cls_argmax_fold(const ArgFold &f, int nblk, int 
     if (threadIdx.x == 0) *f.epoch += 1u;   /* the next step's hand-off tags */
 }
 
-/* Classifier work-group blk of nblk (rows blk*CLS_ROWS_PER_WG ..): logits,
- * and the argmax partial of each row b to part[b*nblk + blk] or, with
- * fold.tw, as tagged words; the input rows from x, or from tagged words (xw,
- * the whole-token launch). */
 template <int D, int NB>
-__device__ __forceinline__ void cls_rows(
-    const float *__restrict__ x, XWords xw, const float *__restrict__ rms_w,
-    const u16 *__restrict__ W, int V, int B, float *__restrict__ logits,
-    LMArgPart *__restrict__ part, const ArgFold &fold, int blk, int nblk)
+__global__ void __launch_bounds__(WG) k_cls(
+    const float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W,
+    int V, int B, float *__restrict__ logits, LMArgPart *__restrict__ part, ArgFold fold)
 {
+    if (fold.tw && blockIdx.x == gridDim.x - 1) {
+        cls_argmax_fold(fold, gridDim.x - 1, B);
+        return;
+    }
     const unsigned ftag = fold.tw ? *fold.epoch + 1u : 0u;
     __shared__ __attribute__((aligned(16))) float xs[NB * D];
     __shared__ float bvs[NB][NWAVE];
     __shared__ int bis[NB][NWAVE];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
-    const int row0 = blk * CLS_ROWS_PER_WG + wv * 2 * CLS_PAIRS_PER_WAVE;
+    const int row0 = blockIdx.x * CLS_ROWS_PER_WG + wv * 2 * CLS_PAIRS_PER_WAVE;
     uint4 wr[CLS_PAIRS_PER_WAVE][D / 256];
 #pragma unroll
     for (int pp = 0; pp < CLS_PAIRS_PER_WAVE; pp++) {
@@ -1333,16 +1255,8 @@ __device__ __forceinline__ void cls_rows(
         hw_load<D>(W + (size_t)rl * D, hl, wr[pp]);
     }
     NormIn<D, NB> in;
-    if (xw.words) {
-#pragma unroll
-        for (int j = 0; j < D / WG; j++) in.w[j] = rms_w[threadIdx.x + j * WG];
-        tag_doorbell(xw.words, B * D, xw.k, xw.tag, fold.err);
-        tag_wait_span(xw.words, B * D, xw.tag, fold.err, xs);
-        norm_lds_inplace<D, NB>(xs, B, in.w);
-    } else {
-        norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
-        norm_to_lds<D, NB>(in, B, nullptr, false, xs);
-    }
+    norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
+    norm_to_lds<D, NB>(in, B, nullptr, false, xs);
     float bv[NB];
     int bi[NB];
 #pragma unroll
@@ -1383,129 +1297,14 @@ __device__ __forceinline__ void cls_rows(
         int id = bis[b][0];
         for (int w = 1; w < NWAVE; w++) argmax_combine(v, id, bvs[b][w], bis[b][w]);
         if (fold.tw) {
-            tag_store(fold.tw + (size_t)b * nblk + blk, v, ftag);
-            tag_store(fold.tw + (size_t)(LM_TAG_B + b) * nblk + blk, __builtin_bit_cast(float, id), ftag);
+            const int nblk = gridDim.x - 1;
+            tag_store(fold.tw + (size_t)b * nblk + blockIdx.x, v, ftag);
+            tag_store(fold.tw + (size_t)(LM_TAG_B + b) * nblk + blockIdx.x,
+                      __builtin_bit_cast(float, id), ftag);
         } else {
-            part[(size_t)b * nblk + blk] = LMArgPart{v, id};
+            part[(size_t)b * gridDim.x + blockIdx.x] = LMArgPart{v, id};
         }
     }
-}
-
-template <int D, int NB>
-__global__ void __launch_bounds__(WG) k_cls(
-    const float *__restrict__ x, const float *__restrict__ rms_w, const u16 *__restrict__ W,
-    int V, int B, float *__restrict__ logits, LMArgPart *__restrict__ part, ArgFold fold)
-{
-    const int nblk = fold.tw ? (int)gridDim.x - 1 : (int)gridDim.x;
-    if (fold.tw && (int)blockIdx.x == nblk) {
-        cls_argmax_fold(fold, nblk, B);
-        return;
-    }
-    cls_rows<D, NB>(x, XWords{nullptr, 0u, 0}, rms_w, W, V, B, logits, part, fold, blockIdx.x, nblk);
-}
-
-/* ---- the whole decode step in one launch ------------------------------------- */
-
-/* Per-layer operands of k_token and its classifier. */
-struct TokenArgs {
-    const u16 *layers;                  /* layer l at layers + l * layer_elems */
-    size_t layer_elems, off_wo, off_w13, off_w2;
-    const float *rms_att, *rms_ffn;     /* [L][D] */
-    size_t kv_layer;                    /* cache elements per layer */
-    int L;
-    const float *rms_final;
-    const u16 *wcls;
-    int V, nblk;                        /* classifier rows, its work-groups */
-    float *logits;                      /* may be NULL */
-};
-
-/* One decode step of B rows in one launch: for l = 0 .. L-1 the work-groups of
- * k_qkv_attn's whole-layer form for layer l (QKV, attention, Wo, W1/W3, W2),
- * then nblk classifier work-groups and the argmax reducer (k_cls with the
- * fold).  Layer l's W2 work-groups hand x on as tagged words (tag of layer l,
- * LM_TXX_COPIES copies) to layer l+1's QKV and Wo work-groups, or after the
- * last layer to the classifier; layer 0 starts from the embedding rows.
- * Every work-group waits only for work-groups before it in dispatch order (a
- * layer's roles as in k_qkv_attn; layer l+1's first roles and the classifier
- * for the W2 work-groups of the layer before), so the waits end however many
- * work-groups the device holds at once, and the work-groups dispatched while
- * earlier ones wait load their weights ahead: the next layer's QKV weights
- * stream in while the current layer's FFN runs.  Each hand-off buffer is
- * rewritten by layer l+1 only after every reader of layer l's words has
- * handed its own result on (every role reads all of the previous role's
- * words), so no word is overwritten before it is read, and every word carries
- * its layer's tag.  The reducer, last, advances *epoch after every other
- * work-group has read it. */
-template <int D, int NB, typename KT, int HD, int F>
-__global__ void __launch_bounds__(WG) k_token(
-    float *__restrict__ x, const u16 *__restrict__ emb, const int *__restrict__ tok, int NQ,
-    int NKV, const float *__restrict__ rc, const float *__restrict__ rs, const int *__restrict__ pos,
-    int B, KT *__restrict__ kc, KT *__restrict__ vc, int max_seq, int npairs, int nprod, int H,
-    QkvTagged tg, TokenArgs ta, ArgFold fold)
-{
-    static_assert(LM_TXX_COPIES <= 64, "a wave's lanes store the copies");
-    constexpr int NWO = (D / 2 + NWAVE - 1) / NWAVE;
-    constexpr int N13 = (F + NWAVE - 1) / NWAVE;
-    const int per = nprod + H * B + 2 * NWO + N13;
-    const int bid = blockIdx.x;
-    const unsigned tag0 = *tg.epoch * (unsigned)ta.L + 1u;   /* the tag of layer 0 */
-    if (bid >= ta.L * per) {
-        const int c = bid - ta.L * per;
-        if (c == ta.nblk) {
-            cls_argmax_fold(fold, ta.nblk, B);
-            return;
-        }
-        const XWords xw = {tg.txx + (size_t)(c % LM_TXX_COPIES) * LM_TAG_B * D,
-                           tag0 + (unsigned)ta.L - 1u, c / LM_TXX_COPIES};
-        cls_rows<D, NB>(nullptr, xw, ta.rms_final, ta.wcls, ta.V, B, ta.logits, nullptr, fold, c,
-                        ta.nblk);
-        return;
-    }
-    const int l = bid / per;
-    int a = bid - l * per;
-    QkvTagged t = tg;
-    t.layer = l;
-    const u16 *lw = ta.layers + (size_t)l * ta.layer_elems;
-    KT *kcl = kc + (size_t)l * ta.kv_layer, *vcl = vc + (size_t)l * ta.kv_layer;
-    const u16 *embl = l == 0 ? emb : nullptr;
-    /* after layer 0, x comes from the previous layer's W2 work-groups */
-    const unsigned xtag = tag0 + (unsigned)l - 1u;
-    if (a < nprod) {
-        const XWords xw = {l ? tg.txx + (size_t)(a % LM_TXX_COPIES) * LM_TAG_B * D : nullptr, xtag,
-                           a / LM_TXX_COPIES};
-        qkv_rows<D, NB, KT>(x, embl, tok, ta.rms_att + (size_t)l * D, lw, NQ, NKV, HD, rc, rs, pos, B,
-                            nullptr, kcl, vcl, max_seq, npairs, &t, false, a, xw);
-        return;
-    }
-    a -= nprod;
-    if (a < H * B) {
-        attn_role<HD, KT, true>(kcl, vcl, pos, NQ, NKV, max_seq, H, t, a, nullptr);
-        return;
-    }
-    a -= H * B;
-    constexpr int ROW = F > D ? F : D;
-    __shared__ __attribute__((aligned(16))) float xs[NB * ROW];
-    if (l > 0) {
-        /* The Wo, W1/W3 and W2 work-groups of a layer after the first issue
-         * their weight loads only once the layer's input x has arrived.
-         * Issued on dispatch, while the previous layer still runs, those
-         * 10.6 MB slowed that layer's hand-offs by more than the early loads
-         * gained (device timestamps: 12.2 us per layer gated against 12.8
-         * with the per-layer launch; ungated the step was slower than that). */
-        tag_doorbell(tg.txx + (size_t)(a % LM_TXX_COPIES) * LM_TAG_B * D, B * D, a / LM_TXX_COPIES, xtag,
-                     tg.err);
-    }
-    if (a < NWO) {
-        const XWords xw = {l ? tg.txx + (size_t)(a % LM_TXX_COPIES) * LM_TAG_B * D : nullptr, xtag, 0};
-        wo_role<D, NB, F>(x, embl, tok, lw + ta.off_wo, B, NQ, t, a, xs, xw);
-        return;
-    }
-    a -= NWO;
-    if (a < N13) {
-        w13_role<D, NB, F>(ta.rms_ffn + (size_t)l * D, lw + ta.off_w13, B, t, a, xs);
-        return;
-    }
-    w2_role<D, NB, F>(x, lw + ta.off_w2, B, t, a - N13, xs, true, l == ta.L - 1);
 }
 
 /* Work-group b reduces the nblk argmax partials of row b: tok[b] = argmax
@@ -1660,7 +1459,7 @@ extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const 
     unsigned long long *tx = ta + (size_t)LM_TA_COPIES * LM_TAG_B * NQ;
     unsigned long long *tgt = tx + (size_t)LM_TX_COPIES * LM_TAG_B * D;
     const QkvTagged tg = {tagged, tagged + (size_t)LM_TAG_B * NQ, tagged + (size_t)LM_TAG_B * (NQ + NKV),
-                          ta, tx, tgt, nullptr, epoch, layer, n_layers, err};
+                          ta, tx, tgt, epoch, layer, n_layers, err};
     const FfnArgs ffn = {rms_ffn, (const u16 *)w13, (const u16 *)w2};
 #define LAUNCH_QA(HD_, KT_, WO_, F_)                                                                \
     DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_, F_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv, \
@@ -1687,48 +1486,6 @@ extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const 
     }
 #undef LAUNCH_QA_KV
 #undef LAUNCH_QA
-    return hipGetLastError();
-}
-
-extern "C" int lmk_token(hipStream_t s, float *x, const uint16_t *emb, int *tok, const float *rms_att,
-                         const float *rms_ffn, const uint16_t *layers, size_t layer_elems,
-                         size_t off_wo, size_t off_w13, size_t off_w2, int D, int NQ, int NKV, int hd,
-                         int F, int L, const float *rope_cos, const float *rope_sin, int *pos, int B,
-                         void *kc, void *vc, size_t kv_layer, int kv_f32, int max_seq, int H,
-                         unsigned long long *tagged, unsigned *epoch, int *err,
-                         const float *rms_final, const uint16_t *wcls, int V, float *logits,
-                         unsigned long long *fold_tw, int *hist, int hist_stride)
-{
-    if (B != 1 || L < 1 || V < 1 || NQ != D || H < 1 || NQ != H * hd || NKV % hd ||
-        H % (NKV / hd) || (hd != 64 && hd != 128) || F < 1 || F % LMK_GATE_BLOCK || !emb || !tok ||
-        !pos || !layers || !rms_att || !rms_ffn || !rms_final || !wcls || !tagged || !epoch || !err ||
-        !fold_tw || !kc || !vc || !lmk_layer_fusable(D, F, B))
-        return hipErrorInvalidValue;
-    const int npairs = (NQ + 2 * NKV) / 2;
-    const int nprod = (npairs + NWAVE - 1) / NWAVE;
-    const int nblk = lmk_cls_nblk(V);
-    unsigned long long *ta = tagged + (size_t)LM_TAG_B * (NQ + 2 * NKV);
-    unsigned long long *tx = ta + (size_t)LM_TA_COPIES * LM_TAG_B * NQ;
-    unsigned long long *tgt = tx + (size_t)LM_TX_COPIES * LM_TAG_B * D;
-    unsigned long long *txx = tgt + (size_t)LM_TA_COPIES * LM_TAG_B * F;
-    const QkvTagged tg = {tagged, tagged + (size_t)LM_TAG_B * NQ, tagged + (size_t)LM_TAG_B * (NQ + NKV),
-                          ta, tx, tgt, txx, epoch, 0, L, err};
-    const TokenArgs targ = {(const u16 *)layers, layer_elems, off_wo, off_w13, off_w2, rms_att, rms_ffn,
-                            kv_layer, L, rms_final, (const u16 *)wcls, V, nblk, logits};
-    const ArgFold fold = {fold_tw, epoch, tok, pos, hist, hist_stride, err};
-#define LAUNCH_TOK(HD_, KT_)                                                                      \
-    DLAUNCH((k_token<K_, NB_, KT_, HD_, F_>), grid, dim3(WG), 0, s, x, (const u16 *)emb, tok, NQ, NKV, \
-            rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H, tg, targ, fold)
-    DISPATCH_DF(D, F, {
-        constexpr int NB_ = 1;
-        const int per = nprod + H + 2 * ((K_ / 2 + NWAVE - 1) / NWAVE) + (F_ + NWAVE - 1) / NWAVE;
-        const dim3 grid((unsigned)(L * per + nblk + 1));
-        if (hd == 64 && kv_f32) LAUNCH_TOK(64, float);
-        else if (hd == 64) LAUNCH_TOK(64, u16);
-        else if (kv_f32) LAUNCH_TOK(128, float);
-        else LAUNCH_TOK(128, u16);
-    });
-#undef LAUNCH_TOK
     return hipGetLastError();
 }
 

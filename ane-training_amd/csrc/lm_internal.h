@@ -58,9 +58,9 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 
 /* Tagged hand-off words of the batch 1-4 chain (LM_TAG_WORDS of them): q, k
  * and v of up to LM_TAG_B rows, then LM_TA_COPIES copies of the head
- * outputs, LM_TX_COPIES of x after Wo, LM_TA_COPIES of the FFN gate and
- * LM_TXX_COPIES of x after W2, each reading work-group taking one copy, so
- * that the readers of one value spread over more memory channels. */
+ * outputs, LM_TX_COPIES of x after Wo and LM_TA_COPIES of the FFN gate, each
+ * reading work-group taking one copy, so that the readers of one value spread
+ * over more memory channels. */
 #define LM_TAG_B 4
 /* Polls before a hand-off wait gives up (the second int of the flag buffer
  * the launchers take as `err`; about a second of polling). */
@@ -71,14 +71,8 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 #ifndef LM_TX_COPIES
 #define LM_TX_COPIES 4
 #endif
-/* copies of x after W2 (the whole-token launch hands it from layer to layer
- * and to the classifier) */
-#ifndef LM_TXX_COPIES
-#define LM_TXX_COPIES 4
-#endif
-#define LM_TAG_WORDS(NQ, NKV, D, F)                                                      \
-    ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * ((NQ) + (F)) + LM_TX_COPIES * (D) + \
-                        LM_TXX_COPIES * (D)))
+#define LM_TAG_WORDS(NQ, NKV, D, F) \
+    ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * ((NQ) + (F)) + LM_TX_COPIES * (D)))
 
 /* lmk_qkv_rope and the attention of every (head, row) in one launch: the
  * QKV work-groups hand q, k, v of the current position to the attention
@@ -105,24 +99,6 @@ int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 /* Whether the whole-layer form of lmk_qkv_attn (w13 given) is built for this
  * model width, hidden width and batch. */
 int lmk_layer_fusable(int D, int F, int B);
-
-/* The whole decode step of one row (B = 1) in one launch: the work-groups of
- * lmk_qkv_attn's whole-layer form for layer 0, then layer 1, ..., then those
- * of lmk_cls with fold_tw (the classifier and, last, the argmax reducer).
- * Every layer's W2 work-groups hand x on through tagged words (the LM_TXX
- * copies after the gate's in `tagged`) to the next layer's QKV and Wo
- * work-groups and, after the last layer, to the classifier's; layer l's
- * weights are layers + l * layer_elems (Wqkv, then Wo at off_wo, W1/W3 at
- * off_w13, W2 at off_w2), its norm gains rms_att + l * D and rms_ffn + l * D,
- * its cache kc/vc + l * kv_layer elements.  For lmk_layer_fusable(D, F, 1)
- * shapes. */
-int lmk_token(hipStream_t s, float *x, const uint16_t *emb, int *tok, const float *rms_att,
-              const float *rms_ffn, const uint16_t *layers, size_t layer_elems, size_t off_wo,
-              size_t off_w13, size_t off_w2, int D, int NQ, int NKV, int hd, int F, int L,
-              const float *rope_cos, const float *rope_sin, int *pos, int B, void *kc, void *vc,
-              size_t kv_layer, int kv_f32, int max_seq, int H, unsigned long long *tagged,
-              unsigned *epoch, int *err, const float *rms_final, const uint16_t *wcls, int V,
-              float *logits, unsigned long long *fold_tw, int *hist, int hist_stride);
 
 /* Causal attention, one work-group per (head, row): out[b, h*hd ..] =
  * softmax(q_bh . K[0..pos[b]] / sqrt(hd)) . V over cache slot slot[b] (slot

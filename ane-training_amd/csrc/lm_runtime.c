@@ -620,7 +620,7 @@ int lm_set_option(LMModel *m, int option, int value)
         m->use_graph = value ? 1 : 0;
         return LM_OK;
     case LM_OPT_FUSE_QKV_ATTN:
-        if (value < 0 || value > 5) return LM_ERR_INVALID;
+        if (value < 0 || value > 4) return LM_ERR_INVALID;
         if (value == m->fuse_qa) return LM_OK;
         HIPCHK(hipStreamSynchronize(m->stream));
         drop_graphs(m);
@@ -659,34 +659,30 @@ int lm_set_option(LMModel *m, int option, int value)
 /* The decode chain's fusion level for B rows: fuse_qa, where 3 takes the
  * whole-layer launch for one row only (B = 2 and 4 ran faster at level 2:
  * 203 and 281 us/step against 207 and 385) and 4 takes it for every batch;
- * 5 takes the whole step in one launch for one row (level 2 for more rows).
- * The whole-layer and whole-step launches are built only for the (dim,
- * hidden) pairs and batches lmk_layer_fusable names, and level 2 runs
- * elsewhere. */
+ * the whole-layer launch is built only for the (dim, hidden) pairs and
+ * batches lmk_layer_fusable names, and level 2 runs elsewhere. */
 static int chain_level(const LMModel *m, int B)
 {
     int lvl = m->fuse_qa;
-    if ((lvl == 3 || lvl == 5) && B > 1) lvl = 2;
+    if (lvl == 3 && B > 1) lvl = 2;
     if (lvl == 4) lvl = 3;
-    return lvl >= 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : lvl;
+    return lvl == 3 && !lmk_layer_fusable(m->D, m->F, B) ? 2 : lvl;
 }
 
-/* Whether kernel family fam of layer l runs inside another kernel's launch at
- * fusion level lvl (the QKV launch of its layer; at level 3 the argmax inside
- * the classifier's; at level 5 everything inside layer 0's QKV launch). */
-static int fam_inside(int fam, int l, int lvl)
+/* Whether kernel family fam runs inside another family's launch at fusion
+ * level lvl (the QKV launch; at level 3 the argmax inside the classifier's). */
+static int fam_inside(int fam, int lvl)
 {
-    if (lvl >= 5) return !(fam == LM_KERN_QKV && l == 0);
     return (fam == LM_KERN_ATTN && lvl >= 1) || (fam == LM_KERN_WO && lvl >= 2) ||
            ((fam == LM_KERN_W13 || fam == LM_KERN_W2 || fam == LM_KERN_ARGMAX) && lvl >= 3);
 }
 
 /* Queue the kernel of family `fam` (LM_KERN_*) of layer l for rows 0..B-1
- * (nothing for a family that runs inside another launch). */
+ * (nothing for a family that runs inside the QKV launch). */
 static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
 {
     const int lvl = chain_level(m, B);
-    if (fam_inside(fam, l, lvl)) return LM_OK;
+    if (fam_inside(fam, lvl)) return LM_OK;
     hipStream_t s = m->stream;
     const int D = m->D, F = m->F;
     const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
@@ -694,14 +690,7 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
     void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
     switch (fam) {
     case LM_KERN_QKV:
-        if (lvl == 5)   /* every layer, the classifier and the argmax */
-            KCHK(lmk_token(s, m->d_x, m->d_embed, m->d_tok, m->d_rms_att, m->d_rms_ffn, m->d_layers,
-                           m->layer_elems, m->off_wo, m->off_w13, m->off_w2, D, m->NQ, m->NKV, m->hd,
-                           F, m->L, m->d_rope_cos, m->d_rope_sin, m->d_pos, B, m->d_kc, m->d_vc,
-                           m->kv_layer_elems, m->kv_f32, m->max_seq, m->H, m->d_tagged,
-                           m->d_epoch, m->d_err, m->d_rms_final, m->d_wcls, m->V, logits,
-                           m->d_cls_tw, m->d_hist, m->max_seq + 1));
-        else if (lvl)   /* with the attention of every head (Wo from level 2, the FFN at 3) */
+        if (lvl)   /* with the attention of every head (Wo from level 2, the FFN at 3) */
             KCHK(lmk_qkv_attn(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
                               m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
                               m->d_rope_cos, m->d_rope_sin, m->d_pos, B, kc, vc, m->kv_f32,
@@ -750,9 +739,9 @@ static int enqueue_decode_gemv(LMModel *m, int B, float *logits)
 {
     static const int fams[5] = {LM_KERN_QKV, LM_KERN_ATTN, LM_KERN_WO, LM_KERN_W13, LM_KERN_W2};
     int rc;
-    for (int l = 0; l < m->L; l++)   /* (the whole-step launch writes the logits too) */
+    for (int l = 0; l < m->L; l++)
         for (int f = 0; f < 5; f++)
-            if ((rc = enqueue_kernel(m, B, fams[f], l, logits))) return rc;
+            if ((rc = enqueue_kernel(m, B, fams[f], l, NULL))) return rc;
     if ((rc = enqueue_kernel(m, B, LM_KERN_CLS, 0, logits))) return rc;
     return enqueue_kernel(m, B, LM_KERN_ARGMAX, 0, NULL);
 }
@@ -952,10 +941,10 @@ static int check_err(LMModel *m)
     fprintf(stderr, "stories_lm: a hand-off wait inside a fused launch gave up (results invalid)\n");
     *err_slot(m) = 0;
     /* Once a wait has given up, every wait of the launch ends early, so the
-     * argmax reducer can advance the step count while work-groups dispatched
-     * before it have yet to read it; their words then carry the tags of the
-     * next step.  Clear every hand-off word (tag 0 matches no step) with the
-     * flag, on the model's stream, before the next call. */
+     * argmax reducer can advance the step count while classifier work-groups
+     * dispatched before it have yet to read it; their words then carry the
+     * tags of the next step.  Clear every hand-off word (tag 0 matches no
+     * step) with the flag, on the model's stream, before the next call. */
     HIPCHK(hipMemsetAsync(m->d_tagged, 0, LM_TAG_WORDS(m->NQ, m->NKV, m->D, m->F) * 8, m->stream));
     HIPCHK(hipMemsetAsync(m->d_cls_tw, 0, (size_t)2 * LM_TAG_B * m->cls_nblk * 8, m->stream));
     HIPCHK(hipMemsetAsync(m->d_err, 0, 4, m->stream));
@@ -1316,14 +1305,14 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
         int k = 0;
         for (int l = 0; l < m->L && rc == LM_OK; l++)
             for (int f = 0; f < 5 && rc == LM_OK; f++) {
-                if (fam_inside(fams[f], l, chain_level(m, B))) continue;   /* inside another launch */
+                if (fam_inside(fams[f], chain_level(m, B))) continue;   /* inside the QKV launch */
                 kfam[k] = fams[f];
                 lmk_time_next(ev[2 * k], ev[2 * k + 1]);
                 rc = enqueue_kernel(m, B, fams[f], l, NULL);
                 k++;
             }
         for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
-            if (fam_inside(f, 0, chain_level(m, B))) continue;   /* inside another launch */
+            if (fam_inside(f, chain_level(m, B))) continue;   /* inside the classifier launch */
             kfam[k] = f;
             lmk_time_next(ev[2 * k], ev[2 * k + 1]);
             rc = enqueue_kernel(m, B, f, 0, NULL);
@@ -1340,9 +1329,8 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
-            launches_per_step[f] = fam_inside(f, 0, chain_level(m, B))           ? 0
+            launches_per_step[f] = fam_inside(f, chain_level(m, B))              ? 0
                                    : f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1
-                                   : fam_inside(f, 1, chain_level(m, B))     ? 1
                                                                              : m->L;
     }
     for (int i = 0; ev && i < 2 * nk; i++)

@@ -48,10 +48,8 @@ SEQ = 256
 
 # FETCH_SIZE per launch of the C0 chain's kernels with QKV + attention in one launch and
 # the rest apart (bytes, the counter's KiB x 1024 x 2.000)
-C0_FETCH = {"qkv": 4737000, "wo": 1234000, "w13": 6382000, "w2": 3265000, "cls": 49273000,
-            "argmax": 14000}
+C0_FETCH = {"qkv": 4737000, "wo": 1234000, "w13": 6382000, "w2": 3265000}
 TAG_COPIES = 8    # copies of each tagged word set that several work-groups read
-TXX_COPIES = 4    # copies of x after W2 in the whole-step launch (LM_TXX_COPIES)
 
 
 def qkv_launch_writes(cfg, kvb, folded):
@@ -364,7 +362,7 @@ def main():
     ap.add_argument("--steps", type=int, default=32, help="timed 256-token C0 sequences")
     ap.add_argument("--warmup", type=int, default=2, help="untimed 256-token C0 sequences")
     ap.add_argument("--direct", action="store_true", help="launch kernels directly, no graphs")
-    ap.add_argument("--fuse", type=int, choices=[0, 1, 2, 3, 4, 5], default=None,
+    ap.add_argument("--fuse", type=int, choices=[0, 1, 2, 3, 4], default=None,
                     help="LM_OPT_FUSE_QKV_ATTN for the C0 chain (A/B; default: the library's)")
     ap.add_argument("--kv16", action="store_true",
                     help="binary16 K/V cache (default fp32, as the reference forward keeps K/V)")
@@ -429,32 +427,21 @@ def main():
         # kernel timed by hipEvents at its own dispatch's start and end
         us, launches = m.profile_chain([1], [0], SEQ - 2)
     m.close()
-    fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
     if launches is None:   # the chain's launch counts: one per layer, attention (Wo from
-        # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once; at
-        # level 5 the whole step is one launch (counted as the QKV family's)
-        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz >= 3, "w2": fz >= 3, "argmax": fz >= 3,
-                  "cls": fz >= 5}
-        launches = {k: (0 if inside.get(k) else 1 if k in ("cls", "argmax") or fz >= 5 else cfg.n_layers)
+        # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once
+        fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
+        inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz >= 3, "w2": fz >= 3, "argmax": fz >= 3}
+        launches = {k: (0 if inside.get(k) else 1 if k in ("cls", "argmax") else cfg.n_layers)
                     for k in algo}
-    whole_step = launches.get("qkv") == 1 and launches.get("cls") == 0
-    if whole_step:
-        # one launch holds every layer, the classifier and the argmax
-        L = cfg.n_layers
-        algo = {"qkv": sum(algo[k] * L for k in ("qkv", "attn", "wo", "w13", "w2")) +
-                algo["cls"] + algo["argmax"]}
-        launches = {"qkv": 1}
-        folded = ["attn", "wo", "w13", "w2", "cls", "argmax"]
-    else:
-        if launches.get("argmax") == 0:   # the argmax runs inside the classifier launch
-            algo["cls"] += algo.pop("argmax")
-            launches.pop("argmax")
-        folded = []
-        for k in ("attn", "wo", "w13", "w2"):    # families that run inside the QKV launch
-            if launches.get(k) == 0:
-                folded.append(k)
-                algo["qkv"] += algo.pop(k)
-                launches.pop(k)
+    if launches.get("argmax") == 0:   # the argmax runs inside the classifier launch
+        algo["cls"] += algo.pop("argmax")
+        launches.pop("argmax")
+    folded = []
+    for k in ("attn", "wo", "w13", "w2"):    # families that run inside the QKV launch
+        if launches.get(k) == 0:
+            folded.append(k)
+            algo["qkv"] += algo.pop(k)
+            launches.pop(k)
     step_bytes = sum(algo[k] * launches[k] for k in algo)
     step_gbs = step_bytes / (us_tok * 1e-6) / 1e9
     out = {
@@ -472,7 +459,6 @@ def main():
                    "batch": 1, "seq_len": SEQ, "tokens_timed": tokens, "graphs": not args.direct},
         "us_per_token": round(us_tok, 3),
         "launches_per_token": int(sum(launches.values())),
-        "fusion_level": fz,
         "wall_s": round(wall, 3),
         "step_roofline": {"bytes_per_token": int(step_bytes), "achieved": round(step_gbs, 1),
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
@@ -483,20 +469,13 @@ def main():
         dur_us = us[dom]
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
         traffic = None
-        if dom == "qkv" and not args.kv16 and whole_step:
-            # every layer's parts as below, the x words between layers, the classifier
-            layer = ["wo", "w13", "w2"]
-            traffic = cfg.n_layers * (sum(C0_FETCH[k] for k in ["qkv"] + layer) +
-                                      qkv_launch_writes(cfg, kvb, layer) +
-                                      8 * TXX_COPIES * cfg.dim) + C0_FETCH["cls"] + C0_FETCH["argmax"]
-        elif dom == "qkv" and not args.kv16 and "attn" in folded:
+        if dom == "qkv" and not args.kv16 and "attn" in folded:
             # fp32 cache: FETCH_SIZE (x 2.000, the 256 MiB copy calibration) of each part
             # launched on its own, QKV + attention fused (profiles/decode_b1_stories110m_chain.md),
             # summed over the parts this launch holds, + its writes, taken as algorithmic
             traffic = sum(C0_FETCH[k] for k in ["qkv"] + folded if k != "attn") + \
                 qkv_launch_writes(cfg, kvb, folded)
-        kname = ("k_token" if whole_step else "k_qkv_attn") if dom == "qkv" else dom
-        out["roofline"] = {"bound": "hbm", "kernel": kname,
+        out["roofline"] = {"bound": "hbm", "kernel": "k_qkv_attn" if dom == "qkv" else dom,
                            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                            "bytes_per_launch": int(algo[dom]), "launch_us": round(dur_us, 3),

@@ -46,12 +46,11 @@ def test_dpp_wave_reductions(lm):
 
 @pytest.mark.parametrize("name,d", [("mha", TINY), ("gqa", TINY_GQA), ("hd128", TINY_HD128)])
 @pytest.mark.parametrize("kv", [32, 16])
-@pytest.mark.parametrize("fuse", [5, 4, 3, 2, 1, 0])
+@pytest.mark.parametrize("fuse", [4, 3, 2, 1, 0])
 def test_tiny_decode_steps_match_oracle(lm, name, d, kv, fuse):
-    """fuse: the whole step in one launch (5), the whole layer in one launch
-    (4, and 3 at B = 1), QKV, attention and Wo (2), QKV and attention (1), or
-    each apart (0); the work-groups of one launch hand values over through
-    tagged words."""
+    """fuse: the whole layer in one launch (4, and 3 at B = 1), QKV, attention
+    and Wo (2), QKV and attention (1), or each apart (0); the work-groups of
+    one launch hand values over through tagged words."""
     _say(f"[tiny decode {name} kv{kv} fuse{fuse}]")
     fx = np.load(os.path.join(GOLDEN, f"tiny_{name}.npz"))
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
@@ -65,7 +64,7 @@ def test_tiny_decode_steps_match_oracle(lm, name, d, kv, fuse):
 
 
 @pytest.mark.parametrize("B", [2, 3, 4])
-@pytest.mark.parametrize("fuse", [5, 4, 3, 2, 1, 0])
+@pytest.mark.parametrize("fuse", [4, 3, 2, 1, 0])
 def test_tiny_batch_decode_matches_oracle(lm, orc, B, fuse):
     """B slots in one batched step, first in lock-step, then at different
     positions (slot b advances every b+1 steps; a repeated (token, pos) step
@@ -192,17 +191,14 @@ def test_graph_replay_equals_direct_launches(lm):
     m2.close()
 
 
-@pytest.mark.parametrize("fuse", [5, 3])
-def test_handoff_timeout_reports_error(lm, fuse):
+def test_handoff_timeout_reports_error(lm):
     """A hand-off wait that gives up, forced from the host with a limit of one
     poll, ends its launch normally and turns into LM_ERR_HIP; with the limit
-    restored, the next calls give the fixture's logits again (the whole step
-    in one launch, or each layer)."""
-    _say(f"[hand-off timeout fuse{fuse}]")
+    restored, the next calls give the fixture's logits again."""
+    _say("[hand-off timeout]")
     d = TINY
     fx = np.load(os.path.join(GOLDEN, "tiny_mha.npz"))
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], True)
-    m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     assert m.forward(int(fx["tokens"][0]), 0) is not None      # the limit still at its default
     m.set_option(lm.LM_OPT_HANDOFF_SPINS, 1)
     with pytest.raises(lm.LMError) as ei:      # lm_forward_batch returns the status itself
@@ -219,7 +215,7 @@ def test_handoff_timeout_reports_error(lm, fuse):
     m.close()
 
 
-@pytest.mark.parametrize("fuse", [5, 4, 3, 2, 1, 0])
+@pytest.mark.parametrize("fuse", [4, 3, 2, 1, 0])
 def test_profile_chain_times_every_family(lm, fuse):
     """lm_profile_chain: every kernel of real decode steps timed at its own
     dispatch; positive durations, the launch counts of a step, and the range
@@ -230,12 +226,9 @@ def test_profile_chain_times_every_family(lm, fuse):
     m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     us, n = m.profile_chain([1], [20], 6)
     L = d["n_layers"]
-    if fuse == 5:      # the whole step, one launch counted as the QKV family's
-        assert n == {"qkv": 1, "attn": 0, "wo": 0, "w13": 0, "w2": 0, "cls": 0, "argmax": 0}
-    else:
-        assert n == {"qkv": L, "attn": 0 if fuse >= 1 else L, "wo": 0 if fuse >= 2 else L,
-                     "w13": 0 if fuse >= 3 else L, "w2": 0 if fuse >= 3 else L, "cls": 1,
-                     "argmax": 0 if fuse >= 3 else 1}
+    assert n == {"qkv": L, "attn": 0 if fuse >= 1 else L, "wo": 0 if fuse >= 2 else L,
+                 "w13": 0 if fuse >= 3 else L, "w2": 0 if fuse >= 3 else L, "cls": 1,
+                 "argmax": 0 if fuse >= 3 else 1}
     for k in us:
         assert (us[k] > 0) == (n[k] > 0), k
         assert us[k] < 1e4, k
