@@ -288,6 +288,16 @@ int lm_write_llama2c(const char *path, const Config *cfg, const LMWeights *w)
     return LM_OK;
 }
 
+/* Bytes from the current position of f to its end (0 when unknown). */
+static unsigned long long bytes_left(FILE *f)
+{
+    const long here = ftell(f);
+    if (here < 0 || fseek(f, 0, SEEK_END) != 0) return 0;
+    const long end = ftell(f);
+    if (fseek(f, here, SEEK_SET) != 0 || end < here) return 0;
+    return (unsigned long long)(end - here);
+}
+
 int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data)
 {
     *data = NULL;
@@ -314,6 +324,14 @@ int lmh_read_llama2c(const char *path, Config *cfg, int *untied, float **data)
     int u = hdr.vocab_size < 0;                    /* model.h:85-86 */
     if (u) hdr.vocab_size = -hdr.vocab_size;
     size_t n = lm_weights_numel(&hdr, u);
+    /* a file shorter than its header says is refused before the allocation */
+    const unsigned long long left = bytes_left(f);
+    if (left < (unsigned long long)n * sizeof(float)) {
+        fprintf(stderr, "lm_load_llama2c: %s holds %llu bytes of weights, its header needs %llu "
+                "(file truncated?)\n", path, left, (unsigned long long)n * sizeof(float));
+        fclose(f);
+        return LM_ERR_FORMAT;
+    }
     float *buf = (float *)malloc(n * sizeof(float));
     if (!buf) {
         fclose(f);
@@ -403,6 +421,16 @@ int lmh_read_blzt(const char *path, Config *cfg, float **data)
     const size_t wq = sz[LMH_T_WQ] / L, wk = sz[LMH_T_WK] / L, wv = sz[LMH_T_WV] / L;
     const size_t wo = sz[LMH_T_WO] / L, w1 = sz[LMH_T_W1] / L, w2 = sz[LMH_T_W2] / L;
     const size_t w3 = sz[LMH_T_W3] / L;
+    /* the weights and their Adam m and v: three values per parameter, up to
+     * the embedding, whose Adam state the loop does not read */
+    const size_t per_layer = wq + wk + wv + wo + w1 + w2 + w3 + 2 * D;
+    const unsigned long long need =
+        4ull * (3 * (L * per_layer + D) + (unsigned long long)c.vocab_size * D);
+    if (bytes_left(f) < need) {
+        fprintf(stderr, "lm_load_blzt: %s is truncated\n", path);
+        fclose(f);
+        return LM_ERR_FORMAT;
+    }
     float *buf = (float *)malloc(lm_weights_numel(&c, 0) * sizeof(float));
     if (!buf) {
         fclose(f);

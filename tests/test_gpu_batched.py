@@ -137,6 +137,32 @@ def test_prefill_many_sequences_matches_oracle(lm, orc, name, d, kv32):
     m.close()
 
 
+# eight heads, so that a chunk of 13 sequences of 150 tokens gives the shared-tile
+# kernel its 128+ work-groups (two 128-query blocks per sequence and head)
+LONG_PREFILL = dict(dim=512, hidden_dim=1024, n_layers=2, n_heads=8, n_kv_heads=4, vocab_size=1000,
+                    seq_len=160)
+LONG_PREFILL_HD128 = dict(dim=1024, hidden_dim=1024, n_layers=2, n_heads=8, n_kv_heads=4,
+                          vocab_size=600, seq_len=160)
+
+
+@pytest.mark.parametrize("name,d,kv32", [("gqa", LONG_PREFILL, False), ("gqa32", LONG_PREFILL, True),
+                                         ("hd128", LONG_PREFILL_HD128, False)])
+def test_prefill_long_blocks_match_oracle(lm, orc, name, d, kv32):
+    """24 sequences of 150 tokens (chunks of 13 and 11 whole sequences): the
+    shared-tile kernel's 128-query blocks over 2 and 3 key tiles (its register
+    and LDS double buffers turn over), at head dims 64 and 128."""
+    _say(f"[prefill long blocks {name}]")
+    n, P = 24, 150
+    m, w16 = make(lm, d, 45, n, 160, kv32)
+    toks = np.random.default_rng(45).integers(0, d["vocab_size"], (n, P)).astype(np.int32)
+    lg = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    w32 = lm.f16_to_f32(w16)
+    for i in (0, 11, 23):
+        ref = orc.Oracle(cfg7(d), w32, True, 160, kv_f16=not kv32).forward_full(toks[i])
+        close_enough(lg[i * P:(i + 1) * P], ref)
+    m.close()
+
+
 def _batched_decode_vs_oracle(lm, orc, d, B, seed, kv32=False):
     """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
     decode path) against the oracle, then greedy runs."""
