@@ -964,7 +964,10 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * traffic wins; a decode-row classifier (N >= 16384) takes a 64 x 128 tile;
  * up to 32 rows take 32 x 64 tiles of two waves (a 64-row tile would stage and
  * multiply half padding: 5% faster on the scaled model's 32-row QKV and W2;
- * the LDS-staged QKV epilogue keeps its four-wave 64-row tile).  K is a
+ * the LDS-staged QKV epilogue keeps its four-wave 64-row tile), and so does
+ * the gate GEMM of 33-64 decode rows, which cannot be K-split: two row tiles
+ * per column tile put 128 work-groups instead of 64 on the 64-row W1/W3 of
+ * Stories (C2 0.4690/0.4683 -> 0.4643/0.4641 ms/step, same box).  K is a
  * multiple of the 64-wide stage. */
 template <int E>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
@@ -973,7 +976,7 @@ static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t
     if (K % BKH) return hipErrorInvalidValue;
     if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
-    else if (E != EPI_QKV && M <= 32) {
+    else if (E != EPI_QKV && (M <= 32 || (E == EPI_GATE && M <= 64))) {
         if constexpr (E != EPI_QKV) launch_tile<32, 64, E>(s, A, lda, W, M, N, K, e);
     } else launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
     return hipGetLastError();
