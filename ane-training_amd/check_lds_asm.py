@@ -5,8 +5,10 @@ waits for them with a separate `s_waitcnt lgkmcnt(0)` statement that names the
 destination registers as in/out operands.  The compiler cannot see that a read
 is still in flight between the two statements; this script scans the device
 assembly of every k_gemm_tile instantiation and fails if any instruction
-between a read and the next lgkmcnt(0) wait reads or writes one of the pending
-destination registers.
+reads or writes the destination register of an LDS read that no wait has
+retired yet: lgkmcnt(0) retires every read, and the compiler's own
+lgkmcnt(n) retires all but the n youngest LDS operations when no scalar load
+is in flight (LDS operations complete in order).
 
     python3 check_lds_asm.py k_gemm.s
 """
@@ -28,18 +30,34 @@ def check(asm_text):
     for name in names:
         a = asm_text.index(name + ":")
         b = asm_text.index(".Lfunc_end", a)
-        pending = set()
+        # lgkm operations in flight, oldest first: (destination registers, is
+        # scalar memory).  LDS operations complete in order, so a wait
+        # lgkmcnt(n) retires all but the n youngest; scalar loads complete out
+        # of order, so with one in flight only lgkmcnt(0) retires anything.
+        queue = []
         for ln in asm_text[a:b].split("\n"):
             t = ln.split(";")[0].strip()
             if not t or t.startswith("."):
                 continue
             ops = [x for x in re.split(r"[ ,]+", t) if x]
-            if ops[0] == "ds_read_b128":
-                pending |= regset(ops[1])
+            if ops[0].startswith("ds_"):
+                dst = regset(ops[1]) if ops[0].startswith(("ds_read", "ds_bpermute", "ds_permute",
+                                                           "ds_swizzle")) else set()
+                queue.append((dst, False))
                 continue
-            if ops[0] == "s_waitcnt" and "lgkmcnt(0)" in t:
-                pending = set()
+            if ops[0].startswith(("s_load", "s_buffer_load")):
+                queue.append((set(), True))
                 continue
+            if ops[0] == "s_waitcnt":
+                m = re.search(r"lgkmcnt\((\d+)\)", t)
+                if m:
+                    n = int(m.group(1))
+                    if n == 0:
+                        queue = []
+                    elif not any(s for _, s in queue):
+                        queue = queue[-n:] if n < len(queue) else queue
+                continue
+            pending = set().union(*(d for d, _ in queue)) if queue else set()
             if pending:
                 used = set()
                 for o in ops[1:]:

@@ -15,6 +15,11 @@
  *              blocks of 16, so h3 sits 16 columns right of h1 (forward.h:149-151)
  *   EPI_QKV    RoPE on q/k column pairs (forward.h:55-70); q -> fp32 [M, NQ];
  *              k, v -> the K/V cache at (slot[m], pos[m])
+ *   EPI_RESNORM x[m, n] += C (forward.h:136, 159), u[m, n] = fp16(x[m, n] *
+ *              gain[n]) and the sum of x[m, n]^2 over each row's 32 columns:
+ *              the RMSNorm of x (forward.h:46-53) finished by the GEMM that
+ *              reads u, which scales its product row m by 1/sqrt(mean + 1e-5)
+ *              (rs_ss) before its own epilogue
  *
  * MFMA lane layout (checked on the device): for a 32x32x16 step lane l holds
  * A[l%32][8*(l/32) .. +8], B[8*(l/32) .. +8][l%32] (= W[n0 + l%32][k ..]), and
@@ -78,16 +83,26 @@ struct EpiArgs {
     const float *rope_cos, *rope_sin;
     size_t sstride;         /* STORE of a K-split GEMM: out of split s is out + s*sstride */
     int nt;                 /* STORE / ARGMAX: non-temporal stores of out */
+    const float *gain;      /* RESNORM: gain [N]; u [M, N] fp16; ss [M, nss] */
+    u16 *u;
+    float *ss;
+    const float *rs_ss;     /* STORE / GATE / QKV: row sums of squares [M, nss] of the
+                             * RESNORM that wrote A, or NULL */
+    int nss;
 };
 
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_QKV = 3, EPI_ARGMAX = 4, EPI_RESNORM = 5 };
 
 /* Apply epilogue E to one 32x32 accumulator tile at (m0, n0).  Every operand
  * the epilogue reads (residual, positions, rotation angles) is loaded for the
  * whole tile before the first store: stores the compiler cannot prove disjoint
- * from those loads would otherwise serialise one memory round trip per element. */
+ * from those loads would otherwise serialise one memory round trip per element.
+ * xpre: the tile's residual values (RESID, RESNORM) and, after them, the
+ * lane's gain (RESNORM), loaded before the main loop, or nullptr to load them
+ * here. */
 template <int E>
-__device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0, const EpiArgs &e)
+__device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0, const EpiArgs &e,
+                                              const float *xpre = nullptr)
 {
     const int lane = threadIdx.x & 63;
     const int n = n0 + (lane & 31);
@@ -124,10 +139,56 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
     } else if (E == EPI_RESID) {
         float xv[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) xv[i] = ok[i] ? e.out[(size_t)rr[i] * e.ldc + n] : 0.f;
+        for (int i = 0; i < 16; i++) xv[i] = xpre ? xpre[i] : ok[i] ? e.out[(size_t)rr[i] * e.ldc + n] : 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++)
             if (ok[i]) e.out[(size_t)rr[i] * e.ldc + n] = xv[i] + acc[i];
+    } else if (E == EPI_RESNORM) {
+        /* the residual add, the gained fp16 row for the next GEMM, and each
+         * row's sum of squares over this tile's 32 columns (N is a multiple
+         * of 32) */
+        float xv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) xv[i] = xpre ? xpre[i] : ok[i] ? e.out[(size_t)rr[i] * e.ldc + n] : 0.f;
+        const float gn = xpre ? xpre[16] : n < e.N ? e.gain[n] : 0.f;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = xv[i] + acc[i];
+        if (m0 + 32 <= e.M && n0 + 32 <= e.N) {   /* whole tile: no per-element masks */
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                e.out[(size_t)rr[i] * e.ldc + n] = v[i];
+                e.u[(size_t)rr[i] * e.N + n] = f2h(v[i] * gn);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (ok[i]) {
+                    e.out[(size_t)rr[i] * e.ldc + n] = v[i];
+                    e.u[(size_t)rr[i] * e.N + n] = f2h(v[i] * gn);
+                }
+        }
+        /* Row sums over the 32 lanes of each half by reduce-scatter: at the
+         * stage of offset o each lane keeps half of its remaining sums (the
+         * upper half where lane & o) and adds the partner's copy of them, so
+         * after the offsets 16, 8, 4, 2 and a last add over offset 1, lane l
+         * holds the sum of row index (l & 31) >> 1 of its half. */
+        float q[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) q[i] = ok[i] ? v[i] * v[i] : 0.f;
+        static_for<0, 4>([&](auto S) {
+            constexpr int o = 16 >> decltype(S)::value, c = 8 >> decltype(S)::value;
+            const bool hi = lane & o;
+#pragma unroll
+            for (int j = 0; j < c; j++) {
+                const float keep = hi ? q[j + c] : q[j], give = hi ? q[j] : q[j + c];
+                q[j] = keep + __shfl_xor(give, o, 64);
+            }
+        });
+        q[0] += __shfl_xor(q[0], 1, 64);
+        const int ri = (lane & 31) >> 1;
+        const int row = rbase + 8 * (ri >> 2) + (ri & 3);
+        if (!(lane & 1) && row < e.M && n0 < e.N) e.ss[(size_t)row * e.nss + n0 / 32] = q[0];
     } else if (E == EPI_GATE) {
         /* tile columns 0..15 hold W1 rows 16j.., columns 16..31 the W3 rows */
         /* rows rr[i], rr[i+1] (i even) of gate index gi: lane c < 16 takes row
@@ -447,7 +508,7 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
     }
 }
 
-template <int BM, int BN, int E, int NS, int WVM>
+template <int BM, int BN, int E, int NS, int WVM, bool RS = false>
 __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                          const u16 *__restrict__ W, int K, int kc,
                                                          EpiArgs e, int tm, int tn)
@@ -604,10 +665,57 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
             qpre[k].sl = e.slot[row];
         }
     }
+    /* the residual a one-tile wave adds (RESID, RESNORM) and the gain
+     * (RESNORM), loaded before the ring so that they arrive during the main
+     * loop instead of after it */
+    constexpr bool XPRE = (E == EPI_RESID || E == EPI_RESNORM) && TM * TN == 1;
+    float xpre[XPRE ? 17 : 1];
+    if constexpr (XPRE) {
+        const int n = n0 + wn * WN + (lane & 31);
+        const int rb = m0 + wm * WM + 4 * (lane >> 5);
+        if constexpr (E == EPI_RESNORM) xpre[16] = n < N ? e.gain[n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = rb + 8 * (i >> 2) + (i & 3);
+            xpre[i] = r < M && n < N ? e.out[(size_t)r * e.ldc + n] : 0.f;
+        }
+    }
+    /* Row scale after a RESNORM GEMM (RS, e.rs_ss set): thread r < BM loads
+     * the nss sums of squares of tile row r (float4s, a uniform count) before
+     * the ring's first loads, and adds them once those are issued (the wait
+     * then covers only these older loads), leaving the row's scale in LDS; no
+     * register stays live through the main loop.  A separate instantiation:
+     * in the unscaled kernels the extra arguments and branches delayed the
+     * start of every tile (C1's GEMMs 5% slower with the scale unused). */
+    static_assert(!RS || E == EPI_GATE || E == EPI_QKV, "row scale before a gate or QKV epilogue");
+    static_assert(!RS || BM <= 128 * WVM, "a thread per tile row");
+    constexpr int MAXV = RS ? 16 : 1;   /* float4s per row: nss <= 64 */
+    __shared__ float rs_sh[RS ? BM : 1];
+    float4 ssv[MAXV];
+    if constexpr (RS) {
+        if (tid < BM) {
+            const float4 *src = (const float4 *)(e.rs_ss + (size_t)min(m0 + tid, M - 1) * e.nss);
+            const int nv = e.nss >> 2;
+#pragma unroll
+            for (int j = 0; j < MAXV; j++) ssv[j] = j < nv ? src[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
     issue(lds0, 0);
     static_for<1, NS - 1>([&](auto I) {
         if (decltype(I)::value < nk) issue(ring(I), decltype(I)::value);
     });
+    if constexpr (RS) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (tid < BM) {
+            /* 1/sqrt(mean(x^2) + 1e-5) of the row (forward.h:46-53), the
+             * partials added in a fixed order */
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < MAXV; j++) sum += (ssv[j].x + ssv[j].y) + (ssv[j].z + ssv[j].w);
+            rs_sh[tid] = 1.0f / sqrtf(sum / (float)(32 * e.nss) + 1e-5f);
+        }
+    }
     for (int kt = 0; kt < nk; kt += NS) {
         static_for<0, NS>([&](auto I) {
             constexpr int i = decltype(I)::value;
@@ -615,6 +723,16 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
                 step(kt + i, ring(std::integral_constant<int, i>{}),
                      ring(std::integral_constant<int, i + NS - 1>{}));
         });
+    }
+    if constexpr (RS) {   /* the product rows scaled by their row's scale */
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int k = 0; k < 16; k++)
+                    acc[i][j][k] *= rs_sh[wm * WM + i * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3)];
     }
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
     if constexpr (E == EPI_GATE) {
@@ -631,7 +749,8 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
-            epilogue_tile<E>(acc[i][j], m0 + wm * WM + i * 32, n0 + wn * WN + j * 32, e);
+            epilogue_tile<E>(acc[i][j], m0 + wm * WM + i * 32, n0 + wn * WN + j * 32, e,
+                             XPRE ? xpre : nullptr);
 }
 
 /* ---- per-row RMSNorm ------------------------------------------------------------ */
@@ -901,6 +1020,8 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     e.slot = p->slot; e.pos = p->pos; e.rope_cos = p->rope_cos; e.rope_sin = p->rope_sin;
     e.sstride = 0;
     e.nt = p->stream_out;
+    e.gain = p->gain; e.u = (u16 *)p->u; e.ss = p->ss;
+    e.rs_ss = p->rs_ss; e.nss = p->nss;
     return e;
 }
 
@@ -916,23 +1037,23 @@ static constexpr int ring_depth(bool rows64, bool gate = false)
     return BM <= 64 && rows64 ? ((gate ? want : DEC_RING) < fit ? (gate ? want : DEC_RING) : fit) : 3;
 }
 
-template <int BM, int BN, int E>
+template <int BM, int BN, int E, bool RS = false>
 static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                         int K, const EpiArgs &e)
 {
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
     if constexpr (BM == 256 && E != EPI_QKV) {   /* eight waves (4 x 2): two per SIMD */
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 4>), dim3(tm * tn), dim3(512), 0, s, (const u16 *)A,
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 4, RS>), dim3(tm * tn), dim3(512), 0, s, (const u16 *)A,
                            lda, (const u16 *)W, K, K, e, tm, tn);
     } else if constexpr (BM == 32) {               /* two waves (1 x 2) over 32 rows */
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1>), dim3(tm * tn),
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS>), dim3(tm * tn),
                            dim3(128), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
     } else {
         if (M <= 64 && BM == 64)
-            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2>), dim3(tm * tn),
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2, RS>), dim3(tm * tn),
                                dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
         else
-            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2, RS>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
                                lda, (const u16 *)W, K, K, e, tm, tn);
     }
 }
@@ -969,12 +1090,19 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * per column tile put 128 work-groups instead of 64 on the 64-row W1/W3 of
  * Stories (C2 0.4690/0.4683 -> 0.4643/0.4641 ms/step, same box).  K is a
  * multiple of the 64-wide stage. */
-template <int E>
+template <int E, bool RS = false>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
 {
     if (K % BKH) return hipErrorInvalidValue;
-    if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
+    if constexpr (RS) {
+        /* row-scaled GEMMs (prefill rows): the two prefill tiles, but QKV only
+         * on 64 x 64 (its four-wave 256 x 128 tile with the row scale used
+         * in-flight LDS read registers early; the assembly check rejects it) */
+        if (E == EPI_GATE && (long)((M + 255) / 256) * ((N + 127) / 128) >= 240) {
+            if constexpr (E == EPI_GATE) launch_tile<256, 128, E, true>(s, A, lda, W, M, N, K, e);
+        } else launch_tile<64, 64, E, true>(s, A, lda, W, M, N, K, e);
+    } else if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
     else if (E != EPI_QKV && (M <= 32 || (E == EPI_GATE && M <= 64))) {
         if constexpr (E != EPI_QKV) launch_tile<32, 64, E>(s, A, lda, W, M, N, K, e);
@@ -992,15 +1120,26 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
                            N != ep->NQ + 2 * ep->NKV))
         return hipErrorInvalidValue;
     if (epi == EPI_RESID && (!ep->out || ep->ldc < N)) return hipErrorInvalidValue;
+    if (epi == EPI_RESNORM && (!ep->out || ep->ldc < N || !ep->gain || !ep->u || !ep->ss || N % 32 ||
+                               ep->nss != N / 32))
+        return hipErrorInvalidValue;
+    if (ep->rs_ss && ((epi != EPI_GATE && epi != EPI_QKV) || ep->nss < 4 ||
+                      ep->nss > 64 || ep->nss % 4 || ((uintptr_t)ep->rs_ss & 15)))
+        return hipErrorInvalidValue;
     if ((epi == EPI_STORE || epi == EPI_ARGMAX) && ep->out && ep->ldc < N) return hipErrorInvalidValue;
     if (epi == EPI_ARGMAX && !ep->part) return hipErrorInvalidValue;
     const EpiArgs e = to_epi(ep, M, N);
     switch (epi) {
     case EPI_STORE: return launch_gemm<EPI_STORE>(s, A, lda, W, M, N, K, e);
     case EPI_RESID: return launch_gemm<EPI_RESID>(s, A, lda, W, M, N, K, e);
-    case EPI_GATE: return launch_gemm<EPI_GATE>(s, A, lda, W, M, N, K, e);
-    case EPI_QKV: return launch_gemm<EPI_QKV>(s, A, lda, W, M, N, K, e);
+    case EPI_GATE:
+        return ep->rs_ss ? launch_gemm<EPI_GATE, true>(s, A, lda, W, M, N, K, e)
+                         : launch_gemm<EPI_GATE>(s, A, lda, W, M, N, K, e);
+    case EPI_QKV:
+        return ep->rs_ss ? launch_gemm<EPI_QKV, true>(s, A, lda, W, M, N, K, e)
+                         : launch_gemm<EPI_QKV>(s, A, lda, W, M, N, K, e);
     case EPI_ARGMAX: return launch_gemm<EPI_ARGMAX>(s, A, lda, W, M, N, K, e);
+    case EPI_RESNORM: return launch_gemm<EPI_RESNORM>(s, A, lda, W, M, N, K, e);
     default: return hipErrorInvalidValue;
     }
 }

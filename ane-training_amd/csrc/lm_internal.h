@@ -157,6 +157,8 @@ int lmk_attn_prefill(hipStream_t s, const float *q, const void *kc, const void *
 #define LMK_EPI_GATE    2   /* g[m, i] = fp16(silu(h1) * h3), W1/W3 interleaved    */
 #define LMK_EPI_QKV     3   /* RoPE; q -> fp32 [M, NQ]; k, v -> cache(slot, pos)   */
 #define LMK_EPI_ARGMAX  4   /* out (may be NULL) + [M, ceil(N/32)] argmax partials */
+#define LMK_EPI_RESNORM 5   /* out += C; u = fp16(out * gain); ss = row sums of out^2
+                               per 32 columns (a row norm left to the next GEMM)   */
 
 typedef struct {
     float *out;              /* STORE / RESID                                      */
@@ -171,6 +173,18 @@ typedef struct {
     int kv_f32, NQ, NKV, hd, Hkv, max_seq;
     const int *slot, *pos;   /* per row                                             */
     const float *rope_cos, *rope_sin;
+    /* RESNORM: out[m, n] += C (the residual add), then u[m, n] = fp16(out[m, n] *
+     * gain[n]) ([M, N], the next GEMM's operand before its row scale) and
+     * ss[m, n/32] = sum of out[m, n]^2 over the 32 columns of block n/32 */
+    const float *gain;
+    uint16_t *u;
+    float *ss;
+    /* GATE / QKV after a RESNORM GEMM: with rs_ss, product row m is
+     * first scaled by 1/sqrt(sum_b rs_ss[m, b] / (32 nss) + 1e-5), the RMSNorm
+     * of that row (forward.h:46-53) whose gain is already in the operand */
+    const float *rs_ss;
+    int nss;                 /* blocks of 32 columns per row of rs_ss / ss; with
+                              * rs_ss a multiple of 4, <= 64, rs_ss 16-byte aligned */
 } LMEpilogue;
 
 int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,

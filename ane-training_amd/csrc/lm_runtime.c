@@ -54,7 +54,8 @@ struct LMModel {
     size_t kv_layer_elems;
     int kv_f32;                 /* cache element: 0 = binary16, 1 = fp32 */
     /* per-row activations, max_rows rows (decode rows, or a prefill chunk) */
-    float *d_x, *d_q, *d_attn, *d_g, *d_logits, *d_rstd;
+    float *d_x, *d_q, *d_attn, *d_g, *d_logits;
+    float *d_ss;                /* per-row sums of squares of x, D/32 per row  */
     float *d_part;              /* partials of K-split GEMMs, Wo/W2 products    */
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
@@ -318,11 +319,11 @@ static void drop_graphs(LMModel *m)
 
 static void free_rows(LMModel *m)
 {
-    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_rstd, m->d_part, m->d_g16,
+    void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_ss, m->d_part, m->d_g16,
                    m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
-    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_rstd = m->d_part = NULL;
+    m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_ss = m->d_part = NULL;
     m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
     m->d_rtok = m->d_rpos = m->d_rslot = NULL;
@@ -346,7 +347,7 @@ static int alloc_rows(LMModel *m, int R)
     if ((st = dev_alloc((void **)&m->d_xn16, r * D * 2))) return st;
     if ((st = dev_alloc((void **)&m->d_a16, r * NQ * 2))) return st;
     if ((st = dev_alloc((void **)&m->d_logits, r * V * 4))) return st;
-    if ((st = dev_alloc((void **)&m->d_rstd, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_ss, r * (D / 32) * 4))) return st;
     {
         /* K-split partials (widest: QKV of decode rows), or one [R, D] product
          * of prefill rows */
@@ -778,6 +779,18 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
     const int ns_wo = lmk_pick_split(M, D, NQ);
     const int ns_w2 = lmk_pick_split(M, D, F);
     const int sep_wo = !dec || ns_wo > 1, sep_w2 = !dec || ns_w2 > 1;
+    /* Beyond 64 rows, an unsplit Wo or W2 folds the row norm that follows it
+     * into the GEMMs: it adds its product to x and writes u = fp16(x * gain)
+     * and the sums of squares of x per 32 columns (RESNORM), and the GEMM that
+     * reads u scales its product rows by 1/sqrt(mean(x^2) + 1e-5), which
+     * distributes over the row's dot products.  That saves the row-norm
+     * launch and the product's round trip through memory.  K-split
+     * projections keep the row norm, which adds their partials (an unsplit
+     * 2048-row W2 took 20 us against 14 + 5.6 for the split and the norm);
+     * so do layer 0 (embedding) and the classifier. */
+    const int can_fold = !dec && D % 128 == 0 && D / 32 <= 64;
+    const int fold_wo = can_fold && ns_wo == 1, fold_w2 = can_fold && ns_w2 == 1;
+    int rs_next = 0;                   /* x's norm is pending in u for QKV */
     const float *pend = NULL;          /* W2 partials not yet added to x */
     int pend_ns = 0;
     LMEpilogue ep;
@@ -785,8 +798,10 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         const uint16_t *lw = m->d_layers + (size_t)l * m->layer_elems;
         const size_t kvo = (size_t)l * m->kv_layer_elems * (m->kv_f32 ? 4 : 2);
         void *kc = (char *)m->d_kc + kvo, *vc = (char *)m->d_vc + kvo;
-        KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok, pend, pend_ns, sx,
-                         m->d_rms_att + (size_t)l * D, m->d_xn16));
+        const float *rs = rs_next ? m->d_ss : NULL;   /* u's row scale */
+        if (!rs)
+            KCHK(lmk_rownorm(s, m->d_x, D, M, l == 0 ? m->d_embed : NULL, tok, pend, pend_ns, sx,
+                             m->d_rms_att + (size_t)l * D, m->d_xn16));
         pend = NULL;
         pend_ns = 0;
         if (ns_qkv > 1) {
@@ -804,6 +819,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             ep.q = m->d_q; ep.kc = kc; ep.vc = vc; ep.kv_f32 = m->kv_f32;
             ep.NQ = NQ; ep.NKV = NKV; ep.hd = m->hd; ep.Hkv = m->Hkv; ep.max_seq = m->max_seq;
             ep.slot = slot; ep.pos = pos; ep.rope_cos = m->d_rope_cos; ep.rope_sin = m->d_rope_sin;
+            ep.rs_ss = rs; ep.nss = D / 32;
             KCHK(lmk_gemm(s, m->d_xn16, D, lw, M, NQKV, D, LMK_EPI_QKV, &ep));
         }
         if (ns_qkv > 1) {
@@ -814,7 +830,12 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             KCHK(lmk_attn_decode(s, m->d_q, kc, vc, m->kv_f32, pos, slot, M, m->H, m->Hkv, m->hd,
                                  m->max_seq, NULL, m->d_a16));
         }
-        if (sep_wo) {
+        if (fold_wo) {
+            memset(&ep, 0, sizeof(ep));
+            ep.out = m->d_x; ep.ldc = D;
+            ep.gain = m->d_rms_ffn + (size_t)l * D; ep.u = m->d_xn16; ep.ss = m->d_ss; ep.nss = D / 32;
+            KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, LMK_EPI_RESNORM, &ep));
+        } else if (sep_wo) {
             if (ns_wo > 1) {
                 KCHK(lmk_gemm_split(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, ns_wo, m->d_part));
             } else {
@@ -833,8 +854,19 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
         }
         memset(&ep, 0, sizeof(ep));
         ep.g = m->d_g16; ep.F = F;
+        if (fold_wo) { ep.rs_ss = m->d_ss; ep.nss = D / 32; }
         KCHK(lmk_gemm(s, m->d_xn16, D, lw + m->off_w13, M, 2 * F, D, LMK_EPI_GATE, &ep));
-        if (sep_w2) {
+        rs_next = fold_w2 && l + 1 < m->L;
+        if (fold_w2) {
+            memset(&ep, 0, sizeof(ep));
+            ep.out = m->d_x; ep.ldc = D;
+            if (l + 1 < m->L) {   /* u of the next layer's attention norm */
+                ep.gain = m->d_rms_att + (size_t)(l + 1) * D; ep.u = m->d_xn16; ep.ss = m->d_ss;
+                ep.nss = D / 32;
+            }
+            KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F,
+                          l + 1 < m->L ? LMK_EPI_RESNORM : LMK_EPI_RESID, &ep));
+        } else if (sep_w2) {
             if (ns_w2 > 1) {
                 KCHK(lmk_gemm_split(s, m->d_g16, F, lw + m->off_w2, M, D, F, ns_w2, m->d_part));
             } else {

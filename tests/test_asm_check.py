@@ -40,6 +40,24 @@ def test_passes_use_after_wait_and_unrelated_work():
     assert len(names) == 1 and not bad
 
 
+def test_partial_wait_retires_only_older_reads():
+    """lgkmcnt(1) after two LDS reads retires the older one only (LDS operations
+    complete in order)."""
+    two = "\tds_read_b128 v[4:7], v1\n\tds_read_b128 v[8:11], v1 offset:32\n\ts_waitcnt lgkmcnt(1)\n"
+    assert not check_lds_asm.check(HEAD + two + "\tv_mul_f32_e32 v20, v4, v20\n" + TAIL)[1]
+    assert len(check_lds_asm.check(HEAD + two + "\tv_mul_f32_e32 v20, v8, v20\n" + TAIL)[1]) == 1
+
+
+def test_partial_wait_with_scalar_load_retires_nothing():
+    """A scalar load in flight can complete out of order: lgkmcnt(1) then
+    retires no LDS read."""
+    asm = HEAD + ("\tds_read_b128 v[4:7], v1\n"
+                  "\ts_load_dwordx2 s[0:1], s[4:5], 0x0\n"
+                  "\ts_waitcnt lgkmcnt(1)\n"
+                  "\tv_mul_f32_e32 v20, v4, v20\n") + TAIL
+    assert len(check_lds_asm.check(asm)[1]) == 1
+
+
 @pytest.mark.skipif(os.path.exists("/dev/kfd"),
                     reason="build check: runs where the library is built, not on a GPU host "
                            "(no child processes next to an initialised GPU)")

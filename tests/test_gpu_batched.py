@@ -163,6 +163,35 @@ def test_prefill_long_blocks_match_oracle(lm, orc, name, d, kv32):
     m.close()
 
 
+FOLD_WO = dict(dim=768, hidden_dim=2048, n_layers=3, n_heads=12, n_kv_heads=12, vocab_size=512,
+               seq_len=256)
+FOLD_BOTH = dict(dim=2048, hidden_dim=5632, n_layers=3, n_heads=16, n_kv_heads=8, vocab_size=512,
+                 seq_len=128)
+
+
+@pytest.mark.parametrize("name,d,nseq,kv32", [("wo", FOLD_WO, 8, False), ("wo_w2", FOLD_BOTH, 4, True)])
+def test_prefill_folded_norms_match_oracle(lm, orc, name, d, nseq, kv32):
+    """Prefill chunks whose unsplit Wo (and W2) carry the row norm that
+    follows them: the GEMM adds its product to x and writes x * gain with the
+    sums of squares of x, and the next GEMM scales its rows by the norm.  At
+    2048 rows of dim 768 only Wo is unsplit (W2 is K-split: its partials go
+    through the row norm); at 512 rows of dim 2048 both are (64 sums per row),
+    so layer l+1's QKV scales its rows as well."""
+    _say(f"[prefill folded norms {name}]")
+    S, D, F = d["seq_len"], d["dim"], d["hidden_dim"]
+    M = nseq * S
+    assert lm.gemm_split_count(M, D, D) == 1
+    assert (lm.gemm_split_count(M, D, F) == 1) == (name == "wo_w2")
+    m, w16 = make(lm, d, 47, nseq, S, kv32)
+    toks = np.random.default_rng(47).integers(0, d["vocab_size"], (nseq, S)).astype(np.int32)
+    lg = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    w32 = lm.f16_to_f32(w16)
+    for i in (0, nseq - 1):
+        ref = orc.Oracle(cfg7(d), w32, True, S, kv_f16=not kv32).forward_full(toks[i])
+        close_enough(lg[i * S:(i + 1) * S], ref)
+    m.close()
+
+
 def _batched_decode_vs_oracle(lm, orc, d, B, seed, kv32=False):
     """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
     decode path) against the oracle, then greedy runs."""
