@@ -19,8 +19,10 @@ Alongside the headline the JSON line carries:
                 event-bracketed dispatches are not used); every family's time
                 is in kernel_us_per_launch
   step_roofline the whole token: algorithmic bytes per token / time per token
-  configs       C1-C4 (MFMA paths) and C0 in the reference's own algorithm (a
-                256-position window forward per token, generate.m:427-516)
+  configs       C1-C4 (MFMA paths), C0 in the reference's own algorithm (a
+                256-position window forward per token, generate.m:427-516),
+                C0 with the binary16 K/V cache, and C0 per-token time warm
+                against after a sweep that evicts the Infinity Cache
   cpu_baseline  the reference's portable CPU forward with OpenBLAS in place of
                 Accelerate (oracle/cpu_ref.c) on this host's cores: C0 KV-cache
                 decode (its ids compared with the GPU's), and under "configs"
@@ -212,6 +214,59 @@ def c0_kv16(S, cfg, w16, ids, direct, seqs=8):
             "us_per_token": round(ms * 1e3 / (seqs * SEQ), 3),
             "first_id_differing_from_fp32_cache": int(diff[0]) if diff.size else None,
             "sample": f"{seqs} timed 256-token greedy sequences from token id 1"}
+
+
+def c0_cold_cache(S, cfg, w16, ids, sweep_mib=512):
+    """C0 with and without a cache sweep before every token.  The decode
+    working set (219 MB of fp16 weights, the K/V cache and activations) fits
+    the 256 MB Infinity Cache, so a warm token may be served partly from it
+    rather than from HBM.  Both legs run the 255 decode steps of a C0 sequence
+    one call each (lm_generate_greedy of one step: its graph replay, the id
+    copied back to the host), timed by hipEvents on the model's stream around
+    the call; the cold leg first copies a sweep_mib MiB buffer into another
+    (sweep_mib MiB read + written, twice the cache) and waits for the copy, so
+    the token starts with the weights evicted from the L2s and the Infinity
+    Cache.  cold_minus_warm_us is the cost of fetching from HBM what a warm
+    token finds in the caches."""
+    import ctypes
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    hip = ctypes.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    n = int(sweep_mib) << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), n) or hip.hipMalloc(ctypes.byref(b), n):
+        raise SystemExit("c0_cold_cache: hipMalloc failed")
+    if hip.hipMemset(a, 1, ctypes.c_size_t(n)) or hip.hipDeviceSynchronize():
+        raise SystemExit("c0_cold_cache: hipMemset failed")
+    m = S.Model.create(cfg, w16, True, 1, SEQ)
+    m.set_option(S.LM_OPT_KV_F32, 1)
+    toks = np.concatenate([[1], np.asarray(ids[:SEQ - 2])]).astype(np.int32)
+
+    def leg(cold):
+        total = 0.0
+        for p, t in enumerate(toks):
+            if cold and (hip.hipMemcpy(b, a, n, 3) or hip.hipDeviceSynchronize()):
+                raise SystemExit("c0_cold_cache: sweep copy failed")
+            m.timer_begin()
+            got = m.generate_greedy([int(t)], [p], 1)[0, 0]
+            total += m.timer_end()
+            if got != ids[p]:
+                raise SystemExit(f"c0_cold_cache: step {p} gave id {got}, the timed run {ids[p]}")
+        return total * 1e3 / toks.size
+    leg(False)
+    warm = leg(False)
+    cold = leg(True)
+    m.close()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    return {"warm_us_per_token": round(warm, 3), "cold_us_per_token": round(cold, 3),
+            "cold_minus_warm_us": round(cold - warm, 3),
+            "sample": f"the {toks.size} decode steps of one C0 sequence, one lm_generate_greedy call "
+                      f"each (graph replay + id to the host), cold: a {2 * sweep_mib} MiB device copy "
+                      f"(read + write) before every step"}
 
 
 MFMA_PEAK_TFLOPS = 2500.0      # dense fp16
@@ -487,6 +542,7 @@ def main():
         out["configs"]["c0_reference_algorithm"] = ra
         if not args.kv16:
             out["configs"]["c0_kv16"] = c0_kv16(S, cfg, w16, ids, args.direct)
+            out["configs"]["c0_cold_cache"] = c0_cold_cache(S, cfg, w16, ids)
         out["vs_baseline_same_algorithm"] = round(ra["value"] / REF_TOK_S, 1)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg.astuple(), w16, S, ids, args.cpu_seconds)
