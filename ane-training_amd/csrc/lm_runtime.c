@@ -60,7 +60,9 @@ struct LMModel {
     uint16_t *d_g16;            /* gate rows in fp16 (input of the W2 GEMM)    */
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
-    int *d_rtok, *d_rpos, *d_rslot;   /* prefill rows: token, position, slot */
+    int *d_rin;                 /* prefill rows of a chunk of R: tokens, positions, slots
+                                 * (R ints each, back to back), copied in one piece */
+    int *h_rin;                 /* their pinned host staging                        */
     /* per-slot greedy state */
     int *d_tok, *d_pos, *d_hist, *d_slot_id;
     /* batch 1-4 chain: QKV, attention (fuse_qa >= 1), Wo (>= 2) and the FFN
@@ -320,13 +322,14 @@ static void drop_graphs(LMModel *m)
 static void free_rows(LMModel *m)
 {
     void *dev[] = {m->d_x, m->d_q, m->d_attn, m->d_g, m->d_logits, m->d_ss, m->d_part, m->d_g16,
-                   m->d_xn16, m->d_a16, m->d_amax, m->d_rtok, m->d_rpos, m->d_rslot};
+                   m->d_xn16, m->d_a16, m->d_amax, m->d_rin};
     for (size_t i = 0; i < sizeof(dev) / sizeof(dev[0]); i++)
         if (dev[i]) hipFree(dev[i]);
+    if (m->h_rin) hipHostFree(m->h_rin);
     m->d_x = m->d_q = m->d_attn = m->d_g = m->d_logits = m->d_ss = m->d_part = NULL;
     m->d_g16 = m->d_xn16 = m->d_a16 = NULL;
     m->d_amax = NULL;
-    m->d_rtok = m->d_rpos = m->d_rslot = NULL;
+    m->d_rin = m->h_rin = NULL;
     m->max_rows = 0;
 }
 
@@ -359,9 +362,11 @@ static int alloc_rows(LMModel *m, int R)
         if ((st = dev_alloc((void **)&m->d_part, n * 4))) return st;
     }
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
-    if ((st = dev_alloc((void **)&m->d_rtok, r * 4))) return st;
-    if ((st = dev_alloc((void **)&m->d_rpos, r * 4))) return st;
-    if ((st = dev_alloc((void **)&m->d_rslot, r * 4))) return st;
+    if ((st = dev_alloc((void **)&m->d_rin, 3 * r * 4))) return st;
+    if (hipHostMalloc((void **)&m->h_rin, 3 * r * 4, 0) != hipSuccess) {
+        m->h_rin = NULL;
+        return LM_ERR_OOM;
+    }
     m->max_rows = R;
     return LM_OK;
 }
@@ -1114,13 +1119,14 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
  * `logits` (may be NULL) receives them in sequence order; the last chunk's
  * logits stay in d_logits. */
 /* The layers of a prefill chunk of R rows (sequences of S rows; tokens,
- * positions and slots in d_rtok / d_rpos / d_rslot) and, with `all`, the
+ * positions and slots in d_rin, R ints each) and, with `all`, the
  * classifier into d_logits: replayed from a captured graph of that shape
  * (captured on first use) unless graphs are off. */
 static int run_rows(LMModel *m, int R, int S, int all)
 {
+    const int *tok = m->d_rin, *pos = m->d_rin + R, *slot = m->d_rin + 2 * (size_t)R;
     if (!m->use_graph)
-        return enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot, all ? m->d_logits : NULL, all);
+        return enqueue_rows(m, R, S, tok, pos, slot, all ? m->d_logits : NULL, all);
     int k = 0;
     while (k < PREFILL_GRAPHS &&
            !(m->pgraph[k].ge && m->pgraph[k].R == R && m->pgraph[k].S == S && m->pgraph[k].all == all))
@@ -1134,8 +1140,7 @@ static int run_rows(LMModel *m, int R, int S, int all)
         }
         hipGraph_t g;
         HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_rows(m, R, S, m->d_rtok, m->d_rpos, m->d_rslot,
-                                    all ? m->d_logits : NULL, all);
+        const int rc = enqueue_rows(m, R, S, tok, pos, slot, all ? m->d_logits : NULL, all);
         hipError_t e = hipStreamEndCapture(m->stream, &g);
         if (rc) return rc;
         HIPCHK(e);
@@ -1184,8 +1189,7 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
     const int chunk_rows = (nseq < cs ? nseq : cs) * S;
     int rc;
     if (chunk_rows > m->max_rows && (rc = alloc_rows(m, chunk_rows))) return rc;
-    int *h = (int *)malloc((size_t)3 * chunk_rows * sizeof(int));
-    if (!h) return LM_ERR_OOM;
+    int *h = m->h_rin;   /* pinned; each chunk ends with a stream synchronise */
     rc = LM_OK;
     for (int i0 = 0; i0 < nseq && rc == LM_OK; i0 += cs) {
         const int n = nseq - i0 < cs ? nseq - i0 : cs;
@@ -1197,9 +1201,7 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
                 h[R + r] = pos0[i0 + i] + t;
                 h[2 * R + r] = slots[i0 + i];
             }
-        if (hipMemcpyAsync(m->d_rtok, h, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
-            hipMemcpyAsync(m->d_rpos, h + R, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess ||
-            hipMemcpyAsync(m->d_rslot, h + 2 * R, (size_t)R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess) {
+        if (hipMemcpyAsync(m->d_rin, h, (size_t)3 * R * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess) {
             rc = LM_ERR_HIP;
             break;
         }
@@ -1225,7 +1227,9 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
         }
         if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
     }
-    free(h);
+    /* after a failure, let the copy out of the staging buffer finish before
+     * a later call refills it */
+    if (rc != LM_OK) (void)hipStreamSynchronize(m->stream);
     return rc;
 }
 
