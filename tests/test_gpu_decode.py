@@ -148,6 +148,21 @@ def test_stories_c0_greedy_ids_fp32_cache(lm):
     m.close()
 
 
+def test_stories_c0_ids_stable_over_repeated_runs(lm):
+    """The C0 greedy run repeated 64 times on one model (16,384 tokens, 212,992
+    whole-layer and classifier launches with their tagged hand-offs, the step
+    tag advancing throughout): every run's ids equal the reference forward's,
+    and no hand-off wait gives up (that would raise)."""
+    _say("[stories C0 repeated greedy runs]")
+    fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
+    m, _ = _stories(lm, True)
+    for r in range(64):
+        ids = m.generate_greedy([1], [0], 256)[:, 0]
+        bad = np.where(ids != fx["ids_kv32"])[0]
+        assert bad.size == 0, f"run {r}: first divergence at step {bad[:5]}"
+    m.close()
+
+
 def test_stories_c0_greedy_ids_fp16_cache(lm):
     _say("[stories C0 greedy kv16]")
     fx = np.load(os.path.join(GOLDEN, "stories_c0.npz"))
