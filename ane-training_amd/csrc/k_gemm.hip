@@ -30,7 +30,8 @@
  *                  2 x 2), 256 x 128 for the largest (eight waves 4 x 2), 128 x 128
  *                  (eight waves) K-split in 2 for long-K narrow GEMMs of 1024+
  *                  rows, 64 x 128 for decode-row classifiers, 32 x 64 for up to
- *                  32 rows (two waves); K streamed by direct global->LDS loads into a ring of
+ *                  32 rows (two waves), 32 x 32 (one wave) for decode-row gate
+ *                  GEMMs of few tiles; K streamed by direct global->LDS loads into a ring of
  *                  64-wide stages (3 deep for prefill, 4 for decode rows, 6 for
  *                  32-row gate tiles); XCD-aware tile order; an optional K-split
  *                  over blockIdx.y (fp32 partials, summed by the kernel that
@@ -354,11 +355,11 @@ __device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
  * BN/2 gates, then written with one 16-byte store per 8 gates instead of one
  * 2-byte store per gate.  sg: LDS of at least BM * (BN/2 + 8) halves, no longer
  * read by any wave's main loop. */
-template <int BM, int BN, int TM, int TN, int WVM>
+template <int BM, int BN, int TM, int TN, int WVM, int WVN>
 __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *sg, int m0, int n0,
                                               int wm, int wn, const EpiArgs &e)
 {
-    constexpr int NT = 128 * WVM;   /* threads: WVM x 2 waves */
+    constexpr int NT = 64 * WVM * WVN;   /* threads: WVM x WVN waves */
     constexpr int GW = BN / 2, GLD = GW + 8;
     const int lane = threadIdx.x & 63, c = lane & 31;
     const bool lo = c < 16;
@@ -368,7 +369,7 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int rl = wm * (BM / WVM) + i * 32 + 4 * (lane >> 5);
-            const int gl = (wn * (BN / 2) + j * 32) / 2 + (c & 15);
+            const int gl = (wn * (BN / WVN) + j * 32) / 2 + (c & 15);
 #pragma unroll
             for (int k = 0; k < 16; k += 2) {
                 /* lane c < 16: row of element k (h1 own, h3 from lane c + 16);
@@ -508,20 +509,21 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
     }
 }
 
-template <int BM, int BN, int E, int NS, int WVM, bool RS = false>
-__global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__ A, int lda,
+template <int BM, int BN, int E, int NS, int WVM, bool RS = false, int WVN = 2>
+__global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                          const u16 *__restrict__ W, int K, int kc,
                                                          EpiArgs e, int tm, int tn)
 {
-    constexpr int NWV = 2 * WVM;                /* waves: WVM along M x 2 along N */
-    constexpr int WM = BM / WVM, WN = BN / 2;   /* wave tile */
+    constexpr int NWV = WVM * WVN;                /* waves: WVM along M x WVN along N */
+    constexpr int WM = BM / WVM, WN = BN / WVN;   /* wave tile */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
     constexpr int ROWS = BM + BN;               /* tile rows per stage */
     constexpr int STAGE = ROWS * 64;            /* halves per stage (128 B per row) */
     constexpr int LDW = ROWS / 8 / NWV;         /* load instructions per wave per stage */
     static_assert(TM >= 1 && TN >= 1 && LDW >= 1 && ROWS % (8 * NWV) == 0, "tile shape");
     /* the LDS-staged QKV epilogue is written for four waves */
-    static_assert(WVM == 2 || E != EPI_QKV, "wave layout");
+    static_assert((WVM == 2 && WVN == 2) || E != EPI_QKV, "wave layout");
+    static_assert(WVN == 1 || WVN == 2, "one or two waves along N");
     static_assert(NS >= 3 && NS <= 8 && LDW * (NS - 2) <= 63, "ring depth (vmcnt holds 63)");
     /* the NS stage buffers are separate arrays (not one indexed ring) so that
      * the compiler can tell a stage's LDS reads from the direct loads in flight
@@ -544,7 +546,7 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = WVN == 2 ? wave >> 1 : wave, wn = WVN == 2 ? wave & 1 : 0;
     /* XCD-aware tile order: work-group id goes to XCD id % 8; give each XCD a
      * contiguous run of tiles (M fastest), i.e. a slice of N, so the W rows of
      * its tiles stay in its own L2. */
@@ -688,7 +690,7 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
      * in the unscaled kernels the extra arguments and branches delayed the
      * start of every tile (C1's GEMMs 5% slower with the scale unused). */
     static_assert(!RS || E == EPI_GATE || E == EPI_QKV, "row scale before a gate or QKV epilogue");
-    static_assert(!RS || BM <= 128 * WVM, "a thread per tile row");
+    static_assert(!RS || BM <= 64 * NWV, "a thread per tile row");
     constexpr int MAXV = RS ? 16 : 1;   /* float4s per row: nss <= 64 */
     __shared__ float rs_sh[RS ? BM : 1];
     float4 ssv[MAXV];
@@ -737,7 +739,7 @@ __global__ void __launch_bounds__(128 * WVM) k_gemm_tile(const u16 *__restrict__
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
     if constexpr (E == EPI_GATE) {
         static_assert(BM * (BN / 2 + 8) <= STAGE, "gate staging fits one stage buffer");
-        gate_tile_lds<BM, BN, TM, TN, WVM>(acc, lds0, m0, n0, wm, wn, e);
+        gate_tile_lds<BM, BN, TM, TN, WVM, WVN>(acc, lds0, m0, n0, wm, wn, e);
         return;
     }
     if constexpr (QKV_LDS) {
@@ -1045,6 +1047,9 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
     if constexpr (BM == 256 && E != EPI_QKV) {   /* eight waves (4 x 2): two per SIMD */
         hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 4, RS>), dim3(tm * tn), dim3(512), 0, s, (const u16 *)A,
                            lda, (const u16 *)W, K, K, e, tm, tn);
+    } else if constexpr (BM == 32 && BN == 32) {   /* one wave */
+        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS, 1>),
+                           dim3(tm * tn), dim3(64), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
     } else if constexpr (BM == 32) {               /* two waves (1 x 2) over 32 rows */
         hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS>), dim3(tm * tn),
                            dim3(128), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
@@ -1088,8 +1093,13 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * the LDS-staged QKV epilogue keeps its four-wave 64-row tile), and so does
  * the gate GEMM of 33-64 decode rows, which cannot be K-split: two row tiles
  * per column tile put 128 work-groups instead of 64 on the 64-row W1/W3 of
- * Stories (C2 0.4690/0.4683 -> 0.4643/0.4641 ms/step, same box).  K is a
- * multiple of the 64-wide stage. */
+ * Stories (C2 0.4690/0.4683 -> 0.4643/0.4641 ms/step, same box).  A gate GEMM
+ * of up to 64 rows whose 32 x 64 tiles would leave half the CUs or more
+ * without a work-group takes 32 x 32 tiles of one wave instead (twice the
+ * work-groups; each 32-column tile is 16 W1 rows and their 16 W3 partners):
+ * C2 0.4618-0.4627 -> 0.4580-0.4583 ms/step, while the scaled model's 176
+ * gate tiles of 32 rows lost 1.6% as 352 one-wave tiles.  K is a multiple of
+ * the 64-wide stage. */
 template <int E, bool RS = false>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
@@ -1104,7 +1114,9 @@ static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t
         } else launch_tile<64, 64, E, true>(s, A, lda, W, M, N, K, e);
     } else if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
-    else if (E != EPI_QKV && (M <= 32 || (E == EPI_GATE && M <= 64))) {
+    else if (E == EPI_GATE && M <= 64 && (long)((M + 31) / 32) * ((N + 63) / 64) <= 128) {
+        if constexpr (E == EPI_GATE) launch_tile<32, 32, E>(s, A, lda, W, M, N, K, e);
+    } else if (E != EPI_QKV && (M <= 32 || (E == EPI_GATE && M <= 64))) {
         if constexpr (E != EPI_QKV) launch_tile<32, 64, E>(s, A, lda, W, M, N, K, e);
     } else launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
     return hipGetLastError();
