@@ -80,6 +80,31 @@ def test_prefill_at_offset(lm, orc):
     m.close()
 
 
+@pytest.mark.parametrize("name,d", [("gqa", TINY_GQA), ("hd128", TINY_HD128)])
+def test_prefill_of_one_and_two_tokens(lm, orc, name, d):
+    """Prompts of one and two tokens: a one-token chunk's row takes the decode
+    attention kernel inside the prefill path.  At position 0, then after the
+    earlier prefills (the cache they left serving each next one and a decode
+    step), against the oracle's forward of the whole sequence; then one token
+    in each of four slots in one batch, against the oracle's one-token
+    forward."""
+    _say(f"[prefill 1-2 tokens {name}]")
+    m, w16 = make(lm, d, 44, 4, 64)
+    w32 = lm.f16_to_f32(w16)
+    toks = np.random.default_rng(44).integers(0, d["vocab_size"], 8).astype(np.int32)
+    ref = orc.Oracle(cfg7(d), w32, True, 64, kv_f16=True).forward_full(toks[:5])
+    close_enough(m.prefill(toks[:1], slot=0), ref[:1])              # one token at 0
+    close_enough(m.prefill(toks[1:3], slot=0, pos0=1), ref[1:3])    # two tokens at 1
+    close_enough(m.prefill(toks[3:4], slot=0, pos0=3), ref[3:4])    # one token at 3
+    close_enough(m.forward(int(toks[4]), 4), ref[4])                # decode from that cache
+    one = orc.Oracle(cfg7(d), w32, True, 64, kv_f16=True).forward_full(toks[5:6])[0]
+    lg = m.prefill_batch(np.tile(toks[5:6], (4, 1)), slots=np.array([2, 0, 3, 1], np.int32),
+                         mode=lm.LM_LOGITS_ALL)
+    for i in range(4):
+        close_enough(lg[i], one)
+    m.close()
+
+
 @pytest.mark.parametrize("mode", ["all", "last"])
 def test_prefill_batch_matches_oracle(lm, orc, mode):
     _say(f"[prefill batch {mode}]")
