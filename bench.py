@@ -23,6 +23,9 @@ Alongside the headline the JSON line carries:
                 256-position window forward per token, generate.m:427-516),
                 C0 with the binary16 K/V cache, and C0 per-token time warm
                 against after a sweep that evicts the Infinity Cache
+  device_copy_rate  a plain device-to-device copy's bytes read + written per
+                second on this GPU (what a stream reaches, beside the
+                published 8 TB/s the fractions use)
   cpu_baseline  the reference's portable CPU forward with OpenBLAS in place of
                 Accelerate (oracle/cpu_ref.c) on this host's cores: C0 KV-cache
                 decode (its ids compared with the GPU's), and under "configs"
@@ -403,6 +406,48 @@ def calibration_copy(mbytes):
         raise SystemExit("calibration copy failed")
 
 
+def device_copy_rate(mib=1024, reps=5):
+    """The device-to-device copy rate on this GPU (hipMemcpy of mib MiB, the
+    runtime's copy kernel, timed by hipEvents over reps queued copies after one
+    untimed): bytes read + written per second.  Context for the HBM fractions,
+    which are against the published 8 TB/s: this is what a plain stream
+    reaches here."""
+    import ctypes
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    hip = ctypes.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+    vp = ctypes.c_void_p
+    hip.hipMalloc.argtypes = [ctypes.POINTER(vp), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpyAsync.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]
+    hip.hipMemset.argtypes = [vp, ctypes.c_int, ctypes.c_size_t]
+    hip.hipFree.argtypes = [vp]
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+    hip.hipEventRecord.argtypes = [vp, vp]
+    hip.hipEventSynchronize.argtypes = [vp]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+    hip.hipEventDestroy.argtypes = [vp]
+    n = int(mib) << 20
+    a, b, e0, e1 = vp(), vp(), vp(), vp()
+    if hip.hipMalloc(ctypes.byref(a), n) or hip.hipMalloc(ctypes.byref(b), n):
+        raise SystemExit("device_copy_rate: hipMalloc failed")
+    ms = ctypes.c_float(0)
+    rc = hip.hipMemset(a, 1, ctypes.c_size_t(n)) or hip.hipMemcpy(b, a, n, 3) or \
+        hip.hipEventCreate(ctypes.byref(e0)) or hip.hipEventCreate(ctypes.byref(e1)) or \
+        hip.hipEventRecord(e0, None)
+    for _ in range(reps):   # queued back to back on the null stream
+        rc = rc or hip.hipMemcpyAsync(b, a, n, 3, None)
+    rc = rc or hip.hipEventRecord(e1, None) or hip.hipEventSynchronize(e1) or \
+        hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1)
+    hip.hipEventDestroy(e0)
+    hip.hipEventDestroy(e1)
+    hip.hipFree(a)
+    hip.hipFree(b)
+    if rc or ms.value <= 0:
+        raise SystemExit("device_copy_rate: copy timing failed")
+    return {"value": round(2 * n * reps / (ms.value * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "sample": f"{reps} device-to-device copies of {mib} MiB (hipMemcpy), bytes read + written"}
+
+
 def under_profiler():
     """True inside rocprofv3 (its preloaded tool library and ROCPROF* variables):
     event-bracketed dispatches (lm_profile_chain) are then not used."""
@@ -543,6 +588,7 @@ def main():
         if not args.kv16:
             out["configs"]["c0_kv16"] = c0_kv16(S, cfg, w16, ids, args.direct)
             out["configs"]["c0_cold_cache"] = c0_cold_cache(S, cfg, w16, ids)
+        out["device_copy_rate"] = device_copy_rate()
         out["vs_baseline_same_algorithm"] = round(ra["value"] / REF_TOK_S, 1)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg.astuple(), w16, S, ids, args.cpu_seconds)
