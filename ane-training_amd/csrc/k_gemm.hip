@@ -1158,8 +1158,14 @@ extern "C" int lmk_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_
 
 /* K-split count (measured on MI355X): K is cut into the fewest splits whose
  * k-chunks (a multiple of 64) are at most 512 long, for decode rows (M <= 64,
- * up to LMK_MAX_SPLIT splits) and for prefill GEMMs with fewer than 128 tiles
- * of 64 x 64 (up to LMK_MAX_ROW_SPLIT); larger GEMMs are not split. */
+ * up to LMK_MAX_DEC_SPLIT splits) and for prefill GEMMs with fewer than 128
+ * tiles of 64 x 64 (up to LMK_MAX_ROW_SPLIT); larger GEMMs are not split.
+ * Decode rows stop at 8 splits even where more would give every CU a
+ * work-group: each split adds a partial that is written, read back and summed
+ * by the row norm, which loads eight partials per memory round trip.  The
+ * W2 of 64 Stories rows at 8 splits instead of 16: C2 0.4580-0.4589 ->
+ * 0.4482-0.4490 ms/step; the scaled model's 32-row W2 at 8 instead of 11:
+ * C4 1.180-1.182 -> 1.146-1.150 ms/step (6 or 4 were slower on both). */
 /* Long-K narrow GEMMs of many rows (the 2048-row W2) run 128 x 128 tiles of
  * eight waves K-split in 2: 12.8 us against 14.5 for unsplit 64 x 64 tiles at
  * C3's W2, while the row norm that adds the partials reads the second one for
@@ -1168,7 +1174,7 @@ static bool wide_split(int M, int N, int K) { return M >= 1024 && N <= 1024 && K
 
 extern "C" int lmk_pick_split(int M, int N, int K)
 {
-    int cap = LMK_MAX_SPLIT;
+    int cap = LMK_MAX_DEC_SPLIT;
     if (M > 64) {
         if (wide_split(M, N, K)) return 2;
         if ((long)((M + 63) / 64) * ((N + 63) / 64) >= 128) return 1;

@@ -206,6 +206,7 @@ void lmk_time_next(hipEvent_t start, hipEvent_t stop);
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
  * A W^T; lmk_pick_split chooses ns for a shape (1: do not split). */
 #define LMK_MAX_SPLIT 16
+#define LMK_MAX_DEC_SPLIT 8    /* most splits lmk_pick_split gives for M <= 64 */
 #define LMK_MAX_ROW_SPLIT 4    /* most splits lmk_pick_split gives for M > 64 */
 int lmk_pick_split(int M, int N, int K);
 int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
