@@ -29,7 +29,7 @@
  *   k_gemm_tile    work-group tile BM x BN: 64 x 64 for most shapes (four waves
  *                  2 x 2), 256 x 128 for the largest (eight waves 4 x 2), 128 x 128
  *                  (eight waves) K-split in 2 for long-K narrow GEMMs of 1024+
- *                  rows, 64 x 128 for decode-row classifiers, 32 x 64 for up to
+ *                  rows, 64 x 64 also for decode-row classifiers, 32 x 64 for up to
  *                  32 rows (two waves), 32 x 32 (one wave) for decode-row gate
  *                  GEMMs of few tiles; K streamed by direct global->LDS loads into a ring of
  *                  64-wide stages (3 deep for prefill, 4 for decode rows, 6 for
@@ -1087,7 +1087,9 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * 64 x 64 tiles everywhere, since four of them share a CU and hide each
  * other's latency, except for GEMMs big enough to give every CU a 256 x 128
  * tile (classifiers, the 2048-row W1/W3), where the larger tile's lower L2
- * traffic wins; a decode-row classifier (N >= 16384) takes a 64 x 128 tile;
+ * traffic wins; a decode-row classifier (N >= 16384, which cannot be K-split
+ * ahead of its argmax) takes 64 x 64 tiles, twice the work-groups of 64 x 128
+ * (C2 0.4480 -> 0.4434, C4 1.148 -> 1.142 ms/step; 32 x 64 lost at C2);
  * up to 32 rows take 32 x 64 tiles of two waves (a 64-row tile would stage and
  * multiply half padding: 5% faster on the scaled model's 32-row QKV and W2;
  * the LDS-staged QKV epilogue keeps its four-wave 64-row tile), and so does
@@ -1112,7 +1114,9 @@ static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t
         if (E == EPI_GATE && (long)((M + 255) / 256) * ((N + 127) / 128) >= 240) {
             if constexpr (E == EPI_GATE) launch_tile<256, 128, E, true>(s, A, lda, W, M, N, K, e);
         } else launch_tile<64, 64, E, true>(s, A, lda, W, M, N, K, e);
-    } else if (M <= 64 && N >= 16384) launch_tile<64, 128, E>(s, A, lda, W, M, N, K, e);
+    } else if (M <= 64 && N >= 16384) {
+        if constexpr (E != EPI_QKV) launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
+    }
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
     else if (E == EPI_GATE && M <= 64 && (long)((M + 31) / 32) * ((N + 63) / 64) <= 128) {
         if constexpr (E == EPI_GATE) launch_tile<32, 32, E>(s, A, lda, W, M, N, K, e);
