@@ -252,21 +252,26 @@ __device__ __forceinline__ void tag_store(unsigned long long *w, float v, unsign
     __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* Poll one tagged word until it carries `tag` (bounded: a wait that gives up
- * after err[1] polls sets err[0] and returns the word's value as it is).  A
- * wait also stops early once err[0] is set, so that after one wait has given
- * up the rest of the launch, and the launches queued behind it, end within
- * microseconds; the host reads the flag after the step and reports the
- * failure. */
+/* Poll one tagged word until it carries `tag`.  The wait is bounded in real
+ * time: err[1] is its limit in microseconds of the 100 MHz real-time counter
+ * (s_memrealtime), so it ends however slowly polls return (a profiler's
+ * counter pass, a busy memory system); one that gives up sets err[0] and
+ * returns the word's value as it is.  A wait also stops at once when err[0]
+ * is set (checked before the first sleep and every 256 polls after), so that
+ * after one wait has given up, or after the host has raised the flag, the
+ * rest of the launch and the launches queued behind it end within
+ * microseconds; the host reads the flag with the call's results and reports
+ * the failure. */
 __device__ __forceinline__ float tag_wait(const unsigned long long *w, unsigned tag, int *err)
 {
     unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((unsigned)(v >> 32) == tag) return __builtin_bit_cast(float, (unsigned)v);
-    const int lim = err[1];
+    const unsigned long long lim = 100ull * (unsigned)err[1];   /* us -> 10 ns ticks */
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     for (int spin = 0; (unsigned)(v >> 32) != tag; spin++) {
         if ((spin & 255) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
             break;
-        if (spin >= lim) {
+        if ((spin & 15) == 15 && __builtin_amdgcn_s_memrealtime() - t0 > lim) {
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }

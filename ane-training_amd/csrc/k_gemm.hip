@@ -1115,7 +1115,9 @@ static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t
             if constexpr (E == EPI_GATE) launch_tile<256, 128, E, true>(s, A, lda, W, M, N, K, e);
         } else launch_tile<64, 64, E, true>(s, A, lda, W, M, N, K, e);
     } else if (M <= 64 && N >= 16384) {
-        if constexpr (E != EPI_QKV) launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
+        /* decode-row classifiers (and any other wide decode-row GEMM, the
+         * QKV epilogue included) on 64 x 64 tiles */
+        launch_tile<64, 64, E>(s, A, lda, W, M, N, K, e);
     }
     else if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 240) launch_tile<256, 128, E>(s, A, lda, W, M, N, K, e);
     else if (E == EPI_GATE && M <= 64 && (long)((M + 31) / 32) * ((N + 63) / 64) <= 128) {

@@ -20,6 +20,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "lm_internal.h"
@@ -29,7 +30,9 @@
 
 static __device__ __attribute__((aligned(256))) LMArgPart scratch[NOALLOC_MAX_PARTS];
 
-static LMArgPart *g_scratch[NOALLOC_MAX_DEVICES];   /* device address, per device */
+/* device address of `scratch`, per device: written once under the mutex with
+ * release order, read by the entry point with acquire order (no lock there) */
+static std::atomic<LMArgPart *> g_scratch[NOALLOC_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
 extern "C" int lmk_noalloc_setup(void)
@@ -39,11 +42,11 @@ extern "C" int lmk_noalloc_setup(void)
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (g_scratch[dev]) return hipSuccess;
+    if (g_scratch[dev].load(std::memory_order_relaxed)) return hipSuccess;
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
-    g_scratch[dev] = (LMArgPart *)p;
+    g_scratch[dev].store((LMArgPart *)p, std::memory_order_release);
     return hipSuccess;
 }
 
@@ -62,7 +65,10 @@ extern "C" int lm_gemm_argmax_noalloc(int M, int N, int K, const uint16_t *A, co
         return LM_ERR_RANGE;
     }
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES || !g_scratch[dev]) {
+    LMArgPart *part = nullptr;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < NOALLOC_MAX_DEVICES)
+        part = g_scratch[dev].load(std::memory_order_acquire);
+    if (!part) {
         fprintf(stderr, "stories_lm: lm_gemm_argmax_noalloc: lm_init has not set up this device\n");
         return LM_ERR_NOT_INIT;
     }
@@ -71,9 +77,9 @@ extern "C" int lm_gemm_argmax_noalloc(int M, int N, int K, const uint16_t *A, co
     memset(&ep, 0, sizeof(ep));
     ep.out = C;
     ep.ldc = N;
-    ep.part = g_scratch[dev];
+    ep.part = part;
     int e = lmk_gemm(s, A, K, W, M, N, K, LMK_EPI_ARGMAX, &ep);
-    if (e == 0) e = lmk_argmax_final(s, g_scratch[dev], nblk, M, ids, nullptr, nullptr, 0, nullptr);
+    if (e == 0) e = lmk_argmax_final(s, part, nblk, M, ids, nullptr, nullptr, 0, nullptr);
     if (e != 0) {
         fprintf(stderr, "stories_lm: lm_gemm_argmax_noalloc: launch failed: %s\n",
                 hipGetErrorString((hipError_t)e));

@@ -62,9 +62,11 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * reading work-group taking one copy, so that the readers of one value spread
  * over more memory channels. */
 #define LM_TAG_B 4
-/* Polls before a hand-off wait gives up (the second int of the flag buffer
- * the launchers take as `err`; about a second of polling). */
-#define LM_HANDOFF_SPINS (1 << 20)
+/* Microseconds (real-time counter) before a hand-off wait gives up: the
+ * second int of the flag buffer the launchers take as `err`.  Waits inside a
+ * launch last microseconds; the limit only ends a launch that cannot make
+ * progress. */
+#define LM_HANDOFF_US 100000
 #ifndef LM_TA_COPIES
 #define LM_TA_COPIES 4
 #endif
@@ -85,8 +87,8 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * x on through tagged words to W1/W3 work-groups (lmk_ffn13's work), and
  * those the gate to W2 work-groups that write x (lmk_w2_residual's work): the
  * whole layer in one launch.  err: two ints, the flag a hand-off wait that
- * gives up sets (the kernel still ends) and the polls before one does
- * (LM_HANDOFF_SPINS unless set by LM_OPT_HANDOFF_SPINS).  B <= 4, hd 64 or
+ * gives up sets (the kernel still ends) and the microseconds before one does
+ * (LM_HANDOFF_US unless set by LM_OPT_HANDOFF_US).  B <= 4, hd 64 or
  * 128. */
 int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,

@@ -19,6 +19,7 @@
  */
 #include "lm_internal.h"
 
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -45,6 +46,7 @@ struct LMModel {
     size_t layer_elems, off_wo, off_w13, off_w2;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
+    hipEvent_t ev_hand;         /* end of this handle's last hand-off launches */
     /* weights */
     uint16_t *d_layers, *d_embed, *d_wcls;
     float *d_rms_att, *d_rms_ffn, *d_rms_final;
@@ -112,37 +114,46 @@ const char *lm_strerror(int status)
     }
 }
 
-int lm_init(void)
+/* The device checks run once per process (pthread_once), so concurrent first
+ * calls from several threads neither race on the status nor repeat the
+ * setup; every call returns the one recorded status. */
+static pthread_once_t g_init_once = PTHREAD_ONCE_INIT;
+
+static void init_once(void)
 {
-    if (g_init_status <= 0) return g_init_status;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
         fprintf(stderr, "stories_lm: no HIP device visible\n");
         g_init_status = LM_ERR_NO_DEVICE;
-        return g_init_status;
+        return;
     }
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, 0) != hipSuccess) {
         g_init_status = LM_ERR_NO_DEVICE;
-        return g_init_status;
+        return;
     }
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
         fprintf(stderr, "stories_lm: device 0 is %s, kernels are built for gfx950\n",
                 p.gcnArchName);
         g_init_status = LM_ERR_NOT_GFX950;
-        return g_init_status;
+        return;
     }
     if (hipSetDevice(0) != hipSuccess) {
         g_init_status = LM_ERR_NO_DEVICE;
-        return g_init_status;
+        return;
     }
     if (lmk_noalloc_setup() != hipSuccess) {
         fprintf(stderr, "stories_lm: lookup of the static scratch's device address failed\n");
         g_init_status = LM_ERR_HIP;
-        return g_init_status;
+        return;
     }
     g_init_status = LM_OK;
-    return LM_OK;
+}
+
+int lm_init(void)
+{
+    if (pthread_once(&g_init_once, init_once) != 0) return LM_ERR_NOT_INIT;
+    return g_init_status;
 }
 
 int lm_device_info(LMDeviceInfo *out)
@@ -479,7 +490,8 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     if (!m->step_graph) FAIL(LM_ERR_OOM);
 
     if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) FAIL(LM_ERR_HIP);
-    if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
+    if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess ||
+        hipEventCreateWithFlags(&m->ev_hand, hipEventDisableTiming) != hipSuccess)
         FAIL(LM_ERR_HIP);
     if ((st = dev_alloc((void **)&m->d_layers, L * m->layer_elems * 2))) goto fail;
     if ((st = dev_alloc((void **)&m->d_embed, V * D * 2))) goto fail;
@@ -504,13 +516,13 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     const size_t ncls = (size_t)2 * LM_TAG_B * m->cls_nblk;
     if ((st = dev_alloc((void **)&m->d_cls_tw, ncls * 8))) goto fail;
     if ((st = dev_alloc((void **)&m->d_epoch, 4))) goto fail;
-    if ((st = dev_alloc((void **)&m->d_err, 8))) goto fail;   /* flag, poll limit */
+    if ((st = dev_alloc((void **)&m->d_err, 8))) goto fail;   /* flag, wait limit (us) */
     if (hipMemset(m->d_tagged, 0, ntag * 8) != hipSuccess || hipMemset(m->d_cls_tw, 0, ncls * 8) != hipSuccess ||
         hipMemset(m->d_epoch, 0, 4) != hipSuccess || hipMemset(m->d_err, 0, 4) != hipSuccess)
         FAIL(LM_ERR_HIP);
     {
-        const int spins = LM_HANDOFF_SPINS;
-        if (hipMemcpy(m->d_err + 1, &spins, 4, hipMemcpyHostToDevice) != hipSuccess) FAIL(LM_ERR_HIP);
+        const int lim_us = LM_HANDOFF_US;
+        if (hipMemcpy(m->d_err + 1, &lim_us, 4, hipMemcpyHostToDevice) != hipSuccess) FAIL(LM_ERR_HIP);
     }
     m->fuse_qa = 3;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
@@ -590,10 +602,57 @@ LMModel *lm_load_blzt(const char *path, int max_batch, int max_seq, int *status)
     return m;
 }
 
+/* Launches that hold hand-off waits (the batch 1-4 decode chain at fusion
+ * levels 1-4) rely on in-order dispatch of their own work-groups on each XCD:
+ * a launch's lowest unfinished work-group always finds its producers done or
+ * running.  Two such launches of different handles in flight at once could
+ * each hold the slots the other's lowest pending work-group needs.  So their
+ * launches are ordered on the device: under g_hand_mu, a handle's stream first
+ * waits for the last hand-off launches any other handle enqueued (g_hand_last),
+ * then enqueues its own and records ev_hand, which becomes g_hand_last.  The
+ * rest of the work of distinct handles (prefill, batched decode, copies) still
+ * runs concurrently. */
+static pthread_mutex_t g_hand_mu = PTHREAD_MUTEX_INITIALIZER;
+static LMModel *g_hand_owner;   /* handle whose ev_hand g_hand_last is */
+
+static int handoff_enter(LMModel *m)
+{
+    pthread_mutex_lock(&g_hand_mu);
+    if (g_hand_owner && g_hand_owner != m &&
+        hipStreamWaitEvent(m->stream, g_hand_owner->ev_hand, 0) != hipSuccess) {
+        pthread_mutex_unlock(&g_hand_mu);
+        fprintf(stderr, "stories_lm: hipStreamWaitEvent on another handle's decode failed\n");
+        return LM_ERR_HIP;
+    }
+    return LM_OK;
+}
+
+/* rc: the status of what was enqueued since handoff_enter (passed through) */
+static int handoff_leave(LMModel *m, int rc)
+{
+    if (hipEventRecord(m->ev_hand, m->stream) == hipSuccess) {
+        g_hand_owner = m;
+    } else {
+        g_hand_owner = NULL;   /* nothing later waits on an unrecorded event */
+        if (rc == LM_OK) rc = LM_ERR_HIP;
+    }
+    pthread_mutex_unlock(&g_hand_mu);
+    return rc;
+}
+
+/* A handle being freed (its stream already synchronised) leaves the chain. */
+static void handoff_forget(LMModel *m)
+{
+    pthread_mutex_lock(&g_hand_mu);
+    if (g_hand_owner == m) g_hand_owner = NULL;
+    pthread_mutex_unlock(&g_hand_mu);
+}
+
 void lm_free(LMModel *m)
 {
     if (!m) return;
     if (m->stream) hipStreamSynchronize(m->stream);
+    handoff_forget(m);
     drop_graphs(m);
     free(m->step_graph);
     free_rows(m);
@@ -607,6 +666,7 @@ void lm_free(LMModel *m)
     if (m->h_io) hipHostFree(m->h_io);
     if (m->ev0) hipEventDestroy(m->ev0);
     if (m->ev1) hipEventDestroy(m->ev1);
+    if (m->ev_hand) hipEventDestroy(m->ev_hand);
     if (m->stream) hipStreamDestroy(m->stream);
     free(m);
 }
@@ -632,10 +692,18 @@ int lm_set_option(LMModel *m, int option, int value)
         drop_graphs(m);
         m->fuse_qa = value;
         return LM_OK;
-    case LM_OPT_HANDOFF_SPINS:
+    case LM_OPT_HANDOFF_US:
         if (value < 1) return LM_ERR_INVALID;
         HIPCHK(hipStreamSynchronize(m->stream));
         HIPCHK(hipMemcpy(m->d_err + 1, &value, 4, hipMemcpyHostToDevice));
+        return LM_OK;
+    case LM_OPT_HANDOFF_ABORT:
+        /* raise the give-up flag from the host: every hand-off wait of the
+         * next call ends at once (the kernels still run to their end) and
+         * the call reports LM_ERR_HIP, then clears the flag */
+        if (value != 1) return LM_ERR_INVALID;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(hipMemcpy(m->d_err, &value, 4, hipMemcpyHostToDevice));
         return LM_OK;
     case LM_OPT_KV_F32:
         if ((value ? 1 : 0) == m->kv_f32) return LM_OK;
@@ -927,13 +995,8 @@ static int enqueue_decode(LMModel *m, int B, float *logits)
 /* Run `nsteps` (1 or GRAPH_STEPS) decode steps of rows 0..B-1, replaying the
  * captured graph of that shape (captured on first use).  Single steps write
  * the logits to d_logits; multi-step runs only feed the argmax forward. */
-static int run_decode_steps(LMModel *m, int B, int nsteps)
+static int enqueue_decode_steps(LMModel *m, int B, int nsteps)
 {
-    if (B > MAX_GEMM_B) {
-        fprintf(stderr, "stories_lm: decode batch %d > %d not supported\n", B, MAX_GEMM_B);
-        return LM_ERR_UNSUPPORTED;
-    }
-    if (nsteps != 1 && nsteps != GRAPH_STEPS) return LM_ERR_INVALID;
     if (!m->use_graph) {
         for (int t = 0; t < nsteps; t++) {
             int rc = enqueue_decode(m, B, nsteps == 1 ? m->d_logits : NULL);
@@ -957,6 +1020,26 @@ static int run_decode_steps(LMModel *m, int B, int nsteps)
     }
     HIPCHK(hipGraphLaunch(*ge, m->stream));
     return LM_OK;
+}
+
+/* Whether the decode step of B rows holds hand-off waits (the batch 1-4
+ * chain with QKV and attention in one launch, levels 1-4). */
+static int step_waits(const LMModel *m, int B)
+{
+    return B <= MAX_GEMV_B && chain_level(m, B) >= 1;
+}
+
+static int run_decode_steps(LMModel *m, int B, int nsteps)
+{
+    if (B > MAX_GEMM_B) {
+        fprintf(stderr, "stories_lm: decode batch %d > %d not supported\n", B, MAX_GEMM_B);
+        return LM_ERR_UNSUPPORTED;
+    }
+    if (nsteps != 1 && nsteps != GRAPH_STEPS) return LM_ERR_INVALID;
+    if (!step_waits(m, B)) return enqueue_decode_steps(m, B, nsteps);
+    int rc = handoff_enter(m);
+    if (rc) return rc;
+    return handoff_leave(m, enqueue_decode_steps(m, B, nsteps));
 }
 
 static int run_decode_step(LMModel *m, int B) { return run_decode_steps(m, B, 1); }
@@ -1320,14 +1403,19 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     if (rc) return rc;
     for (int b = 0; b < B; b++)
         if (pos[b] + steps + 1 > m->max_seq) return LM_ERR_RANGE;
-    /* kernels of one step: 5 per layer, then the classifier and the argmax */
-    const int nk = 5 * m->L + 2;
-    hipEvent_t *ev = (hipEvent_t *)calloc(2 * (size_t)nk, sizeof(hipEvent_t));
-    int *kfam = (int *)calloc((size_t)nk, sizeof(int));
+    /* kernels of one step: 5 per layer, then the classifier and the argmax.
+     * Steps are queued back to back in runs of GRAPH_STEPS, as the greedy
+     * loop's graphs run them (the argmax feeds each step's token to the next
+     * on the device), with one event pair per kernel; the stream is
+     * synchronised and the events read once per run. */
+    const int nk = 5 * m->L + 2, run = GRAPH_STEPS;
+    const size_t nev = 2 * (size_t)nk * run;
+    hipEvent_t *ev = (hipEvent_t *)calloc(nev, sizeof(hipEvent_t));
+    int *kfam = (int *)calloc((size_t)nk * run, sizeof(int));
     double sum[LM_KERN_COUNT] = {0};
     int cnt[LM_KERN_COUNT] = {0};
     if (!ev || !kfam) rc = LM_ERR_OOM;
-    for (int i = 0; i < 2 * nk && rc == LM_OK; i++)
+    for (size_t i = 0; i < nev && rc == LM_OK; i++)
         if (hipEventCreate(&ev[i]) != hipSuccess) rc = LM_ERR_HIP;
     int *hio = m->h_io;
     if (rc == LM_OK) {
@@ -1337,26 +1425,33 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
             hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
             rc = LM_ERR_HIP;
     }
-    for (int st = 0; st <= steps && rc == LM_OK; st++) {   /* step 0 untimed */
+    const int waits = step_waits(m, B), lvl = chain_level(m, B);
+    for (int st0 = 0; st0 <= steps && rc == LM_OK; st0 += run) {   /* step 0 untimed */
+        const int nst = steps + 1 - st0 < run ? steps + 1 - st0 : run;
         int k = 0;
-        for (int l = 0; l < m->L && rc == LM_OK; l++)
-            for (int f = 0; f < 5 && rc == LM_OK; f++) {
-                if (fam_inside(fams[f], chain_level(m, B))) continue;   /* inside the QKV launch */
-                kfam[k] = fams[f];
+        if (waits && (rc = handoff_enter(m))) break;
+        for (int t = 0; t < nst && rc == LM_OK; t++) {
+            for (int l = 0; l < m->L && rc == LM_OK; l++)
+                for (int f = 0; f < 5 && rc == LM_OK; f++) {
+                    if (fam_inside(fams[f], lvl)) continue;   /* inside the QKV launch */
+                    kfam[k] = st0 + t > 0 ? fams[f] : -1;
+                    lmk_time_next(ev[2 * k], ev[2 * k + 1]);
+                    rc = enqueue_kernel(m, B, fams[f], l, NULL);
+                    k++;
+                }
+            for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
+                if (fam_inside(f, lvl)) continue;   /* inside the classifier launch */
+                kfam[k] = st0 + t > 0 ? f : -1;
                 lmk_time_next(ev[2 * k], ev[2 * k + 1]);
-                rc = enqueue_kernel(m, B, fams[f], l, NULL);
+                rc = enqueue_kernel(m, B, f, 0, NULL);
                 k++;
             }
-        for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
-            if (fam_inside(f, chain_level(m, B))) continue;   /* inside the classifier launch */
-            kfam[k] = f;
-            lmk_time_next(ev[2 * k], ev[2 * k + 1]);
-            rc = enqueue_kernel(m, B, f, 0, NULL);
-            k++;
         }
+        if (waits) rc = handoff_leave(m, rc);
         if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
-        for (int i = 0; i < k && rc == LM_OK && st > 0; i++) {
+        for (int i = 0; i < k && rc == LM_OK; i++) {
             float ms = 0.f;
+            if (kfam[i] < 0) continue;
             if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = LM_ERR_HIP;
             sum[kfam[i]] += ms;
             cnt[kfam[i]]++;
@@ -1365,17 +1460,19 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
         if (launches_per_step)
-            launches_per_step[f] = fam_inside(f, chain_level(m, B))              ? 0
+            launches_per_step[f] = fam_inside(f, lvl)                            ? 0
                                    : f == LM_KERN_CLS || f == LM_KERN_ARGMAX ? 1
                                                                              : m->L;
     }
-    for (int i = 0; ev && i < 2 * nk; i++)
+    for (size_t i = 0; ev && i < nev; i++)
         if (ev[i]) hipEventDestroy(ev[i]);
     free(ev);
     free(kfam);
     if (rc == LM_OK)
         HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
+    if (rc == LM_OK) rc = queue_err_read(m);
     HIPCHK(hipStreamSynchronize(m->stream));
+    if (rc == LM_OK) rc = check_err(m);
     return rc;
 }
 

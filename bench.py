@@ -14,10 +14,11 @@ Alongside the headline the JSON line carries:
   roofline      the dominant kernel of the decode step: algorithmic bytes per
                 launch / mean launch duration, the duration measured after the
                 timed region over the 254 decode steps of one sequence of the same
-                chain, each kernel launched with hipEvents at its own dispatch's
-                start and end (lm_profile_chain; skipped under a profiler, where
-                event-bracketed dispatches are not used); every family's time
-                is in kernel_us_per_launch
+                chain, each kernel launched with events at its own dispatch's
+                device start and end (lm_profile_chain); every family's time is
+                in kernel_us_per_launch.  traffic: the kernel's FETCH_SIZE +
+                WRITE_SIZE per dispatch from the committed C0 profile's counter
+                line, or null when no counter pass of it has completed
   step_roofline the whole token: algorithmic bytes per token / time per token
   configs       C1-C4 (MFMA paths), C0 in the reference's own algorithm (a
                 256-position window forward per token, generate.m:427-516),
@@ -44,6 +45,13 @@ sys.path[:0] = [os.path.join(ROOT, "ane-training_amd"), os.path.join(ROOT, "orac
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+_T0 = time.perf_counter()
+
+
+def progress(msg):
+    """One progress line on stderr per phase (the JSON line alone goes to
+    stdout), flushed, so a run that stops can be placed."""
+    print(f"[bench {time.perf_counter() - _T0:7.1f}s] {msg}", file=sys.stderr, flush=True)
 # Published reference figure for this metric: Stories-110M B=1 greedy decode on
 # the ANE (libane, fp16), M3 Pro: 41.7 tok/s (full 256-window recompute).
 LIB_FUSE_DEFAULT = 3     # LM_OPT_FUSE_QKV_ATTN after lm_load / lm_create
@@ -51,26 +59,25 @@ REF_TOK_S = 41.7
 SEQ = 256
 
 
-# FETCH_SIZE per launch of the C0 chain's kernels with QKV + attention in one launch and
-# the rest apart (bytes, the counter's KiB x 1024 x 2.000)
-C0_FETCH = {"qkv": 4737000, "wo": 1234000, "w13": 6382000, "w2": 3265000}
-TAG_COPIES = 8    # copies of each tagged word set that several work-groups read
+PROFILE_C0 = os.path.join(ROOT, "profiles", "decode_b1_stories110m_chain.md")
 
 
-def qkv_launch_writes(cfg, kvb, folded):
-    """Bytes the fused QKV launch writes for one row: the q, k, v hand-off words
-    (8 bytes each) and the K/V append; then the fp32 head outputs, or (Wo
-    inside) the head-output words in every copy and either x (3 KB) or (the
-    FFN inside too) the words of x and of the gate in every copy, then x."""
-    hd = cfg.dim // cfg.n_heads
-    nq, nkv, D, F = cfg.dim, cfg.n_kv_heads * hd, cfg.dim, cfg.hidden_dim
-    w = 8 * (nq + 2 * nkv) + 2 * nkv * kvb
-    if "wo" not in folded:
-        return w + 4 * nq
-    w += 8 * TAG_COPIES * nq + 4 * D
-    if "w2" in folded:
-        w += 8 * TAG_COPIES * (D + F)
-    return w
+def profiled_traffic(kernel_prefix):
+    """HBM bytes per launch of the kernel named by kernel_prefix, from the
+    counter line of the committed C0 profile: FETCH_SIZE and WRITE_SIZE per
+    dispatch of that kernel in two rocprofv3 --pmc runs, each scaled by what
+    the same counter reads for a device copy of known size in the same run.
+    The line reads `counters <kernel> fetch_bytes=F write_bytes=W`; None when
+    the profile holds no such line (no completed counter pass)."""
+    import re
+    try:
+        text = open(PROFILE_C0).read()
+    except OSError:
+        return None
+    for mt in re.finditer(r"^counters (\S+) fetch_bytes=(\d+) write_bytes=(\d+)", text, re.M):
+        if mt.group(1).startswith(kernel_prefix):
+            return {"fetch": int(mt.group(2)), "write": int(mt.group(3)), "kernel": mt.group(1)}
+    return None
 
 
 def algorithmic_bytes(cfg, B, mean_ctx, kv_bytes=2, logits=False):
@@ -92,22 +99,40 @@ def algorithmic_bytes(cfg, B, mean_ctx, kv_bytes=2, logits=False):
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name, vendor, family,
+    model and stepping numbers (which identify the part when the name is
+    generic, as in some virtual machines), and the online core count."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "vendor_id", "cpu family", "model", "stepping") and k not in info:
+                info[k] = v.strip()
     except OSError:
         pass
-    return "unknown"
+    name = info.get("model name", "unknown")
+    ids = ", ".join(f"{k} {info[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in info)
+    return f"{name} ({ids}; {os.cpu_count()} online cores)" if ids else name
 
 
 def cpu_threads():
-    """Threads for the CPU baseline: OMP_NUM_THREADS when set (the GPU box sets
-    its CPU share there), else every online core."""
-    try:
-        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
-    except ValueError:
-        return os.cpu_count() or 1
+    """Threads for the CPU baseline: the count `nproc` prints, the processing
+    units this process may use.  As GNU nproc does, that is the affinity
+    mask's CPUs, replaced by OMP_NUM_THREADS when it is set and capped by
+    OMP_THREAD_LIMIT.  The GPU box sets OMP_NUM_THREADS to its CPU share for
+    one GPU (16 of the host's cores; the others serve its other GPUs)."""
+    def env_int(k):
+        try:
+            return int(os.environ.get(k, "").split(",")[0])
+        except ValueError:
+            return 0
+    n = len(os.sched_getaffinity(0))
+    if env_int("OMP_NUM_THREADS") > 0:
+        n = env_int("OMP_NUM_THREADS")
+    if env_int("OMP_THREAD_LIMIT") > 0:
+        n = min(n, env_int("OMP_THREAD_LIMIT"))
+    return max(1, n)
 
 
 def cpu_baseline(cfg7, w16, S, gpu_ids, seconds):
@@ -138,7 +163,7 @@ def cpu_baseline(cfg7, w16, S, gpu_ids, seconds):
             break
     dt = time.perf_counter() - t0
     out = {"value": round(passes * ntok / dt, 2), "unit": "tok/s", "cores": n, "kind": "port",
-           "cpu_model": cpu_model(), "blas": R.blas_name(),
+           "cpu_model": cpu_model(), "nproc_all": os.cpu_count(), "blas": R.blas_name(),
            "ids_match_gpu": bool(np.array_equal(ids, gpu_ids[:ntok])),
            "sample": f"C0 KV-cache greedy decode of the first {ntok} tokens from id 1, {passes} passes, "
                      f"{dt:.1f} s, {n} threads (oracle/cpu_ref.c: the reference forward with OpenBLAS)"}
@@ -146,7 +171,7 @@ def cpu_baseline(cfg7, w16, S, gpu_ids, seconds):
     win = np.concatenate([[1], gpu_ids[:SEQ - 1]]).astype(np.int32)
     t0 = time.perf_counter()
     k = 0
-    while k < 2 or (time.perf_counter() - t0 < seconds * 0.25 and k < 16):
+    while k < 2 or (time.perf_counter() - t0 < seconds * 0.25 and k < 64):
         r.forward(win, last_only=True)
         k += 1
     dt = time.perf_counter() - t0
@@ -161,11 +186,11 @@ def cpu_baseline(cfg7, w16, S, gpu_ids, seconds):
                               "sample": "one 256-token prompt, all 256 x 32000 logits"}
     toks = np.random.default_rng(103).integers(0, 32000, (8, SEQ)).astype(np.int32)
     t0 = time.perf_counter()
-    for i in range(2):
+    for i in range(8):
         r.forward(toks[i])
     dt = time.perf_counter() - t0
-    cfgs["c3_forward_8x256"] = {"value": round(2 * SEQ / dt, 1), "unit": "tok/s",
-                                "sample": f"2 of the 8 prompts of 256 tokens, all logits, {dt:.1f} s"}
+    cfgs["c3_forward_8x256"] = {"value": round(8 * SEQ / dt, 1), "unit": "tok/s",
+                                "sample": f"the 8 prompts of 256 tokens one after another, all logits, {dt:.1f} s"}
     r.close()
     out["configs"] = cfgs
     return out
@@ -305,7 +330,7 @@ def attn_flops_prefill(cfg, S, nseq):
     return nseq * cfg.n_layers * cfg.n_heads * 2 * 2 * hd * S * (S + 1) / 2
 
 
-def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, only=None):
+def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, only=None, c4_steps=128):
     """Configs C1-C4 of the baseline (MFMA paths), as extra entries.  direct:
     launch decode kernels directly instead of replaying graphs; only: run just
     these configs ("c1" .. "c4")."""
@@ -318,6 +343,7 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
     V = 32000
     # C1: 256-token causal prefill, all 256 x 32000 fp32 logits (kept on the device)
     if want("c1"):
+        progress("C1: 256-token prefill, all logits")
         m = S.Model.create(cfg, w16_stories, True, 1, 256)
         toks = np.random.default_rng(101).integers(0, V, 256).astype(np.int32)
         ms = _timed(m, lambda: m.prefill(toks, want_logits=False), reps_prefill)
@@ -330,6 +356,7 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
         m.close()
     # C3: 8 x 256 = 2048-token causal forward with all logits (MFMA bound)
     if want("c3"):
+        progress("C3: 8 x 256-token forward")
         m = S.Model.create(cfg, w16_stories, True, 8, 256)
         toks = np.random.default_rng(103).integers(0, V, (8, 256)).astype(np.int32)
         ms = _timed(m, lambda: m.prefill_batch(toks, mode=S.LM_LOGITS_ALL, want_logits=False), reps_prefill)
@@ -340,6 +367,7 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
         m.close()
     # C2: 64 sequences, 192-token prompts prefilled, then 64 greedy steps each
     if want("c2"):
+        progress("C2: 64 x 192-token prefill, then 64 greedy steps")
         m = S.Model.create(cfg, w16_stories, True, 64, 256)
         if direct:
             m.set_option(S.LM_OPT_USE_GRAPH, 0)
@@ -364,21 +392,25 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
         d4 = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
                   seq_len=640)
         cfg4 = S.make_config(**d4)
+        progress("C4: synthesising the scaled model's weights")
         w4 = S.synth_weights_f16(cfg4, 4, 0.02, True)
+        progress("C4: creating the model (weights to the device)")
         m = S.Model.create(cfg4, w4, True, 32, 640)
         if direct:
             m.set_option(S.LM_OPT_USE_GRAPH, 0)
         del w4
         prompts = np.random.default_rng(104).integers(0, V, (32, 512)).astype(np.int32)
+        progress("C4: 32 x 512-token prefill")
         lg = m.prefill_batch(prompts, mode=S.LM_LOGITS_LAST)
         first = np.argmax(lg, axis=1).astype(np.int32)
         pos = np.full(32, 512, np.int32)
-        ms = _timed(m, lambda: m.generate_greedy(first, pos, 128), 1)
+        progress(f"C4: {c4_steps} greedy steps, untimed then timed")
+        ms = _timed(m, lambda: m.generate_greedy(first, pos, c4_steps), 1)
         wb4, _ = model_bytes(cfg4)
-        kv4 = 32 * 16 * 2 * 2048 * 2 * (512 + 128 / 2 + 0.5)
-        t4 = ms * 1e-3 / 128
-        out["c4_scaled_decode_b32"] = {"value": round(32 * 128 / (ms * 1e-3), 1), "unit": "tok/s",
-                                       "ms_per_step": round(ms / 128, 4),
+        kv4 = 32 * 16 * 2 * 2048 * 2 * (512 + c4_steps / 2 + 0.5)
+        t4 = ms * 1e-3 / c4_steps
+        out["c4_scaled_decode_b32"] = {"value": round(32 * c4_steps / (ms * 1e-3), 1), "unit": "tok/s",
+                                       "ms_per_step": round(ms / c4_steps, 4), "steps": c4_steps,
                                        "hbm_frac": round((wb4 + kv4) / t4 / 1e9 / HBM_PEAK_GBS, 4),
                                        "algorithmic_bytes_per_step": int(wb4 + kv4)}
         m.close()
@@ -448,14 +480,6 @@ def device_copy_rate(mib=1024, reps=5):
             "sample": f"{reps} device-to-device copies of {mib} MiB (hipMemcpy), bytes read + written"}
 
 
-def under_profiler():
-    """True inside rocprofv3 (its preloaded tool library and ROCPROF* variables):
-    event-bracketed dispatches (lm_profile_chain) are then not used."""
-    env = os.environ
-    return any(k.startswith(("ROCPROF", "ROCPROFILER")) for k in env) or \
-        "rocprofiler" in env.get("LD_PRELOAD", "")
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -470,9 +494,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip configs C1-C4")
     ap.add_argument("--no-chain-timing", action="store_true",
-                    help="skip the per-kernel event timing (automatic under a profiler)")
+                    help="skip the per-dispatch timing of the decode chain (lm_profile_chain)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first copy this many MiB device to device (counter calibration)")
+    ap.add_argument("--c4-steps", type=int, default=128,
+                    help="greedy steps of the C4 leg (fewer for counter passes)")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"],
                     help="run just this config of C1-C4 (for profiling) and print its entry")
     args = ap.parse_args()
@@ -484,16 +510,24 @@ def main():
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         sys.exit(2)
     import stories_lm as S
+    progress("lm_init")
     rc = S.init()
     if rc:
         raise SystemExit(f"lm_init: {S.strerror(rc)}")
     if args.calib_copy_mb:
+        progress(f"calibration copy of {args.calib_copy_mb} MiB")
         calibration_copy(args.calib_copy_mb)
     cfg = S.make_config(**S.STORIES_110M)
-    w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
+    w16 = None
+    if args.only != "c4":
+        progress("synthesising the Stories-110M weights")
+        w16 = S.synth_weights_f16(cfg, 1, 0.02, True)
     if args.only:
-        print(json.dumps(bench_extra(S, w16, direct=args.direct, only={args.only})), flush=True)
+        print(json.dumps(bench_extra(S, w16, direct=args.direct, only={args.only},
+                                     c4_steps=args.c4_steps)), flush=True)
+        progress("done")
         return
+    progress("creating the C0 model")
     m = S.Model.create(cfg, w16, True, 1, SEQ)
     if not args.kv16:
         m.set_option(S.LM_OPT_KV_F32, 1)
@@ -502,9 +536,11 @@ def main():
     if args.fuse is not None:
         m.set_option(S.LM_OPT_FUSE_QKV_ATTN, args.fuse)
 
+    progress(f"C0: {args.warmup} warm-up sequence(s)")
     for _ in range(args.warmup):
         m.generate_greedy([1], [0], SEQ)
     m.sync()
+    progress(f"C0: {args.steps} timed sequence(s) of {SEQ} tokens")
     m.timer_begin()
     t0 = time.perf_counter()
     ids = None
@@ -519,9 +555,11 @@ def main():
     mean_ctx = (SEQ + 1) / 2
     kvb = 2 if args.kv16 else 4
     algo = algorithmic_bytes(cfg, 1, mean_ctx, kvb)
-    chain_timing = not (args.no_chain_timing or under_profiler())
+    chain_timing = not args.no_chain_timing
+    fuse_level = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
     launches = None
     if chain_timing:
+        progress("per-dispatch timing of the decode chain (lm_profile_chain, 254 steps)")
         # device time per launch of each kernel family inside the decode chain over
         # the positions of a timed sequence (254 steps from position 0): every
         # kernel timed by hipEvents at its own dispatch's start and end
@@ -529,7 +567,7 @@ def main():
     m.close()
     if launches is None:   # the chain's launch counts: one per layer, attention (Wo from
         # level 2, the FFN at 3) inside the QKV launch, classifier and argmax once
-        fz = LIB_FUSE_DEFAULT if args.fuse is None else args.fuse
+        fz = fuse_level
         inside = {"attn": fz >= 1, "wo": fz >= 2, "w13": fz >= 3, "w2": fz >= 3, "argmax": fz >= 3}
         launches = {k: (0 if inside.get(k) else 1 if k in ("cls", "argmax") else cfg.n_layers)
                     for k in algo}
@@ -568,31 +606,44 @@ def main():
         dom = "qkv" if "attn" not in algo else "attn"
         dur_us = us[dom]
         achieved = algo[dom] / (dur_us * 1e-6) / 1e9
-        traffic = None
-        if dom == "qkv" and not args.kv16 and "attn" in folded:
-            # fp32 cache: FETCH_SIZE (x 2.000, the 256 MiB copy calibration) of each part
-            # launched on its own, QKV + attention fused (profiles/decode_b1_stories110m_chain.md),
-            # summed over the parts this launch holds, + its writes, taken as algorithmic
-            traffic = sum(C0_FETCH[k] for k in ["qkv"] + folded if k != "attn") + \
-                qkv_launch_writes(cfg, kvb, folded)
+        traffic, tsrc = None, "no completed counter pass of this kernel in " + os.path.relpath(PROFILE_C0, ROOT)
+        fused = dom == "qkv" and fuse_level == 3 and not args.kv16
+        if fused:
+            c = profiled_traffic("k_qkv_attn<768, 1, float, 64, true, 2048>")
+            if c:
+                traffic = c["fetch"] + c["write"]
+                tsrc = (f"FETCH_SIZE + WRITE_SIZE of {c['kernel']} per dispatch, rocprofv3 --pmc "
+                        f"(one counter per run, each scaled by the same counter over a known device copy), "
+                        f"{os.path.relpath(PROFILE_C0, ROOT)}")
         out["roofline"] = {"bound": "hbm", "kernel": "k_qkv_attn" if dom == "qkv" else dom,
                            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                           "traffic_source": tsrc,
                            "bytes_per_launch": int(algo[dom]), "launch_us": round(dur_us, 3),
-                           "launch_us_source": "hipEvents at each dispatch of the chain (lm_profile_chain)"}
+                           "launch_us_source": "device start/end timestamps of every dispatch of the "
+                                               "kernel over the 254 decode steps of one sequence, direct "
+                                               "launches (lm_profile_chain: hipExtLaunchKernelGGL events); "
+                                               "the kernel trace of the same dispatches is in "
+                                               + os.path.relpath(PROFILE_C0, ROOT)}
         out["kernel_us_per_launch"] = {k: round(v, 3) for k, v in us.items() if launches.get(k)}
     if not args.no_extra:
         out["configs"] = bench_extra(S, w16, direct=args.direct)
+        progress("C0 in the reference's algorithm (window recompute) on the GPU")
         ra = reference_algorithm_gpu(S, cfg, w16, ids)
         out["configs"]["c0_reference_algorithm"] = ra
         if not args.kv16:
+            progress("C0 with the binary16 K/V cache")
             out["configs"]["c0_kv16"] = c0_kv16(S, cfg, w16, ids, args.direct)
+            progress("C0 warm and cold (Infinity Cache sweep) tokens")
             out["configs"]["c0_cold_cache"] = c0_cold_cache(S, cfg, w16, ids)
+        progress("device copy rate")
         out["device_copy_rate"] = device_copy_rate()
         out["vs_baseline_same_algorithm"] = round(ra["value"] / REF_TOK_S, 1)
     if not args.no_cpu:
+        progress("CPU baseline (oracle/cpu_ref.c with OpenBLAS)")
         out["cpu_baseline"] = cpu_baseline(cfg.astuple(), w16, S, ids, args.cpu_seconds)
     print(json.dumps(out), flush=True)
+    progress("done")
 
 
 if __name__ == "__main__":

@@ -252,10 +252,15 @@ int lm_timer_end(LMModel *m, float *ms);
  * runs.  2 runs QKV, attention and Wo as one launch and the FFN as two; 1
  * also launches Wo apart; 0 launches all five apart. */
 #define LM_OPT_FUSE_QKV_ATTN 5
-/* LM_OPT_HANDOFF_SPINS: polls after which a wait for a tagged hand-off word
- * inside a fused launch gives up (default 1 << 20, about a second); the call
- * then returns LM_ERR_HIP.  For tests of that path; >= 1. */
-#define LM_OPT_HANDOFF_SPINS 6
+/* LM_OPT_HANDOFF_US: microseconds (the device's real-time counter) after
+ * which a wait for a tagged hand-off word inside a fused launch gives up
+ * (default 100000); every other wait of the call then ends at once, the
+ * kernels run to their end and the call returns LM_ERR_HIP.  >= 1. */
+#define LM_OPT_HANDOFF_US  6
+/* LM_OPT_HANDOFF_ABORT: value 1 raises the give-up flag from the host, so
+ * that every hand-off wait of the next decode call ends at once and that call
+ * returns LM_ERR_HIP (the flag is then cleared).  For tests of that path. */
+#define LM_OPT_HANDOFF_ABORT 7
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------
@@ -357,10 +362,10 @@ int lm_gemm_split_count(int M, int N, int K);
 
 /* Mean device microseconds per launch of each decode kernel family inside the
  * real decode chain: `steps` greedy decode steps of B rows from tokens[b] at
- * positions pos[b] (advancing as a decode does), launched directly, every
- * kernel timed by events at its own dispatch's start and end (the kernel plus
- * a dispatch overhead a kernel trace leaves out; no kernel measures under
- * about 3.9 us).  One untimed step runs first.  launches_per_step[k] (may
+ * positions pos[b] (advancing as a decode does), launched directly and queued
+ * back to back in runs of 16 steps as the greedy loop's graphs run them,
+ * every kernel timed by events at its own dispatch's device start and end.
+ * One untimed step runs first.  launches_per_step[k] (may
  * be NULL) = launches of family k in one decode step.  Needs pos[b] + steps +
  * 1 <= max_seq; leaves the KV cache at those positions and the activations
  * overwritten. */

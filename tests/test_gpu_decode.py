@@ -206,25 +206,35 @@ def test_graph_replay_equals_direct_launches(lm):
     m2.close()
 
 
-def test_handoff_timeout_reports_error(lm):
-    """A hand-off wait that gives up, forced from the host with a limit of one
-    poll, ends its launch normally and turns into LM_ERR_HIP; with the limit
-    restored, the next calls give the fixture's logits again."""
-    _say("[hand-off timeout]")
+def test_handoff_abort_reports_error(lm):
+    """A hand-off wait that gives up, forced from the host by raising the
+    give-up flag before the call (every wait of the call then ends at once, so
+    the outcome does not depend on timing): the launches end normally and the
+    call returns LM_ERR_HIP (lm_forward: NULL); the flag is then cleared and
+    the next calls give the fixture's logits again.  The real-time limit
+    itself only takes values of at least one microsecond."""
+    _say("[hand-off abort]")
     d = TINY
     fx = np.load(os.path.join(GOLDEN, "tiny_mha.npz"))
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], True)
-    assert m.forward(int(fx["tokens"][0]), 0) is not None      # the limit still at its default
-    m.set_option(lm.LM_OPT_HANDOFF_SPINS, 1)
+    assert m.forward(int(fx["tokens"][0]), 0) is not None
+    m.set_option(lm.LM_OPT_HANDOFF_ABORT, 1)
     with pytest.raises(lm.LMError) as ei:      # lm_forward_batch returns the status itself
-        for p, t in enumerate(fx["tokens"][:32]):
-            m.forward_batch(np.array([t], np.int32), np.array([p], np.int32))
+        m.forward_batch(np.array([fx["tokens"][1]], np.int32), np.array([1], np.int32))
     assert ei.value.status == lm.LM_ERR_HIP
+    m.set_option(lm.LM_OPT_HANDOFF_ABORT, 1)
     with pytest.raises(lm.LMError):            # lm_forward: NULL for the same failure
         m.forward(int(fx["tokens"][0]), 0)
+    m.set_option(lm.LM_OPT_HANDOFF_ABORT, 1)
+    with pytest.raises(lm.LMError) as ei:      # the greedy loop too
+        m.generate_greedy([int(fx["tokens"][0])], [0], 4)
+    assert ei.value.status == lm.LM_ERR_HIP
+    for bad in (0, -1):
+        with pytest.raises(lm.LMError):
+            m.set_option(lm.LM_OPT_HANDOFF_US, bad)
     with pytest.raises(lm.LMError):
-        m.set_option(lm.LM_OPT_HANDOFF_SPINS, 0)
-    m.set_option(lm.LM_OPT_HANDOFF_SPINS, 1 << 20)
+        m.set_option(lm.LM_OPT_HANDOFF_ABORT, 0)
+    m.set_option(lm.LM_OPT_HANDOFF_US, 100000)
     got = np.stack([m.forward(int(t), p) for p, t in enumerate(fx["tokens"])])
     np.testing.assert_allclose(got, fx["logits_kv32"], **TIGHT)
     m.close()
