@@ -32,11 +32,13 @@
 #include "lm_internal.h"
 #include <hip/hip_ext.h>
 
+#include <atomic>
+
 /* Launch-timing slot for lm_profile_chain: when armed, the next decode-chain
  * kernel launch of this host thread goes through hipExtLaunchKernelGGL with the
- * two events, which the device timestamps at that dispatch's start and end.
- * That span includes dispatch overhead a kernel trace leaves out: no kernel of
- * the chain measures under about 3.9 us this way. */
+ * two events (either may be NULL), which the device timestamps at that
+ * dispatch's start and end; a start armed on one launch and a stop on a later
+ * one time the run of launches between them with no event in between. */
 static thread_local hipEvent_t t_ev0, t_ev1;
 static thread_local int t_armed;
 
@@ -102,12 +104,17 @@ __device__ __forceinline__ void norm_load(const float *__restrict__ x, const u16
     }
 }
 
-/* xs[b*K + i] = src_b[i] * (1/sqrt(mean(src_b^2) + 1e-5)) * w[i]
- * (forward.h:46-53).  With store_x, work-group 0 also writes the raw rows to x
- * (the residual stream starts as the embedding). */
+/* The normalising prologue with the row scale left to the caller:
+ * xs[b*K + i] = src_b[i] * w[i] and scale[b] = 1/sqrt(mean(src_b^2) + 1e-5)
+ * (forward.h:46-53).  The norm is one factor per row, so it distributes over
+ * the caller's dot products, which it multiplies in after their sums: one
+ * barrier instead of two (one before the scale is known, one after the
+ * normalised rows are written), and the scale's reduction overlaps the LDS
+ * writes.  With store_x, work-group 0 also writes the raw rows to x. */
 template <int K, int NB>
-__device__ __forceinline__ void norm_to_lds(const NormIn<K, NB> &in, int B, float *__restrict__ x,
-                                            bool store_x, float *xs)
+__device__ __forceinline__ void norm_to_lds_unscaled(const NormIn<K, NB> &in, int B,
+                                                     float *__restrict__ x, bool store_x,
+                                                     float *xs, float scale[NB])
 {
     constexpr int PER = K / WG;
     __shared__ float red[NB][NWAVE];
@@ -116,7 +123,10 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<K, NB> &in, int B, floa
     for (int b = 0; b < NB; b++) {
         float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < PER; j++) ss = fmaf(in.v[b][j], in.v[b][j], ss);
+        for (int j = 0; j < PER; j++) {
+            ss = fmaf(in.v[b][j], in.v[b][j], ss);
+            xs[b * K + tid + j * WG] = in.v[b][j] * in.w[j];
+        }
         ss = wave_sum(ss);
         if (lane == 0) red[b][wv] = ss;
     }
@@ -134,11 +144,8 @@ __device__ __forceinline__ void norm_to_lds(const NormIn<K, NB> &in, int B, floa
         float tot = 0.f;
 #pragma unroll
         for (int i = 0; i < NWAVE; i++) tot += red[b][i];
-        const float scale = 1.0f / sqrtf(tot / K + 1e-5f);
-#pragma unroll
-        for (int j = 0; j < PER; j++) xs[b * K + tid + j * WG] = in.v[b][j] * scale * in.w[j];
+        scale[b] = 1.0f / sqrtf(tot / K + 1e-5f);
     }
-    __syncthreads();
 }
 
 /* NB rows of K fp32 from src (rows >= B zero), loaded into registers. */
@@ -356,12 +363,18 @@ __device__ __forceinline__ void qkv_rows(
         cr[b] = rot ? rc[ti] : 1.f;
         sr[b] = rot ? rs[ti] : 0.f;
     }
-    norm_to_lds<D, NB>(in, B, x, emb != nullptr && store_x, xs);
+    float scale[NB];
+    norm_to_lds_unscaled<D, NB>(in, B, x, emb != nullptr && store_x, xs, scale);
     if (p >= npairs) return;
     float acc[NB], r0[NB], r1[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, r0, r1);
     if (lane != 0) return;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        r0[b] *= scale[b];
+        r1[b] *= scale[b];
+    }
     /* hd is a power of two (64 or 128) */
     const int lg = __builtin_ctz((unsigned)hd);
     const int Hkv = NKV >> lg;
@@ -870,7 +883,8 @@ __device__ __forceinline__ void wo_role(float *__restrict__ x, const u16 *__rest
 
 /* W1/W3 role of k_qkv_attn (the FFN in the launch), work-group a of the role,
  * one hidden unit i per wave as in k_ffn13: x' from copy a % LM_TX_COPIES of
- * its tagged words, normalised in LDS exactly as norm_to_lds does, then
+ * its tagged words, normalised as norm_to_lds_unscaled does (the row scale
+ * applied to the dot products), then
  * g[b, i] = silu(W1[i] . xn) * (W3[i] . xn) stored to every copy of the tagged
  * words tgt.  (One unit per wave measured faster than two or four: more
  * work-groups load the weights.) */
@@ -897,34 +911,31 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
     const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D;
     tag_doorbell(txc, B * D, a / LM_TX_COPIES, tag, tg.err);
     tag_wait_span(txc, B * D, tag, tg.err, xs);
+    /* the row scale is applied to the dot products (it distributes over
+     * them), so xs takes x' * gain at once: one barrier */
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         float ss = 0.f;
-        if (b < B) {
 #pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const float v = xs[b * D + tid + j * WG];
-                ss = fmaf(v, v, ss);
-            }
+        for (int j = 0; j < PER; j++) {
+            float *e = xs + b * D + tid + j * WG;
+            const float v = b < B ? *e : 0.f;
+            ss = fmaf(v, v, ss);
+            *e = v * w[j];
         }
         ss = wave_sum(ss);
         if (lane == 0) red[b][wv_] = ss;
     }
     __syncthreads();
+    if (i0 >= F) return;
+    float scale[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         float tot = 0.f;
 #pragma unroll
         for (int k = 0; k < NWAVE; k++) tot += red[b][k];
-        const float scale = 1.0f / sqrtf(tot / D + 1e-5f);
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            float *e = xs + b * D + tid + j * WG;
-            *e = b < B ? *e * scale * w[j] : 0.f;
-        }
+        scale[b] = 1.0f / sqrtf(tot / D + 1e-5f);
     }
-    __syncthreads();
-    if (i0 >= F) return;
     float acc[NB], h1[NB], h3[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, h1, h3);
@@ -933,6 +944,8 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
+            h1[b] *= scale[b];
+            h3[b] *= scale[b];
             const float silu = h1[b] / (1.0f + expf(-h1[b]));  /* forward.h:101 */
             tag_store(dst + (size_t)b * F, silu * h3[b], tag);  /* forward.h:151 */
         }
@@ -1114,7 +1127,8 @@ __global__ void __launch_bounds__(WG) k_ffn13(
     hw_load<D>(W13 + row * D, hl, wv);
     NormIn<D, NB> in;
     norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
-    norm_to_lds<D, NB>(in, B, x, false, xs);
+    float scale[NB];
+    norm_to_lds_unscaled<D, NB>(in, B, x, false, xs, scale);
     if (i0 >= F) return;
     float acc[NB], h1[NB], h3[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
@@ -1123,6 +1137,8 @@ __global__ void __launch_bounds__(WG) k_ffn13(
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (b >= B) break;
+            h1[b] *= scale[b];
+            h3[b] *= scale[b];
             const float silu = h1[b] / (1.0f + expf(-h1[b]));  /* forward.h:101 */
             g[(size_t)b * F + i] = silu * h3[b];                /* forward.h:151 */
         }
@@ -1261,7 +1277,8 @@ __global__ void __launch_bounds__(WG) k_cls(
     }
     NormIn<D, NB> in;
     norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
-    norm_to_lds<D, NB>(in, B, nullptr, false, xs);
+    float scale[NB];
+    norm_to_lds_unscaled<D, NB>(in, B, nullptr, false, xs, scale);
     float bv[NB];
     int bi[NB];
 #pragma unroll
@@ -1272,6 +1289,11 @@ __global__ void __launch_bounds__(WG) k_cls(
         float acc[NB], r0[NB], r1[NB];
         hw_dot<D, NB>(wr[pp], xs, hl, acc);
         pair_reduce<NB>(acc, r0, r1);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            r0[b] *= scale[b];
+            r1[b] *= scale[b];
+        }
         if (r < V) {
             const bool has1 = r + 1 < V;
 #pragma unroll
@@ -1444,13 +1466,41 @@ extern "C" int lmk_layer_fusable(int D, int F, int B)
     return 0;
 }
 
+/* Dynamic LDS for a launch of kernel KERN that leaves room for at most `cap`
+ * of its work-groups on one CU (160 KiB of LDS per CU on gfx950): enough that
+ * cap + 1 no longer fit, never so much that cap do not, and never past one
+ * CU's LDS.  0 when cap < 1, when the static LDS already does it, or when the
+ * attributes cannot be read.  Memoised per kernel instantiation (KERN is a
+ * template argument, so each instantiation has its own memo) and cap. */
+template <auto KERN>
+static size_t lds_cap_pad(int cap)
+{
+    constexpr size_t PER_CU = 160 * 1024, GRAIN = 512;
+    static std::atomic<long> memo[5] = {{-1}, {-1}, {-1}, {-1}, {-1}};
+    if (cap < 1 || cap > 4) return 0;
+    long v = memo[cap].load(std::memory_order_relaxed);
+    if (v >= 0) return (size_t)v;
+    hipFuncAttributes a;
+    size_t pad = 0;
+    if (hipFuncGetAttributes(&a, (const void *)KERN) == hipSuccess) {
+        const size_t stat = a.sharedSizeBytes, need = PER_CU / (cap + 1) + 1;
+        if (stat < need) {
+            pad = (need - stat + GRAIN - 1) / GRAIN * GRAIN;
+            if (stat + pad > PER_CU / cap || stat + pad > PER_CU) pad = 0;
+        }
+    }
+    memo[cap].store((long)pad, std::memory_order_relaxed);
+    return pad;
+}
+
 extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                             const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                             const float *rope_cos, const float *rope_sin, const int *pos, int B,
                             void *kc, void *vc, int kv_f32, int max_seq, int H,
                             unsigned long long *tagged, const unsigned *epoch, int layer,
                             int n_layers, int *err, float *out, const uint16_t *wo,
-                            const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F)
+                            const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F,
+                            int wgs_per_cu)
 {
     if (B < 1 || B > 4 || NQ != D || H < 1 || NQ != H * hd || NKV % hd || H % (NKV / hd) ||
         (emb && !tok) || !tagged || !epoch || !err || (!out && !wo) || (hd != 64 && hd != 128) ||
@@ -1466,10 +1516,13 @@ extern "C" int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const 
     const QkvTagged tg = {tagged, tagged + (size_t)LM_TAG_B * NQ, tagged + (size_t)LM_TAG_B * (NQ + NKV),
                           ta, tx, tgt, epoch, layer, n_layers, err};
     const FfnArgs ffn = {rms_ffn, (const u16 *)w13, (const u16 *)w2};
-#define LAUNCH_QA(HD_, KT_, WO_, F_)                                                                \
-    DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_, F_>), grid, dim3(WG), 0, s, x, emb, tok, rms_w, wqkv, \
-            NQ, NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs, nprod, H,     \
-            tg, out, (const u16 *)wo, ffn)
+#define LAUNCH_QA(HD_, KT_, WO_, F_)                                                                 \
+    do {                                                                                             \
+        const size_t shm_ = F_ ? lds_cap_pad<k_qkv_attn<K_, NB_, KT_, HD_, WO_, F_>>(wgs_per_cu) : 0; \
+        DLAUNCH((k_qkv_attn<K_, NB_, KT_, HD_, WO_, F_>), grid, dim3(WG), shm_, s, x, emb, tok, rms_w, \
+                wqkv, NQ, NKV, rope_cos, rope_sin, pos, B, (KT_ *)kc, (KT_ *)vc, max_seq, npairs,      \
+                nprod, H, tg, out, (const u16 *)wo, ffn);                                            \
+    } while (0)
 #define LAUNCH_QA_KV(WO_, F_)                                    \
     do {                                                         \
         if (hd == 64 && kv_f32) LAUNCH_QA(64, float, WO_, F_);   \

@@ -89,14 +89,18 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * whole layer in one launch.  err: two ints, the flag a hand-off wait that
  * gives up sets (the kernel still ends) and the microseconds before one does
  * (LM_HANDOFF_US unless set by LM_OPT_HANDOFF_US).  B <= 4, hd 64 or
- * 128. */
+ * 128.  wgs_per_cu (1-4; 0 = as registers and LDS allow): at most that many
+ * work-groups of the whole-layer launch share a CU, enforced with dynamic
+ * LDS, so the later roles' work-groups (W1/W3, W2) are dispatched as the
+ * early ones finish instead of all at once. */
 int lmk_qkv_attn(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
                  const float *rms_w, const uint16_t *wqkv, int D, int NQ, int NKV, int hd,
                  const float *rope_cos, const float *rope_sin, const int *pos, int B,
                  void *kc, void *vc, int kv_f32, int max_seq, int H,
                  unsigned long long *tagged, const unsigned *epoch, int layer,
                  int n_layers, int *err, float *out, const uint16_t *wo,
-                 const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F);
+                 const float *rms_ffn, const uint16_t *w13, const uint16_t *w2, int F,
+                 int wgs_per_cu);
 
 /* Whether the whole-layer form of lmk_qkv_attn (w13 given) is built for this
  * model width, hidden width and batch. */
@@ -201,9 +205,10 @@ int lmk_attn_decode_part(hipStream_t s, const float *part, size_t sstride, int n
                          const int *pos, const int *slot, int B, int H, int Hkv, int hd,
                          int max_seq, const float *rope_cos, const float *rope_sin, void *kc,
                          void *vc, int kv_f32, uint16_t *out16);
-/* Arm the calling thread's next decode-chain kernel launch (qkv_rope, attn,
- * wo_residual, ffn13, w2_residual, cls, argmax_final) to be timed
- * with these two events at its dispatch's start and end. */
+/* Arm the calling thread's next decode-chain kernel launch (qkv_rope,
+ * qkv_attn, attn, wo_residual, ffn13, w2_residual, cls, argmax_final) to
+ * record `start` at its dispatch's start and `stop` at its end (either may be
+ * NULL). */
 void lmk_time_next(hipEvent_t start, hipEvent_t stop);
 /* GEMM with K cut into ns splits: part[s][M][N] (fp32) is split s's partial of
  * A W^T; lmk_pick_split chooses ns for a shape (1: do not split). */

@@ -73,6 +73,7 @@ struct LMModel {
      * decode-step count that tags them; the flag a hand-off wait that gives up
      * sets, and the polls before one does */
     int fuse_qa;
+    int layer_wgs;              /* whole-layer work-groups per CU at most (0: no cap) */
     unsigned long long *d_tagged;
     unsigned long long *d_cls_tw;     /* the classifier's argmax partials as tagged words (level 3) */
     unsigned *d_epoch;
@@ -525,6 +526,7 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
         if (hipMemcpy(m->d_err + 1, &lim_us, 4, hipMemcpyHostToDevice) != hipSuccess) FAIL(LM_ERR_HIP);
     }
     m->fuse_qa = 3;
+    m->layer_wgs = 2;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
 
@@ -692,6 +694,13 @@ int lm_set_option(LMModel *m, int option, int value)
         drop_graphs(m);
         m->fuse_qa = value;
         return LM_OK;
+    case LM_OPT_LAYER_WGS:
+        if (value < 0 || value > 4) return LM_ERR_INVALID;
+        if (value == m->layer_wgs) return LM_OK;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        drop_graphs(m);
+        m->layer_wgs = value;
+        return LM_OK;
     case LM_OPT_HANDOFF_US:
         if (value < 1) return LM_ERR_INVALID;
         HIPCHK(hipStreamSynchronize(m->stream));
@@ -771,7 +780,7 @@ static int enqueue_kernel(LMModel *m, int B, int fam, int l, float *logits)
                               m->max_seq, m->H, m->d_tagged, m->d_epoch, l, m->L, m->d_err,
                               m->d_attn, lvl >= 2 ? lw + m->off_wo : NULL,
                               m->d_rms_ffn + (size_t)l * D, lvl == 3 ? lw + m->off_w13 : NULL,
-                              lw + m->off_w2, F));
+                              lw + m->off_w2, F, m->layer_wgs));
         else
             KCHK(lmk_qkv_rope(s, m->d_x, l == 0 ? m->d_embed : NULL, m->d_tok,
                               m->d_rms_att + (size_t)l * D, lw, D, m->NQ, m->NKV, m->hd,
@@ -1403,18 +1412,33 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     if (rc) return rc;
     for (int b = 0; b < B; b++)
         if (pos[b] + steps + 1 > m->max_seq) return LM_ERR_RANGE;
-    /* kernels of one step: 5 per layer, then the classifier and the argmax.
-     * Steps are queued back to back in runs of GRAPH_STEPS, as the greedy
-     * loop's graphs run them (the argmax feeds each step's token to the next
-     * on the device), with one event pair per kernel; the stream is
-     * synchronised and the events read once per run. */
-    const int nk = 5 * m->L + 2, run = GRAPH_STEPS;
-    const size_t nev = 2 * (size_t)nk * run;
+    const int lvl = chain_level(m, B), waits = step_waits(m, B);
+    /* the launches of one step, in order: (family, layer) */
+    const int nmax = 5 * m->L + 2;
+    int *kf = (int *)calloc((size_t)nmax, sizeof(int)), *kl = (int *)calloc((size_t)nmax, sizeof(int));
+    int nk = 0;
+    if (!kf || !kl) rc = LM_ERR_OOM;
+    for (int l = 0; l < m->L && rc == LM_OK; l++)
+        for (int f = 0; f < 5; f++)
+            if (!fam_inside(fams[f], lvl)) { kf[nk] = fams[f]; kl[nk++] = l; }   /* else inside QKV's */
+    for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++)
+        if (!fam_inside(f, lvl)) { kf[nk] = f; kl[nk++] = 0; }   /* else inside the classifier's */
+    /* Each run of consecutive launches of one family (at level 3 the L
+     * whole-layer launches, then the classifier) is timed by one event pair,
+     * the first launch's start to the last one's end, with no event between
+     * them, so the launches meet each other as in the greedy loop's graphs;
+     * the run's time is shared equally among its launches.  Steps are queued
+     * back to back in runs of GRAPH_STEPS, as those graphs run them (the argmax
+     * feeds each step's token to the next on the device); the stream is
+     * synchronised and the events read once per run of steps. */
+    int nrun = 0;
+    for (int i = 0; i < nk; i++) nrun += i == 0 || kf[i] != kf[i - 1];
+    const int chunk = GRAPH_STEPS;
+    const size_t nev = 2 * (size_t)nrun * chunk;
     hipEvent_t *ev = (hipEvent_t *)calloc(nev, sizeof(hipEvent_t));
-    int *kfam = (int *)calloc((size_t)nk * run, sizeof(int));
     double sum[LM_KERN_COUNT] = {0};
     int cnt[LM_KERN_COUNT] = {0};
-    if (!ev || !kfam) rc = LM_ERR_OOM;
+    if (!ev) rc = LM_ERR_OOM;
     for (size_t i = 0; i < nev && rc == LM_OK; i++)
         if (hipEventCreate(&ev[i]) != hipSuccess) rc = LM_ERR_HIP;
     int *hio = m->h_io;
@@ -1425,37 +1449,32 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
             hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream) != hipSuccess)
             rc = LM_ERR_HIP;
     }
-    const int waits = step_waits(m, B), lvl = chain_level(m, B);
-    for (int st0 = 0; st0 <= steps && rc == LM_OK; st0 += run) {   /* step 0 untimed */
-        const int nst = steps + 1 - st0 < run ? steps + 1 - st0 : run;
-        int k = 0;
+    for (int st0 = 0; st0 <= steps && rc == LM_OK; st0 += chunk) {   /* step 0 untimed */
+        const int nst = steps + 1 - st0 < chunk ? steps + 1 - st0 : chunk;
         if (waits && (rc = handoff_enter(m))) break;
-        for (int t = 0; t < nst && rc == LM_OK; t++) {
-            for (int l = 0; l < m->L && rc == LM_OK; l++)
-                for (int f = 0; f < 5 && rc == LM_OK; f++) {
-                    if (fam_inside(fams[f], lvl)) continue;   /* inside the QKV launch */
-                    kfam[k] = st0 + t > 0 ? fams[f] : -1;
-                    lmk_time_next(ev[2 * k], ev[2 * k + 1]);
-                    rc = enqueue_kernel(m, B, fams[f], l, NULL);
-                    k++;
-                }
-            for (int f = LM_KERN_CLS; f <= LM_KERN_ARGMAX && rc == LM_OK; f++) {
-                if (fam_inside(f, lvl)) continue;   /* inside the classifier launch */
-                kfam[k] = st0 + t > 0 ? f : -1;
-                lmk_time_next(ev[2 * k], ev[2 * k + 1]);
-                rc = enqueue_kernel(m, B, f, 0, NULL);
-                k++;
+        for (int t = 0, r = 0; t < nst && rc == LM_OK; t++)
+            for (int i = 0; i < nk && rc == LM_OK; i++) {
+                const int first = i == 0 || kf[i] != kf[i - 1], last = i == nk - 1 || kf[i + 1] != kf[i];
+                if (first || last)
+                    lmk_time_next(first ? ev[2 * r] : NULL, last ? ev[2 * r + 1] : NULL);
+                rc = enqueue_kernel(m, B, kf[i], kl[i], NULL);
+                r += last;
             }
-        }
         if (waits) rc = handoff_leave(m, rc);
         if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
-        for (int i = 0; i < k && rc == LM_OK; i++) {
-            float ms = 0.f;
-            if (kfam[i] < 0) continue;
-            if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = LM_ERR_HIP;
-            sum[kfam[i]] += ms;
-            cnt[kfam[i]]++;
-        }
+        for (int t = 0, r = 0; t < nst && rc == LM_OK; t++)
+            for (int i = 0, len = 0; i < nk && rc == LM_OK; i++) {
+                len++;
+                if (!(i == nk - 1 || kf[i + 1] != kf[i])) continue;
+                float ms = 0.f;
+                if (hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]) != hipSuccess) rc = LM_ERR_HIP;
+                if (st0 + t > 0) {
+                    sum[kf[i]] += ms;
+                    cnt[kf[i]] += len;
+                }
+                r++;
+                len = 0;
+            }
     }
     for (int f = 0; f < LM_KERN_COUNT; f++) {
         us_per_launch[f] = cnt[f] ? (float)(sum[f] * 1e3 / cnt[f]) : 0.f;
@@ -1467,7 +1486,8 @@ int lm_profile_chain(LMModel *m, int B, const int *tokens, const int *pos, int s
     for (size_t i = 0; ev && i < nev; i++)
         if (ev[i]) hipEventDestroy(ev[i]);
     free(ev);
-    free(kfam);
+    free(kf);
+    free(kl);
     if (rc == LM_OK)
         HIPCHK(hipMemcpyAsync(m->d_pos, hio + B, B * 4, hipMemcpyHostToDevice, m->stream));
     if (rc == LM_OK) rc = queue_err_read(m);

@@ -74,8 +74,9 @@ def profiled_traffic(kernel_prefix):
         text = open(PROFILE_C0).read()
     except OSError:
         return None
+    want = kernel_prefix.replace(" ", "")
     for mt in re.finditer(r"^counters (\S+) fetch_bytes=(\d+) write_bytes=(\d+)", text, re.M):
-        if mt.group(1).startswith(kernel_prefix):
+        if mt.group(1).startswith(want):
             return {"fetch": int(mt.group(2)), "write": int(mt.group(3)), "kernel": mt.group(1)}
     return None
 

@@ -261,6 +261,13 @@ int lm_timer_end(LMModel *m, float *ms);
  * that every hand-off wait of the next decode call ends at once and that call
  * returns LM_ERR_HIP (the flag is then cleared).  For tests of that path. */
 #define LM_OPT_HANDOFF_ABORT 7
+/* LM_OPT_LAYER_WGS: at most this many work-groups of the whole-layer launch
+ * (LM_OPT_FUSE_QKV_ATTN 3/4) share a CU (1-4, default 3; 0 = as many as
+ * registers and LDS allow).  The launch holds more work-groups than the
+ * device runs at once; with the cap, the W1/W3 and W2 work-groups are
+ * dispatched as the QKV ones finish, so their weight loads do not compete
+ * with the first roles'. */
+#define LM_OPT_LAYER_WGS   8
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------
@@ -363,8 +370,11 @@ int lm_gemm_split_count(int M, int N, int K);
 /* Mean device microseconds per launch of each decode kernel family inside the
  * real decode chain: `steps` greedy decode steps of B rows from tokens[b] at
  * positions pos[b] (advancing as a decode does), launched directly and queued
- * back to back in runs of 16 steps as the greedy loop's graphs run them,
- * every kernel timed by events at its own dispatch's device start and end.
+ * back to back in runs of 16 steps as the greedy loop's graphs run them.
+ * Each run of consecutive launches of one family (at the default fusion level
+ * the n_layers whole-layer launches of a step, then the classifier) is timed
+ * by events at its first dispatch's device start and its last one's end, with
+ * no event between them, and its time shared equally among its launches.
  * One untimed step runs first.  launches_per_step[k] (may
  * be NULL) = launches of family k in one decode step.  Needs pos[b] + steps +
  * 1 <= max_seq; leaves the KV cache at those positions and the activations

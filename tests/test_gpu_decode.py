@@ -1,8 +1,13 @@
 """Decode path on the GPU against the oracle (through the C ABI).
 
-Tolerances: with the K/V cache in the oracle's precision only the summation
-order differs (measured <= 6e-6 on Stories logits), so logits must agree to
-atol 1e-4 and greedy ids exactly.  Against the fp32-cache oracle (the
+Tolerances: with an fp32 K/V cache only the summation order differs from the
+oracle (measured <= 6e-6 on Stories logits), so logits must agree to atol
+1e-4 and greedy ids exactly.  With a binary16 cache the oracle rounds K/V the
+same way, but the device's K/V values before that rounding differ from the
+oracle's in the last fp32 bits (summation order), so now and then one cached
+element lands one binary16 ulp away and moves later logits by up to a few
+1e-4: those comparisons take atol 1e-3 + rtol 1e-3 (KV16), as the Stories C0
+comparison of the same cache does.  Against the fp32-cache oracle (the
 reference's own forward) a binary16 cache is held to the north-star bound,
 atol 2e-2 + rtol 1e-2.
 """
@@ -17,6 +22,7 @@ from conftest import GOLDEN, TINY, TINY_GQA, TINY_HD128, cfg7
 pytestmark = pytest.mark.gpu
 
 TIGHT = dict(rtol=1e-4, atol=1e-4)
+KV16 = dict(rtol=1e-3, atol=1e-3)
 NORTH_STAR = dict(rtol=1e-2, atol=2e-2)
 
 
@@ -56,7 +62,7 @@ def test_tiny_decode_steps_match_oracle(lm, name, d, kv, fuse):
     m, _ = make(lm, d, int(fx["seed"]), 1, d["seq_len"], kv == 32)
     m.set_option(lm.LM_OPT_FUSE_QKV_ATTN, fuse)
     got = np.stack([m.forward(int(t), p) for p, t in enumerate(fx["tokens"])])
-    np.testing.assert_allclose(got, fx[f"logits_kv{kv}"], **TIGHT)
+    np.testing.assert_allclose(got, fx[f"logits_kv{kv}"], **(TIGHT if kv == 32 else KV16))
     np.testing.assert_allclose(got, fx["logits_kv32"], **NORTH_STAR)
     g = m.generate_greedy([1], [0], 48)[:, 0]
     assert np.array_equal(g, fx[f"greedy_kv{kv}"])
