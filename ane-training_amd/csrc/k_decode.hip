@@ -429,6 +429,16 @@ __global__ void __launch_bounds__(WG) k_qkv_rope(
 
 /* ---- decode attention ------------------------------------------------------- */
 
+/* Materialise a float4 in registers at this point of the program (an empty
+ * asm that reads and writes each element), so the compiler cannot sink the
+ * code that computed it past later code. */
+__device__ __forceinline__ void pin4(float4 &v)
+{
+    float x = v.x, y = v.y, z = v.z, w = v.w;
+    asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
+    v = make_float4(x, y, z, w);
+}
+
 /* 8 cache elements at p as raw bits (fp16: one 16-byte load; fp32: two). */
 struct KV8h { uint4 a; };
 struct KV8f { float4 a, b; };
@@ -626,6 +636,38 @@ __device__ __forceinline__ void attn_head(
             }
         }
     }
+    /* Binary16 cache in the fused launch: the two tiles loaded above are
+     * converted to fp32 here, before the wait for q, k, v, so that the
+     * conversions (16 per position per lane) are off the path from the
+     * words' arrival to the head output; the empty asm keeps the compiler from
+     * sinking them past the wait.  (The fp32 cache needs no conversion; with
+     * two whole-layer work-groups per CU the registers are there at head dim
+     * 64: 164 VGPRs.  At 128 two converted tiles take 256 registers.) */
+    constexpr bool PRECVT = DB && sizeof(KT) == 2 && HD == 64;
+    KV8f ck[PRECVT ? 2 : 1][NP], cv[PRECVT ? 2 : 1][NP];
+    if constexpr (PRECVT) {
+        if (qt) {
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                float f[8];
+                kv_raw_unpack(kr[i], f);
+                ck[0][i] = KV8f{make_float4(f[0], f[1], f[2], f[3]), make_float4(f[4], f[5], f[6], f[7])};
+                kv_raw_unpack(vr[i], f);
+                cv[0][i] = KV8f{make_float4(f[0], f[1], f[2], f[3]), make_float4(f[4], f[5], f[6], f[7])};
+                kv_raw_unpack(kr1[i], f);
+                ck[1][i] = KV8f{make_float4(f[0], f[1], f[2], f[3]), make_float4(f[4], f[5], f[6], f[7])};
+                kv_raw_unpack(vr1[i], f);
+                cv[1][i] = KV8f{make_float4(f[0], f[1], f[2], f[3]), make_float4(f[4], f[5], f[6], f[7])};
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int i = 0; i < NP; i++) {
+                    pin4(ck[u][i].a); pin4(ck[u][i].b);
+                    pin4(cv[u][i].a); pin4(cv[u][i].b);
+                }
+        }
+    }
     if (qt) {
         /* q, k, v of the current position from the tagged hand-off words the
          * QKV work-groups of this launch store (k, v as the cache holds
@@ -685,7 +727,7 @@ __device__ __forceinline__ void attn_head(
     };
     auto fadd = [](float a, float b) { return a + b; };
     /* online softmax update with tile t (forward.h:82-97), held in kr/vr */
-    auto consume = [&](int t, const Raw (&tk)[NP], const Raw (&tv)[NP]) {
+    auto consume = [&](int t, const auto (&tk)[NP], const auto (&tv)[NP]) {
         float s[NP];
         float tmax = -INFINITY;
 #pragma unroll
@@ -731,7 +773,18 @@ __device__ __forceinline__ void attn_head(
             }
         };
         if (!EARLY && !qt) fetch(wv, kr, vr);
-        if constexpr (DB) {
+        if (PRECVT && qt) {
+            /* the converted first two tiles, then any later ones one at a
+             * time (contexts past 8 tiles) */
+            if (wv < ntiles) {                                   /* wave-uniform */
+                consume(wv, ck[0], cv[0]);
+                if (wv + NWAVE < ntiles) consume(wv + NWAVE, ck[PRECVT ? 1 : 0], cv[PRECVT ? 1 : 0]);
+                for (int t = wv + 2 * NWAVE; t < ntiles; t += NWAVE) {
+                    fetch(t, kr, vr);
+                    consume(t, kr, vr);
+                }
+            }
+        } else if constexpr (DB) {
             /* kr holds the wave's first tile and kr1 its second (both in
              * flight); the first tile is consumed outside the loop, which keeps
              * the loop's registers at two tiles (143 -> 109 VGPRs at hd 64).
