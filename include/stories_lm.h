@@ -262,7 +262,7 @@ int lm_timer_end(LMModel *m, float *ms);
  * returns LM_ERR_HIP (the flag is then cleared).  For tests of that path. */
 #define LM_OPT_HANDOFF_ABORT 7
 /* LM_OPT_LAYER_WGS: at most this many work-groups of the whole-layer launch
- * (LM_OPT_FUSE_QKV_ATTN 3/4) share a CU (1-4, default 3; 0 = as many as
+ * (LM_OPT_FUSE_QKV_ATTN 3/4) share a CU (1-4, default 2; 0 = as many as
  * registers and LDS allow).  The launch holds more work-groups than the
  * device runs at once; with the cap, the W1/W3 and W2 work-groups are
  * dispatched as the QKV ones finish, so their weight loads do not compete
