@@ -87,6 +87,7 @@ struct EpiArgs {
     const float *gain;      /* RESNORM: gain [N]; u [M, N] fp16; ss [M, nss] */
     u16 *u;
     float *ss;
+    int *ovf;               /* RESNORM: set when a u value overflows fp16 (may be NULL) */
     const float *rs_ss;     /* STORE / GATE / QKV: row sums of squares [M, nss] of the
                              * RESNORM that wrote A, or NULL */
     int nss;
@@ -155,6 +156,13 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) v[i] = xv[i] + acc[i];
+        /* u is rounded before the row is normalised: a |x * gain| that fp16
+         * cannot hold (65520 and up round to infinity; NaN too) is reported,
+         * and the caller redoes the rows with the row norm apart */
+        bool big = false;
+#pragma unroll
+        for (int i = 0; i < 16; i++) big |= ok[i] && !(fabsf(v[i] * gn) < 65520.f);
+        if (big && e.ovf) *e.ovf = 1;
         if (m0 + 32 <= e.M && n0 + 32 <= e.N) {   /* whole tile: no per-element masks */
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -1022,7 +1030,7 @@ static EpiArgs to_epi(const LMEpilogue *p, int M, int N)
     e.slot = p->slot; e.pos = p->pos; e.rope_cos = p->rope_cos; e.rope_sin = p->rope_sin;
     e.sstride = 0;
     e.nt = p->stream_out;
-    e.gain = p->gain; e.u = (u16 *)p->u; e.ss = p->ss;
+    e.gain = p->gain; e.u = (u16 *)p->u; e.ss = p->ss; e.ovf = p->ovf;
     e.rs_ss = p->rs_ss; e.nss = p->nss;
     return e;
 }

@@ -185,6 +185,9 @@ typedef struct {
     const float *gain;
     uint16_t *u;
     float *ss;
+    int *ovf;                /* RESNORM: set to 1 when a u value is not finite (fp16
+                              * overflow of out * gain), or NULL; a device-visible
+                              * address (pinned host memory) */
     /* GATE / QKV after a RESNORM GEMM: with rs_ss, product row m is
      * first scaled by 1/sqrt(sum_b rs_ss[m, b] / (32 nss) + 1e-5), the RMSNorm
      * of that row (forward.h:46-53) whose gain is already in the operand */

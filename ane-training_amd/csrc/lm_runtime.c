@@ -73,6 +73,9 @@ struct LMModel {
      * decode-step count that tags them; the flag a hand-off wait that gives up
      * sets, and the polls before one does */
     int fuse_qa;
+    int prefill_fold;           /* LM_OPT_PREFILL_FOLD */
+    int fold_off;               /* the folded norm is off for the rows being redone */
+    int *d_ovf;                 /* device address of ovf_slot: RESNORM's overflow flag */
     int layer_wgs;              /* whole-layer work-groups per CU at most (0: no cap) */
     unsigned long long *d_tagged;
     unsigned long long *d_cls_tw;     /* the classifier's argmax partials as tagged words (level 3) */
@@ -527,8 +530,14 @@ static LMModel *create_model(const Config *cfg, const WSrc *w, int max_batch, in
     }
     m->fuse_qa = 3;
     m->layer_wgs = 2;
+    m->prefill_fold = 1;
     if (hipHostMalloc((void **)&m->h_logits, (size_t)max_batch * V * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
     if (hipHostMalloc((void **)&m->h_io, (size_t)4 * (max_batch + 1) * 4, 0) != hipSuccess) FAIL(LM_ERR_OOM);
+    memset(m->h_io, 0, (size_t)4 * (max_batch + 1) * 4);
+    /* RESNORM's overflow flag: the int after the hand-off flag's slot, written
+     * by the device only when a prefill row overflows */
+    if (hipHostGetDevicePointer((void **)&m->d_ovf, m->h_io + 4 * (size_t)max_batch + 1, 0) != hipSuccess)
+        FAIL(LM_ERR_HIP);
 
     if ((st = upload_weights(m, w))) goto fail;
     {
@@ -701,6 +710,13 @@ int lm_set_option(LMModel *m, int option, int value)
         drop_graphs(m);
         m->layer_wgs = value;
         return LM_OK;
+    case LM_OPT_PREFILL_FOLD:
+        if (value != 0 && value != 1) return LM_ERR_INVALID;
+        if (value == m->prefill_fold) return LM_OK;
+        HIPCHK(hipStreamSynchronize(m->stream));
+        drop_graphs(m);
+        m->prefill_fold = value;
+        return LM_OK;
     case LM_OPT_HANDOFF_US:
         if (value < 1) return LM_ERR_INVALID;
         HIPCHK(hipStreamSynchronize(m->stream));
@@ -869,8 +885,12 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
      * launch and the product's round trip through memory.  K-split
      * projections keep the row norm, which adds their partials (an unsplit
      * 2048-row W2 took 20 us against 14 + 5.6 for the split and the norm);
-     * so do layer 0 (embedding) and the classifier. */
-    const int can_fold = !dec && D % 128 == 0 && D / 32 <= 64;
+     * so do layer 0 (embedding) and the classifier.  Only prefill rows fold
+     * (LM_OPT_PREFILL_FOLD): u is rounded to fp16 before the row is
+     * normalised, and a prefill chunk whose u overflows is redone with the
+     * row norm apart (run_prefill); decode rows have no such retry. */
+    const int can_fold = !dec && seq_rows > 1 && m->prefill_fold && !m->fold_off && D % 128 == 0 &&
+                         D / 32 <= 64;
     const int fold_wo = can_fold && ns_wo == 1, fold_w2 = can_fold && ns_w2 == 1;
     int rs_next = 0;                   /* x's norm is pending in u for QKV */
     const float *pend = NULL;          /* W2 partials not yet added to x */
@@ -916,6 +936,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             memset(&ep, 0, sizeof(ep));
             ep.out = m->d_x; ep.ldc = D;
             ep.gain = m->d_rms_ffn + (size_t)l * D; ep.u = m->d_xn16; ep.ss = m->d_ss; ep.nss = D / 32;
+            ep.ovf = m->d_ovf;
             KCHK(lmk_gemm(s, m->d_a16, NQ, lw + m->off_wo, M, D, NQ, LMK_EPI_RESNORM, &ep));
         } else if (sep_wo) {
             if (ns_wo > 1) {
@@ -944,7 +965,7 @@ static int enqueue_rows(LMModel *m, int M, int seq_rows, const int *tok, const i
             ep.out = m->d_x; ep.ldc = D;
             if (l + 1 < m->L) {   /* u of the next layer's attention norm */
                 ep.gain = m->d_rms_att + (size_t)(l + 1) * D; ep.u = m->d_xn16; ep.ss = m->d_ss;
-                ep.nss = D / 32;
+                ep.nss = D / 32; ep.ovf = m->d_ovf;
             }
             KCHK(lmk_gemm(s, m->d_g16, F, lw + m->off_w2, M, D, F,
                           l + 1 < m->L ? LMK_EPI_RESNORM : LMK_EPI_RESID, &ep));
@@ -1217,7 +1238,7 @@ static int enqueue_cls_rows(LMModel *m, float *x_rows, int M)
 static int run_rows(LMModel *m, int R, int S, int all)
 {
     const int *tok = m->d_rin, *pos = m->d_rin + R, *slot = m->d_rin + 2 * (size_t)R;
-    if (!m->use_graph)
+    if (!m->use_graph || m->fold_off)   /* (the graphs hold the folded form) */
         return enqueue_rows(m, R, S, tok, pos, slot, all ? m->d_logits : NULL, all);
     int k = 0;
     while (k < PREFILL_GRAPHS &&
@@ -1297,27 +1318,37 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
             rc = LM_ERR_HIP;
             break;
         }
-        if (logits_mode == LM_LOGITS_ALL) {
-            rc = run_rows(m, R, S, 1);
-            if (rc == LM_OK && logits &&
-                hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
-                               hipMemcpyDeviceToHost, m->stream) != hipSuccess)
-                rc = LM_ERR_HIP;
-        } else {
-            rc = run_rows(m, R, S, 0);
-            /* gather the last row of each sequence into d_attn (same row width) */
-            if (rc == LM_OK &&
-                hipMemcpy2DAsync(m->d_attn, (size_t)m->D * 4, m->d_x + (size_t)(S - 1) * m->D,
-                                 (size_t)S * m->D * 4, (size_t)m->D * 4, n,
-                                 hipMemcpyDeviceToDevice, m->stream) != hipSuccess)
-                rc = LM_ERR_HIP;
-            if (rc == LM_OK) rc = enqueue_cls_rows(m, m->d_attn, n);
-            if (rc == LM_OK && logits &&
-                hipMemcpyAsync(logits + (size_t)i0 * V, m->d_logits, (size_t)n * V * 4,
-                               hipMemcpyDeviceToHost, m->stream) != hipSuccess)
-                rc = LM_ERR_HIP;
+        /* pass 1 only when pass 0's folded norm overflowed fp16 (its u is
+         * x * gain before the row is normalised): the same rows again with
+         * the row norm apart, rewriting the same cache entries */
+        for (int pass = 0; pass < 2 && rc == LM_OK; pass++) {
+            if (logits_mode == LM_LOGITS_ALL) {
+                rc = run_rows(m, R, S, 1);
+                if (rc == LM_OK && logits &&
+                    hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
+                                   hipMemcpyDeviceToHost, m->stream) != hipSuccess)
+                    rc = LM_ERR_HIP;
+            } else {
+                rc = run_rows(m, R, S, 0);
+                /* gather the last row of each sequence into d_attn (same row width) */
+                if (rc == LM_OK &&
+                    hipMemcpy2DAsync(m->d_attn, (size_t)m->D * 4, m->d_x + (size_t)(S - 1) * m->D,
+                                     (size_t)S * m->D * 4, (size_t)m->D * 4, n,
+                                     hipMemcpyDeviceToDevice, m->stream) != hipSuccess)
+                    rc = LM_ERR_HIP;
+                if (rc == LM_OK) rc = enqueue_cls_rows(m, m->d_attn, n);
+                if (rc == LM_OK && logits &&
+                    hipMemcpyAsync(logits + (size_t)i0 * V, m->d_logits, (size_t)n * V * 4,
+                                   hipMemcpyDeviceToHost, m->stream) != hipSuccess)
+                    rc = LM_ERR_HIP;
+            }
+            if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
+            volatile int *ovf = m->h_io + 4 * (size_t)m->max_batch + 1;
+            if (rc != LM_OK || !*ovf) break;
+            *ovf = 0;
+            m->fold_off = 1;
         }
-        if (rc == LM_OK && hipStreamSynchronize(m->stream) != hipSuccess) rc = LM_ERR_HIP;
+        m->fold_off = 0;
     }
     /* after a failure, let the copy out of the staging buffer finish before
      * a later call refills it */

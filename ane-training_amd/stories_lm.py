@@ -37,6 +37,7 @@ LM_OPT_FUSE_QKV_ATTN = 5
 LM_OPT_HANDOFF_US = 6
 LM_OPT_HANDOFF_ABORT = 7
 LM_OPT_LAYER_WGS = 8
+LM_OPT_PREFILL_FOLD = 9
 # kernel families of a decode step (LM_KERN_* in stories_lm.h)
 KERN_NAMES = ("qkv", "attn", "wo", "w13", "w2", "cls", "argmax")
 

@@ -268,6 +268,13 @@ int lm_timer_end(LMModel *m, float *ms);
  * dispatched as the QKV ones finish, so their weight loads do not compete
  * with the first roles'. */
 #define LM_OPT_LAYER_WGS   8
+/* LM_OPT_PREFILL_FOLD: 1 (default) folds the row norm after an unsplit Wo or
+ * W2 of a prefill chunk into the GEMMs on either side (the GEMM writes
+ * fp16(x * gain) and the row's sums of squares; the next GEMM scales its
+ * product rows), 0 keeps the row norm a launch of its own.  The folded operand
+ * is rounded before the row is normalised; a chunk in which it overflows
+ * fp16 is redone with the norm apart, so both give finite results. */
+#define LM_OPT_PREFILL_FOLD 9
 int lm_set_option(LMModel *m, int option, int value);
 
 /* ---------------------------------------------------------------------------

@@ -217,6 +217,38 @@ def test_prefill_folded_norms_match_oracle(lm, orc, name, d, nseq, kv32):
     m.close()
 
 
+def test_prefill_fold_overflow_is_redone_unfused(lm):
+    """The folded norm rounds x * gain to fp16 before the row is normalised.
+    A model whose residual stream is far from unit scale (embedding rows of
+    magnitude up to about 5e4, FFN norm gains of 8) overflows it: the epilogue
+    flags the chunk, which is redone with the row norm apart, so the logits
+    are finite and equal, bit for bit, those of the same prefill with
+    LM_OPT_PREFILL_FOLD 0 (the same kernels on the same inputs).  At 768 rows
+    of dim 768 both Wo and W2 are unsplit, so both fold."""
+    _say("[prefill fold overflow]")
+    d = FOLD_WO
+    nseq, S, D, F, L, V = 3, d["seq_len"], d["dim"], d["hidden_dim"], d["n_layers"], d["vocab_size"]
+    assert lm.gemm_split_count(nseq * S, D, D) == 1 and lm.gemm_split_count(nseq * S, D, F) == 1
+    cfg = lm.make_config(**d)
+    w16 = lm.synth_weights_f16(cfg, 53, 0.02, True)
+    emb = lm.f16_to_f32(w16[:V * D])
+    w16[:V * D] = lm.f32_to_f16(np.clip(emb * 5e5, -6e4, 6e4))
+    o = V * D + L * D + 4 * L * D * D        # rms_ffn after emb, rms_att, wq, wk, wv, wo (MHA)
+    w16[o:o + L * D] = lm.f32_to_f16(np.full(L * D, 8.0, np.float32))
+    m = lm.Model.create(cfg, w16, True, nseq, S)
+    toks = np.random.default_rng(53).integers(0, V, (nseq, S)).astype(np.int32)
+    a = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    a2 = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    m.set_option(lm.LM_OPT_PREFILL_FOLD, 0)
+    b = m.prefill_batch(toks, mode=lm.LM_LOGITS_ALL)
+    assert np.all(np.isfinite(b))
+    assert np.array_equal(a, b) and np.array_equal(a2, b)
+    for bad in (-1, 2):
+        with pytest.raises(lm.LMError):
+            m.set_option(lm.LM_OPT_PREFILL_FOLD, bad)
+    m.close()
+
+
 def _batched_decode_vs_oracle(lm, orc, d, B, seed, kv32=False):
     """Prompts prefilled per slot, then teacher-forced batched steps (MFMA
     decode path) against the oracle, then greedy runs."""
