@@ -19,10 +19,11 @@ to the device path are caught, and so GPU tests need no long CPU runs.
                    (the reference forward): the prompt's last-row logits, then
                    128 greedy decode steps at positions 512..639; per row the
                    top-32 (logit, id) pairs, 256 fixed sampled columns, sum and
-                   sum of squares, and the 129 greedy ids.
+                   sum of squares, and the 129 greedy ids; and the same digest of
+                   the prompt's last-row logits of all 32 sequences (*_prompts).
 
 Run:  python tests/golden/make_fixtures.py [name ...]   (names: tiny, c0, c4;
-      about a minute for tiny + c0 and a few minutes for c4 on 8 cores)
+      about a minute for tiny + c0 and about ten minutes for c4 on 8 cores)
 """
 import os
 import sys
@@ -110,6 +111,14 @@ def scaled_c4():
             out[f"{k}_{b}"] = v
         out[f"ids_{b}"] = np.array(ids, np.int32)
         print(f"c4 sequence {b}: {time.time() - t0:.1f} s", flush=True)
+    rows = []
+    for b in range(32):
+        o = O.Oracle(cfg7(SCALED), w32, True, 640)
+        rows.append(o.forward_cached(prompts[b], 0, last_only=True))
+        o.close()
+    for k, v in row_digest(np.stack(rows), cols).items():
+        out[f"{k}_prompts"] = v
+    print("c4 prompt rows of every sequence", flush=True)
     np.savez_compressed(os.path.join(HERE, "scaled_c4.npz"), **out)
     print("wrote scaled_c4")
 

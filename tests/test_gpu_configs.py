@@ -110,7 +110,11 @@ def test_stories_c2_full_shape(lm, orc):
     seed) prefilled into the fp16 cache, then 64 decode steps of all 64 rows on
     the MFMA decode path (K-split QKV, split-sum attention over 192-255 cached
     positions).  Four sequences against the reference forward: prompt logits,
-    every logit of the 64 teacher-forced steps, and the greedy ids."""
+    every logit of the 64 teacher-forced steps, and the greedy ids.  Every
+    sequence's prompt logits against the reference forward, and every sequence
+    through the slots: with sequence i in slot perm[i] the prompt logits and
+    greedy ids are the same bit for bit (a decode row's arithmetic does not
+    depend on its slot or its place in the batch)."""
     _say("[C2 full shape]")
     d = lm.STORIES_110M
     B, P, T = 64, 192, 64
@@ -133,11 +137,22 @@ def test_stories_c2_full_shape(lm, orc):
     # greedy from the prompt's argmax (positions 192..255 rewritten in order)
     first = np.argmax(lg0, 1).astype(np.int32)
     ids = m.generate_greedy(first, np.full(B, P, np.int32), T)
+    # sequence i in slot perm[i]: the same prefill chunks, the decode rows permuted
+    perm = np.random.default_rng(5).permutation(B).astype(np.int32)
+    assert np.array_equal(m.prefill_batch(prompts, slots=perm, mode=lm.LM_LOGITS_LAST), lg0)
+    first_slot = np.empty_like(first)
+    first_slot[perm] = first
+    assert np.array_equal(m.generate_greedy(first_slot, np.full(B, P, np.int32), T)[:, perm], ids)
     m.close()
     for b in check:
         rows, rids = ref[b]
         got = np.concatenate([[first[b]], ids[:, b]])
         check_trajectory(got, rids, [margin(r) for r in rows], f"sequence {b}")
+    for b in range(B):
+        if b not in check:
+            o = orc.Oracle(cfg7(d), w32, True, 256)
+            close_ns(lg0[b], o.forward_cached(prompts[b], 0, last_only=True), f"prompt {b}")
+            o.close()
 
 
 # ---- C4: the scaled model, 32 x (512-token prompt + 128 greedy steps) ----------
@@ -146,17 +161,28 @@ SCALED = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16,
               seq_len=640)
 
 
+def _digest_ok(row, cols, top_idx, top_val, cols_val, rsum, rsumsq, what):
+    got = np.concatenate([row[top_idx], row[cols]])
+    close_ns(got, np.concatenate([top_val, cols_val]), what)
+    r64 = row.astype(np.float64)
+    assert abs(r64.sum() - rsum) < 2.0, what
+    assert abs((r64 ** 2).sum() - rsumsq) < 1e-2 * rsumsq, what
+
+
 def check_digest(row, fx, b, k, what):
     """A logit row against the committed digest of the oracle's row k of
     sequence b: its top-32 ids and the 256 sampled columns within the
     north-star bound (mean |error| below 2e-3), the row sum within 2 (32000
     terms of the same bound would allow 640) and the sum of squares within 1%."""
-    got = np.concatenate([row[fx[f"top_idx_{b}"][k]], row[fx["cols"]]])
-    want = np.concatenate([fx[f"top_val_{b}"][k], fx[f"cols_val_{b}"][k]])
-    close_ns(got, want, what)
-    r64 = row.astype(np.float64)
-    assert abs(r64.sum() - fx[f"sum_{b}"][k]) < 2.0, what
-    assert abs((r64 ** 2).sum() - fx[f"sumsq_{b}"][k]) < 1e-2 * fx[f"sumsq_{b}"][k], what
+    _digest_ok(row, fx["cols"], fx[f"top_idx_{b}"][k], fx[f"top_val_{b}"][k], fx[f"cols_val_{b}"][k],
+               fx[f"sum_{b}"][k], fx[f"sumsq_{b}"][k], what)
+
+
+def check_prompt_digest(row, fx, b, what):
+    """The prompt's last-row logits of sequence b against the committed digest
+    of the oracle's (every sequence has one), with check_digest's bounds."""
+    _digest_ok(row, fx["cols"], fx["top_idx_prompts"][b], fx["top_val_prompts"][b],
+               fx["cols_val_prompts"][b], fx["sum_prompts"][b], fx["sumsq_prompts"][b], what)
 
 
 def test_scaled_c4_full_shape(lm):
@@ -165,7 +191,10 @@ def test_scaled_c4_full_shape(lm):
     prefilled into the fp16 cache, then 128 decode steps of all 32 rows over
     512-639 cached positions.  Sequences 0 and 31 against the committed digest
     of the reference forward (tests/golden/scaled_c4.npz): prompt logits, the
-    128 teacher-forced steps, and the greedy ids."""
+    128 teacher-forced steps, and the greedy ids; the prompt logits of all 32
+    sequences against their digests.  Every sequence through the
+    slots: with sequence i in slot perm[i] the prompt logits and greedy ids are
+    the same bit for bit."""
     _say("[C4 full shape]")
     fx = np.load(os.path.join(GOLDEN, "scaled_c4.npz"))
     B, P, T = 32, 512, int(fx["n_steps"])
@@ -178,6 +207,8 @@ def test_scaled_c4_full_shape(lm):
     seqs = [int(b) for b in fx["seqs"]]
     for b in seqs:
         check_digest(lg0[b], fx, b, 0, f"prompt {b}")
+    for b in range(B):
+        check_prompt_digest(lg0[b], fx, b, f"prompt row of sequence {b}")
     toks = np.argmax(lg0, 1).astype(np.int32)
     for s in range(T):
         for b in seqs:
@@ -188,6 +219,12 @@ def test_scaled_c4_full_shape(lm):
         toks = am
     first = np.argmax(lg0, 1).astype(np.int32)
     ids = m.generate_greedy(first, np.full(B, P, np.int32), T)
+    # sequence i in slot perm[i]: the same prefill chunks, the decode rows permuted
+    perm = np.random.default_rng(6).permutation(B).astype(np.int32)
+    assert np.array_equal(m.prefill_batch(prompts, slots=perm, mode=lm.LM_LOGITS_LAST), lg0)
+    first_slot = np.empty_like(first)
+    first_slot[perm] = first
+    assert np.array_equal(m.generate_greedy(first_slot, np.full(B, P, np.int32), T)[:, perm], ids)
     m.close()
     for b in seqs:
         got = np.concatenate([[first[b]], ids[:, b]])
