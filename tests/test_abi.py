@@ -28,6 +28,34 @@ def test_header_declares_the_boundary():
         assert must in names
 
 
+def declared_constants():
+    """Every integer #define and explicitly valued enumerator of the headers
+    (status codes, dtypes, options, logits modes): name -> value."""
+    out = {}
+    for h in HEADERS:
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for name, val in re.findall(r"^#define\s+((?:LM|ANE)_\w+)\s+\(?(-?\d+)\)?\s*$", src, flags=re.M):
+            out[name] = int(val)
+        for body in re.findall(r"enum\s*\{([^}]*)\}", src):   # enumerators with explicit values
+            for name, val in re.findall(r"((?:LM|ANE)_\w+)\s*=\s*(-?\d+)", body):
+                out[name] = int(val)
+    return out
+
+
+def test_binding_constants_match_the_header(lm):
+    """The ctypes mirror's status codes, dtypes, options and logits modes carry
+    the header's values (a renumbered option would otherwise set another)."""
+    consts = declared_constants()
+    assert {"LM_OK", "LM_ERR_HIP", "LM_OPT_USE_GRAPH", "LM_OPT_PREFILL_FOLD", "LM_LOGITS_LAST"} <= set(consts)
+    mirrored = {n: v for n, v in vars(lm).items() if n.startswith("LM_") and isinstance(v, int)}
+    assert mirrored, "no constants in the binding"
+    wrong = {n: (v, consts.get(n)) for n, v in mirrored.items() if consts.get(n) != v}
+    assert not wrong, wrong
+    missing = [n for n in consts if n.startswith(("LM_OPT_", "LM_ERR_", "LM_DTYPE_", "LM_LOGITS_"))
+               and n not in mirrored]
+    assert not missing, missing
+
+
 def test_library_exports_every_declared_symbol(lm):
     L = lm.lib()
     missing = [n for n in declared_functions() if not hasattr(L, n)]
