@@ -229,6 +229,15 @@ int lmk_gemm_split(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W,
 int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t *emb, const int *tok,
                 const float *sp, int ns, size_t sstride, const float *gain, uint16_t *xn);
 
+/* ---- loss terms (k_loss.hip) ---------------------------------------------- */
+
+/* M logit rows [M, V] of M/S sequences of S rows, tokens tok[M]: lp[r] =
+ * log softmax(logits[r])[tok[r+1]] for rows that are not the last of their
+ * sequence (model_forward's loss terms, training/forward.h:174-183), 0 for
+ * the last.  V % 4 == 0, S >= 2, M % S == 0. */
+int lmk_row_logprob(hipStream_t s, const float *logits, int V, const int *tok, int S, int M,
+                    float *lp);
+
 /* ---- allocation-free entry point (k_noalloc.hip) -------------------------- */
 
 /* Look up, once for the current device, the device address of the static

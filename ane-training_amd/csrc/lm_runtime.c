@@ -63,8 +63,9 @@ struct LMModel {
     uint16_t *d_xn16, *d_a16;   /* normalised rows / attention rows in fp16    */
     LMArgPart *d_amax;
     int *d_rin;                 /* prefill rows of a chunk of R: tokens, positions, slots
-                                 * (R ints each, back to back), copied in one piece */
-    int *h_rin;                 /* their pinned host staging                        */
+                                 * (R ints each, back to back), copied in one piece;
+                                 * then R floats of loss terms (lm_prefill_loss)     */
+    int *h_rin;                 /* their pinned host staging (same layout)          */
     /* per-slot greedy state */
     int *d_tok, *d_pos, *d_hist, *d_slot_id;
     /* batch 1-4 chain: QKV, attention (fuse_qa >= 1), Wo (>= 2) and the FFN
@@ -377,8 +378,9 @@ static int alloc_rows(LMModel *m, int R)
         if ((st = dev_alloc((void **)&m->d_part, n * 4))) return st;
     }
     if ((st = dev_alloc((void **)&m->d_amax, r * m->cls_nblk * sizeof(LMArgPart)))) return st;
-    if ((st = dev_alloc((void **)&m->d_rin, 3 * r * 4))) return st;
-    if (hipHostMalloc((void **)&m->h_rin, 3 * r * 4, 0) != hipSuccess) {
+    /* tokens, positions and slots of a chunk's rows, then its rows' loss terms */
+    if ((st = dev_alloc((void **)&m->d_rin, 4 * r * 4))) return st;
+    if (hipHostMalloc((void **)&m->h_rin, 4 * r * 4, 0) != hipSuccess) {
         m->h_rin = NULL;
         return LM_ERR_OOM;
     }
@@ -1269,7 +1271,7 @@ static int run_rows(LMModel *m, int R, int S, int all)
 }
 
 static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, const int *tokens,
-                       int S, int logits_mode, float *logits)
+                       int S, int logits_mode, float *logits, float *loss)
 {
     const int V = m->V;
     unsigned char *seen = (unsigned char *)calloc((size_t)m->max_batch, 1);
@@ -1328,6 +1330,14 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
                     hipMemcpyAsync(logits + (size_t)i0 * S * V, m->d_logits, (size_t)R * V * 4,
                                    hipMemcpyDeviceToHost, m->stream) != hipSuccess)
                     rc = LM_ERR_HIP;
+                /* the chunk's loss terms, before the next chunk reuses d_logits */
+                if (rc == LM_OK && loss) {
+                    float *d_lp = (float *)(m->d_rin + 3 * (size_t)R);
+                    if (lmk_row_logprob(m->stream, m->d_logits, V, m->d_rin, S, R, d_lp) != hipSuccess ||
+                        hipMemcpyAsync(h + 3 * (size_t)R, d_lp, (size_t)R * 4, hipMemcpyDeviceToHost,
+                                       m->stream) != hipSuccess)
+                        rc = LM_ERR_HIP;
+                }
             } else {
                 rc = run_rows(m, R, S, 0);
                 /* gather the last row of each sequence into d_attn (same row width) */
@@ -1349,6 +1359,16 @@ static int run_prefill(LMModel *m, int nseq, const int *slots, const int *pos0, 
             m->fold_off = 1;
         }
         m->fold_off = 0;
+        if (rc == LM_OK && loss) {
+            /* mean over each sequence, summed in the reference's order
+             * (forward.h:174-183: loss -= log_prob; loss / (S-1)) */
+            const float *lp = (const float *)(h + 3 * (size_t)R);
+            for (int i = 0; i < n; i++) {
+                float acc = 0.f;
+                for (int t = 0; t < S - 1; t++) acc -= lp[(size_t)i * S + t];
+                loss[i0 + i] = acc / (S - 1);
+            }
+        }
     }
     /* after a failure, let the copy out of the staging buffer finish before
      * a later call refills it */
@@ -1360,7 +1380,21 @@ int lm_prefill(LMModel *m, int slot, int pos0, const int *tokens, int S, float *
 {
     if (!m || !tokens || S < 1) return LM_ERR_INVALID;
     if (slot < 0 || slot >= m->max_batch || pos0 < 0 || pos0 + S > m->max_seq) return LM_ERR_RANGE;
-    return run_prefill(m, 1, &slot, &pos0, tokens, S, LM_LOGITS_ALL, logits);
+    return run_prefill(m, 1, &slot, &pos0, tokens, S, LM_LOGITS_ALL, logits, NULL);
+}
+
+static int prefill_from_zero(LMModel *m, int nseq, const int *slots, const int *tokens, int S,
+                             int logits_mode, float *logits, float *loss)
+{
+    int *sl = (int *)malloc((size_t)nseq * 2 * sizeof(int));
+    if (!sl) return LM_ERR_OOM;
+    for (int i = 0; i < nseq; i++) {
+        sl[i] = slots ? slots[i] : i;
+        sl[nseq + i] = 0;
+    }
+    int rc = run_prefill(m, nseq, sl, sl + nseq, tokens, S, logits_mode, logits, loss);
+    free(sl);
+    return rc;
 }
 
 int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens, int S,
@@ -1369,15 +1403,18 @@ int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens, 
     if (!m || !tokens || nseq < 1 || S < 1 ||
         (logits_mode != LM_LOGITS_ALL && logits_mode != LM_LOGITS_LAST))
         return LM_ERR_INVALID;
-    int *sl = (int *)malloc((size_t)nseq * 2 * sizeof(int));
-    if (!sl) return LM_ERR_OOM;
-    for (int i = 0; i < nseq; i++) {
-        sl[i] = slots ? slots[i] : i;
-        sl[nseq + i] = 0;
+    return prefill_from_zero(m, nseq, slots, tokens, S, logits_mode, logits, NULL);
+}
+
+int lm_prefill_loss(LMModel *m, int nseq, const int *slots, const int *tokens, int S, float *logits,
+                    float *loss)
+{
+    if (!m || !tokens || !loss || nseq < 1 || S < 2) return LM_ERR_INVALID;
+    if (m->V % 4) {   /* the loss kernel reads each logit row as 16-byte groups */
+        fprintf(stderr, "stories_lm: lm_prefill_loss: vocab_size %d is not a multiple of 4\n", m->V);
+        return LM_ERR_UNSUPPORTED;
     }
-    int rc = run_prefill(m, nseq, sl, sl + nseq, tokens, S, logits_mode, logits);
-    free(sl);
-    return rc;
+    return prefill_from_zero(m, nseq, slots, tokens, S, LM_LOGITS_ALL, logits, loss);
 }
 
 int lm_read_logits(LMModel *m, int row0, int nrows, float *dst)

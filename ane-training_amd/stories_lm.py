@@ -249,6 +249,7 @@ def lib():
         "lm_forward_batch": (I, [P, ip, ip, I, fp, ip]),
         "lm_prefill": (I, [P, I, I, ip, I, fp]),
         "lm_prefill_batch": (I, [P, I, ip, ip, I, I, fp]),
+        "lm_prefill_loss": (I, [P, I, ip, ip, I, fp, fp]),
         "lm_read_logits": (I, [P, I, I, fp]),
         "lm_generate_greedy": (I, [P, I, ip, ip, I, ip]),
         "lm_sync": (I, [P]),
@@ -630,6 +631,22 @@ class Model:
                                     S, mode, _fp(logits) if logits is not None else None)
         self._check(rc, "lm_prefill_batch")
         return logits
+
+    def prefill_loss(self, tokens, slots=None, want_logits=False):
+        """Mean next-token cross-entropy of each sequence (tokens: nseq x S),
+        taken on the device (lm_prefill_loss); returns (loss[nseq], logits or
+        None)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        nseq, S = tokens.shape
+        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.int32).ravel()
+        if sl is not None and sl.size != nseq:
+            raise ValueError(f"prefill_loss: {sl.size} slots for {nseq} sequences")
+        logits = np.empty((nseq * S, self.vocab), dtype=np.float32) if want_logits else None
+        loss = np.empty(nseq, dtype=np.float32)
+        rc = lib().lm_prefill_loss(self._h, nseq, _ip(sl) if sl is not None else None, _ip(tokens), S,
+                                   _fp(logits) if logits is not None else None, _fp(loss))
+        self._check(rc, "lm_prefill_loss")
+        return loss, logits
 
     def read_logits(self, row0, nrows):
         out = np.empty((nrows, self.vocab), dtype=np.float32)

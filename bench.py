@@ -365,6 +365,9 @@ def bench_extra(S, w16_stories, reps_prefill=10, reps_decode=2, direct=False, on
         out["c3_forward_8x256"] = {"value": round(2048 / (ms * 1e-3), 1), "unit": "tok/s", "ms": round(ms, 4),
                                    "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                                    "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "flops": fl}
+        # the same forward with model_forward's loss taken on the device
+        ms_loss = _timed(m, lambda: m.prefill_loss(toks), reps_prefill)
+        out["c3_forward_8x256"]["with_loss_ms"] = round(ms_loss, 4)
         m.close()
     # C2: 64 sequences, 192-token prompts prefilled, then 64 greedy steps each
     if want("c2"):

@@ -209,6 +209,18 @@ int lm_prefill(LMModel *m, int slot, int pos0, const int *tokens, int S,
 int lm_prefill_batch(LMModel *m, int nseq, const int *slots, const int *tokens,
                      int S, int logits_mode, float *logits);
 
+/* model_forward with its loss (training/forward.h:104-184; train.m:64 is its
+ * caller): the causal forward of nseq sequences of S >= 2 tokens from position
+ * 0, as lm_prefill_batch with LM_LOGITS_ALL, and the mean next-token
+ * cross-entropy of each sequence, loss[i] = -(1/(S-1)) sum_{t<S-1}
+ * log softmax(logits[i, t])[tokens[i, t+1]].  The log-probabilities are taken
+ * on the device from the device logits, one fp32 value per row comes back, and
+ * the host sums them per sequence in the reference's order; `logits` (host,
+ * may be NULL) also receives all nseq*S rows.  loss: nseq floats.
+ * LM_ERR_UNSUPPORTED when vocab_size is not a multiple of 4. */
+int lm_prefill_loss(LMModel *m, int nseq, const int *slots, const int *tokens,
+                    int S, float *logits, float *loss);
+
 /* Copy rows [row0, row0+nrows) of the last forward's device logits to dst. */
 int lm_read_logits(LMModel *m, int row0, int nrows, float *dst);
 

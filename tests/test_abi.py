@@ -87,6 +87,7 @@ def test_null_arguments_rejected_before_device(lm):
     assert st.value == lm.LM_ERR_INVALID
     assert L.lm_forward_batch(None, None, None, 1, None, None) == lm.LM_ERR_INVALID
     assert L.lm_prefill(None, 0, 0, None, 1, None) == lm.LM_ERR_INVALID
+    assert L.lm_prefill_loss(None, 1, None, None, 2, None, None) == lm.LM_ERR_INVALID
     assert L.lm_generate_greedy(None, 1, None, None, 1, None) == lm.LM_ERR_INVALID
     assert not L.lm_forward(None, 0, 0)
     L.lm_free(None)
