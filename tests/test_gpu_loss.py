@@ -124,3 +124,29 @@ def test_stories_c3_loss(lm, orc):
     o.close()
     assert abs(float(loss[0]) - orc.loss(ref, toks[0])) < ORACLE_ATOL
     m.close()
+
+
+def test_prefill_loss_after_fold_overflow_redo(lm):
+    """A chunk whose folded norm overflows fp16 is redone with the row norm
+    apart; the loss terms are taken again from the redone logits, so the loss
+    equals, bit for bit, that of the same call with LM_OPT_PREFILL_FOLD 0 and
+    the reference loss loop over the returned logits."""
+    _say("[prefill loss after fold overflow]")
+    from test_gpu_batched import FOLD_WO
+    d = FOLD_WO
+    nseq, S, D, L, V = 3, d["seq_len"], d["dim"], d["n_layers"], d["vocab_size"]
+    cfg = lm.make_config(**d)
+    w16 = lm.synth_weights_f16(cfg, 53, 0.02, True)
+    emb = lm.f16_to_f32(w16[:V * D])
+    w16[:V * D] = lm.f32_to_f16(np.clip(emb * 5e5, -6e4, 6e4))
+    o = V * D + L * D + 4 * L * D * D        # rms_ffn after emb, rms_att, wq, wk, wv, wo (MHA)
+    w16[o:o + L * D] = lm.f32_to_f16(np.full(L * D, 8.0, np.float32))
+    m = lm.Model.create(cfg, w16, True, nseq, S)
+    toks = np.random.default_rng(53).integers(0, V, (nseq, S)).astype(np.int32)
+    la, ga = m.prefill_loss(toks, want_logits=True)
+    m.set_option(lm.LM_OPT_PREFILL_FOLD, 0)
+    lb, gb = m.prefill_loss(toks, want_logits=True)
+    m.close()
+    assert np.array_equal(ga, gb) and np.array_equal(la, lb)
+    for i in range(nseq):
+        np.testing.assert_allclose(la[i], lm.mean_ce(ga[i * S:(i + 1) * S], toks[i]), **SAME_LOGITS)
