@@ -13,17 +13,24 @@ to the device path are caught, and so GPU tests need no long CPU runs.
                    untied classifier): 256 greedy ids from token 1 at positions
                    0..255 with fp32 K/V and with binary16 K/V, and per step the
                    top-32 (logit, id) pairs plus logit sum / sum of squares.
+  stories_c2.npz   config C2 (Stories-110M, seed 1): each of the 64 x 192 uniform
+                   prompts (seed 102), fp32 K/V (the reference forward): the
+                   prompt's last-row logits, then 64 greedy decode steps at
+                   positions 192..255; per row the same digest as C4's (top-32
+                   pairs, 64 fixed sampled columns, sum, sum of squares) and the
+                   65 greedy ids.
   scaled_c4.npz    config C4 (the scaled Llama-2 model: dim 2048, 16 layers, 16
-                   heads of 128, SwiGLU 5632, vocab 32000, seed 4): prompts 0
-                   and 31 of the 32 x 512 uniform prompts (seed 104), fp32 K/V
-                   (the reference forward): the prompt's last-row logits, then
-                   128 greedy decode steps at positions 512..639; per row the
-                   top-32 (logit, id) pairs, 256 fixed sampled columns, sum and
-                   sum of squares, and the 129 greedy ids; and the same digest of
-                   the prompt's last-row logits of all 32 sequences (*_prompts).
+                   heads of 128, SwiGLU 5632, vocab 32000, seed 4): each of the
+                   32 x 512 uniform prompts (seed 104), fp32 K/V (the reference
+                   forward): the prompt's last-row logits, then 128 greedy
+                   decode steps at positions 512..639; per row the top-32
+                   (logit, id) pairs, 64 fixed sampled columns, sum and sum of
+                   squares, and the 129 greedy ids; the prompt rows' digests
+                   also gathered as *_prompts.
 
-Run:  python tests/golden/make_fixtures.py [name ...]   (names: tiny, c0, c4;
-      about a minute for tiny + c0 and about ten minutes for c4 on 8 cores)
+Run:  python tests/golden/make_fixtures.py [name ...]   (names: tiny, c0, c2, c4;
+      about a minute for tiny + c0, a few minutes for c2 and about twenty-five
+      minutes for c4 on 8 cores)
 """
 import os
 import sys
@@ -76,8 +83,8 @@ def stories_c0():
 
 SCALED = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
               seq_len=640)
-C4_SEQS = (0, 31)
-NCOLS = 256
+C4_SEQS = tuple(range(32))
+NCOLS = 64
 
 
 def row_digest(lg, cols):
@@ -87,6 +94,34 @@ def row_digest(lg, cols):
     return dict(top_idx=idx, top_val=np.take_along_axis(lg, idx, axis=1).astype(np.float32),
                 cols_val=lg[:, cols].astype(np.float32), sum=lg.astype(np.float64).sum(1),
                 sumsq=(lg.astype(np.float64) ** 2).sum(1))
+
+
+C2_B, C2_P, C2_T = 64, 192, 64
+
+
+def stories_c2():
+    import time
+    cfg = S.make_config(**S.STORIES_110M)
+    w32 = S.f16_to_f32(S.synth_weights_f16(cfg, 1, 0.02, True))
+    prompts = np.random.default_rng(102).integers(0, 32000, (C2_B, C2_P)).astype(np.int32)
+    cols = np.sort(np.random.default_rng(2020).choice(32000, NCOLS, replace=False)).astype(np.int32)
+    out = dict(seed=np.int64(1), prompt_seed=np.int64(102), seqs=np.arange(C2_B, dtype=np.int32), cols=cols,
+               n_steps=np.int32(C2_T))
+    t0 = time.time()
+    for b in range(C2_B):
+        o = O.Oracle(cfg7(S.STORIES_110M), w32, True, 256)
+        rows = [o.forward_cached(prompts[b], 0, last_only=True)]
+        ids = [O.argmax(rows[0])]
+        for s in range(C2_T):
+            rows.append(o.decode_step(ids[-1], C2_P + s))
+            ids.append(O.argmax(rows[-1]))
+        o.close()
+        for k, v in row_digest(np.stack(rows), cols).items():
+            out[f"{k}_{b}"] = v
+        out[f"ids_{b}"] = np.array(ids, np.int32)
+    print(f"c2: {C2_B} sequences in {time.time() - t0:.1f} s", flush=True)
+    np.savez_compressed(os.path.join(HERE, "stories_c2.npz"), **out)
+    print("wrote stories_c2")
 
 
 def scaled_c4():
@@ -111,25 +146,22 @@ def scaled_c4():
             out[f"{k}_{b}"] = v
         out[f"ids_{b}"] = np.array(ids, np.int32)
         print(f"c4 sequence {b}: {time.time() - t0:.1f} s", flush=True)
-    rows = []
-    for b in range(32):
-        o = O.Oracle(cfg7(SCALED), w32, True, 640)
-        rows.append(o.forward_cached(prompts[b], 0, last_only=True))
-        o.close()
-    for k, v in row_digest(np.stack(rows), cols).items():
-        out[f"{k}_prompts"] = v
-    print("c4 prompt rows of every sequence", flush=True)
+    # the prompt rows (row 0 of each sequence's digest), gathered
+    for k in ("top_idx", "top_val", "cols_val", "sum", "sumsq"):
+        out[f"{k}_prompts"] = np.stack([out[f"{k}_{b}"][0] for b in C4_SEQS])
     np.savez_compressed(os.path.join(HERE, "scaled_c4.npz"), **out)
     print("wrote scaled_c4")
 
 
 if __name__ == "__main__":
-    which = set(sys.argv[1:]) or {"tiny", "c0", "c4"}
+    which = set(sys.argv[1:]) or {"tiny", "c0", "c2", "c4"}
     if "tiny" in which:
         tiny("mha", TINY, 11)
         tiny("gqa", TINY_GQA, 12)
         tiny("hd128", TINY_HD128, 13)
     if "c0" in which:
         stories_c0()
+    if "c2" in which:
+        stories_c2()
     if "c4" in which:
         scaled_c4()

@@ -112,3 +112,46 @@ def test_oracle_reproduces_stories_c0_fixture(lm, orc):
     ids, lg = o.greedy(1, 0, 256, want_logits=True)
     assert np.array_equal(ids, fx["ids_kv32"])
     assert np.array_equal(np.take_along_axis(lg, fx["top_idx_kv32"], 1), fx["top_val_kv32"])
+
+
+def _fixture_sequence(orc, d, w, prompt, n_steps, max_seq):
+    """The oracle's prompt last-row logits and greedy decode rows, as the
+    C2/C4 fixtures were made (tests/golden/make_fixtures.py)."""
+    o = orc.Oracle(cfg7(d), w, True, max_seq)
+    rows = [o.forward_cached(prompt, 0, last_only=True)]
+    ids = [orc.argmax(rows[0])]
+    for s in range(n_steps):
+        rows.append(o.decode_step(ids[-1], len(prompt) + s))
+        ids.append(orc.argmax(rows[-1]))
+    o.close()
+    return np.stack(rows), np.array(ids, np.int32)
+
+
+def test_oracle_reproduces_stories_c2_fixture(lm, orc):
+    """One sequence of the C2 fixture (chosen from the middle): the greedy ids,
+    the top-32 values and the sampled columns, bit for bit."""
+    fx = np.load(os.path.join(GOLDEN, "stories_c2.npz"))
+    d = lm.STORIES_110M
+    w = lm.f16_to_f32(lm.synth_weights_f16(lm.make_config(**d), int(fx["seed"]), 0.02, True))
+    prompts = np.random.default_rng(int(fx["prompt_seed"])).integers(0, 32000, (64, 192)).astype(np.int32)
+    b = 37
+    rows, ids = _fixture_sequence(orc, d, w, prompts[b], int(fx["n_steps"]), 256)
+    assert np.array_equal(ids, fx[f"ids_{b}"])
+    assert np.array_equal(np.take_along_axis(rows, fx[f"top_idx_{b}"], 1), fx[f"top_val_{b}"])
+    assert np.array_equal(rows[:, fx["cols"]], fx[f"cols_val_{b}"])
+
+
+@pytest.mark.slow
+def test_oracle_reproduces_scaled_c4_fixture(lm, orc):
+    """One sequence of the C4 fixture (the dim-2048 model): ids, top-32 values
+    and sampled columns, bit for bit (about a minute of oracle time)."""
+    fx = np.load(os.path.join(GOLDEN, "scaled_c4.npz"))
+    d = dict(dim=2048, hidden_dim=5632, n_layers=16, n_heads=16, n_kv_heads=16, vocab_size=32000,
+             seq_len=640)
+    w = lm.f16_to_f32(lm.synth_weights_f16(lm.make_config(**d), int(fx["seed"]), 0.02, True))
+    prompts = np.random.default_rng(int(fx["prompt_seed"])).integers(0, 32000, (32, 512)).astype(np.int32)
+    b = 13
+    rows, ids = _fixture_sequence(orc, d, w, prompts[b], int(fx["n_steps"]), 640)
+    assert np.array_equal(ids, fx[f"ids_{b}"])
+    assert np.array_equal(np.take_along_axis(rows, fx[f"top_idx_{b}"], 1), fx[f"top_val_{b}"])
+    assert np.array_equal(rows[:, fx["cols"]], fx[f"cols_val_{b}"])
