@@ -31,6 +31,43 @@ def drand48() -> float:
     return _libc.drand48()
 
 
+# POSIX drand48: X' = (a X + c) mod 2^48; srand48(s) sets X = (s mod 2^32) << 16 | 0x330E;
+# each drand48() steps X and returns X / 2^48 (exact in a double)
+_A48, _C48, _M48 = 0x5DEECE66D, 0xB, (1 << 48) - 1
+
+
+def _mulmod48(a: int, x: np.ndarray) -> np.ndarray:
+    """(a * x) mod 2^48 for a 48-bit constant a and uint64 x < 2^48, in
+    24-bit halves so that no product leaves 64 bits."""
+    lo24 = np.uint64((1 << 24) - 1)
+    al, ah = np.uint64(a & ((1 << 24) - 1)), np.uint64(a >> 24)
+    xl, xh = x & lo24, x >> np.uint64(24)
+    mid = (ah * xl + al * xh) & lo24
+    return (al * xl + (mid << np.uint64(24))) & np.uint64(_M48)
+
+
+def drand48_stream(seed: int, n: int) -> np.ndarray:
+    """The first n values drand48() returns after srand48(seed), as float64:
+    the first L states sequentially, then every lane advanced L states at a
+    time by the L-fold composition of the step, (a^L, c (a^(L-1) + ... + 1))
+    mod 2^48.  tests/test_text.py holds it to the C library's own drand48."""
+    L = max(1, min(n, 1 << 16))
+    x = ((int(seed) & 0xFFFFFFFF) << 16) | 0x330E
+    lane = np.empty(L, np.uint64)
+    for i in range(L):
+        x = (_A48 * x + _C48) & _M48
+        lane[i] = x
+    aL, cL = 1, 0
+    for _ in range(L):
+        aL, cL = (_A48 * aL) & _M48, (_A48 * cL + _C48) & _M48
+    out = np.empty(n, np.uint64)
+    out[:min(L, n)] = lane[:n]
+    for k in range(L, n, L):
+        lane = (_mulmod48(aL, lane) + np.uint64(cL)) & np.uint64(_M48)
+        out[k:k + L] = lane[:n - k]
+    return out.astype(np.float64) * 2.0 ** -48
+
+
 def softmax_t(logits, temp):
     """probs[i] = expf((logits[i] - maxv) / temp) / sum (generate.m:140-148)."""
     lg = np.asarray(logits, np.float32)

@@ -72,6 +72,26 @@ def test_rng_matches_libc_drand48():
             assert r.next() == libc.drand48()
 
 
+def test_vectorised_drand48_stream_matches_libc():
+    """tests/ref_samplers.drand48_stream (the inputs of the reference's
+    classifier probe) against libc's drand48, draw for draw over the first
+    lanes, across the first lane jump, and at spot checks deep in the stream."""
+    import ref_samplers as R
+    libc = ctypes.CDLL("libc.so.6")
+    libc.drand48.restype = ctypes.c_double
+    libc.srand48.argtypes = [ctypes.c_long]
+    for seed in (123, 42, 0xDEADBEEF, (1 << 40) + 7):
+        n = 70000 if seed == 123 else 3000
+        got = R.drand48_stream(seed, n)
+        libc.srand48(seed)
+        want = np.array([libc.drand48() for _ in range(n)])
+        assert np.array_equal(got, want), seed
+    far = R.drand48_stream(123, 400000)
+    libc.srand48(123)
+    want = np.array([libc.drand48() for _ in range(400000)])
+    assert np.array_equal(far, want)
+
+
 @pytest.fixture
 def small_vocab(tmp_path):
     # single bytes (including a duplicate of 'a'), merges with ties and
