@@ -266,6 +266,9 @@ __device__ __forceinline__ void epilogue_tile(const f32x16 &acc, int m0, int n0,
 /* ---- tiled GEMM (prefill) ------------------------------------------------- */
 
 #define BKH 64                 /* K (halves) per LDS stage: one 128-byte row per tile row */
+#ifndef LMK_GATE_KS
+#define LMK_GATE_KS 2          /* wave groups splitting K in a decode-row gate tile */
+#endif
 #ifndef DEC_RING
 #define DEC_RING 4             /* LDS ring depth of decode-row (M <= 64) tiles (measured: 4 beats 3, 6 and 8) */
 #endif
@@ -363,11 +366,11 @@ __device__ __forceinline__ void lds_wait_regs(u32x4 (&v)[6])
  * BN/2 gates, then written with one 16-byte store per 8 gates instead of one
  * 2-byte store per gate.  sg: LDS of at least BM * (BN/2 + 8) halves, no longer
  * read by any wave's main loop. */
-template <int BM, int BN, int TM, int TN, int WVM, int WVN>
+template <int BM, int BN, int TM, int TN, int WVM, int WVN, int KG = 1>
 __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *sg, int m0, int n0,
-                                              int wm, int wn, const EpiArgs &e)
+                                              int wm, int wn, const EpiArgs &e, bool own = true)
 {
-    constexpr int NT = 64 * WVM * WVN;   /* threads: WVM x WVN waves */
+    constexpr int NT = 64 * WVM * WVN * KG;   /* threads: KG groups of WVM x WVN waves */
     constexpr int GW = BN / 2, GLD = GW + 8;
     const int lane = threadIdx.x & 63, c = lane & 31;
     const bool lo = c < 16;
@@ -376,6 +379,7 @@ __device__ __forceinline__ void gate_tile_lds(const f32x16 (&acc)[TM][TN], u16 *
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
+            if (!own) continue;   /* another K group's wave: the tile is group 0's */
             const int rl = wm * (BM / WVM) + i * 32 + 4 * (lane >> 5);
             const int gl = (wn * (BN / WVN) + j * 32) / 2 + (c & 15);
 #pragma unroll
@@ -517,12 +521,13 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
     }
 }
 
-template <int BM, int BN, int E, int NS, int WVM, bool RS = false, int WVN = 2>
-__global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restrict__ A, int lda,
+template <int BM, int BN, int E, int NS, int WVM, bool RS = false, int WVN = 2, int KG = 1>
+__global__ void __launch_bounds__(64 * WVM * WVN * KG) k_gemm_tile(const u16 *__restrict__ A, int lda,
                                                          const u16 *__restrict__ W, int K, int kc,
                                                          EpiArgs e, int tm, int tn)
 {
-    constexpr int NWV = WVM * WVN;                /* waves: WVM along M x WVN along N */
+    constexpr int NWV = WVM * WVN;                /* waves: WVM along M x WVN along N, */
+                                                  /* in each of KG groups along K        */
     constexpr int WM = BM / WVM, WN = BN / WVN;   /* wave tile */
     constexpr int TM = WM / 32, TN = WN / 32;   /* MFMA tiles per wave */
     constexpr int ROWS = BM + BN;               /* tile rows per stage */
@@ -533,10 +538,11 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
     static_assert((WVM == 2 && WVN == 2) || E != EPI_QKV, "wave layout");
     static_assert(WVN == 1 || WVN == 2, "one or two waves along N");
     static_assert(NS >= 3 && NS <= 8 && LDW * (NS - 2) <= 63, "ring depth (vmcnt holds 63)");
+    static_assert(KG == 1 || ((E == EPI_GATE || E == EPI_STORE) && !RS), "K groups: gate or store epilogue");
     /* the NS stage buffers are separate arrays (not one indexed ring) so that
      * the compiler can tell a stage's LDS reads from the direct loads in flight
      * into the others and does not wait for those loads */
-#define RING_BUF(i) __shared__ __attribute__((aligned(NS > i ? 1024 : 16))) u16 lds##i[NS > i ? STAGE : 8]
+#define RING_BUF(i) __shared__ __attribute__((aligned(NS > i ? 1024 : 16))) u16 lds##i[NS > i ? KG * STAGE : 8]
     RING_BUF(0); RING_BUF(1); RING_BUF(2); RING_BUF(3);
     RING_BUF(4); RING_BUF(5); RING_BUF(6); RING_BUF(7);
 #undef RING_BUF
@@ -553,7 +559,12 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
     };
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* wave within its K group, and the group (KG > 1: group kg takes the
+     * kg-th of KG equal K chunks through its own stage buffers) */
+    const int wall = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = KG > 1 ? wall / NWV : 0;
+    const int wave = KG > 1 ? wall % NWV : wall;
+    auto gbuf = [&](auto I) -> u16 * { return ring(I) + (KG > 1 ? kg * STAGE : 0); };
     const int wm = WVN == 2 ? wave >> 1 : wave, wn = WVN == 2 ? wave & 1 : 0;
     /* XCD-aware tile order: work-group id goes to XCD id % 8; give each XCD a
      * contiguous run of tiles (M fastest), i.e. a slice of N, so the W rows of
@@ -565,7 +576,7 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
 
     /* per-lane source rows of this wave's load instructions (fixed over k);
      * work-group split y takes k = y*kc .. y*kc + kc - 1 (kc = K unsplit) */
-    const int k0 = blockIdx.y * kc;
+    const int k0 = blockIdx.y * kc + kg * (kc / KG);
     const u16 *src[LDW];
 #pragma unroll
     for (int i = 0; i < LDW; i++) {
@@ -648,7 +659,7 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
      * barrier (a fenced __syncthreads would wait for every outstanding load) so
      * all waves' loads of stage kt have landed and stage kt-1's buffer is free
      * for stage kt+NS-1 */
-    const int nk = kc / BKH;
+    const int nk = kc / KG / BKH;
     auto wait_stage = [&](int kt) {
         const int later = min(NS - 2, nk - 1 - kt);   /* stages issued after kt */
         static_for<0, NS - 1>([&](auto J) {
@@ -711,9 +722,9 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    issue(lds0, 0);
+    issue(gbuf(std::integral_constant<int, 0>{}), 0);
     static_for<1, NS - 1>([&](auto I) {
-        if (decltype(I)::value < nk) issue(ring(I), decltype(I)::value);
+        if (decltype(I)::value < nk) issue(gbuf(I), decltype(I)::value);
     });
     if constexpr (RS) {
         __builtin_amdgcn_sched_barrier(0);
@@ -730,8 +741,8 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
         static_for<0, NS>([&](auto I) {
             constexpr int i = decltype(I)::value;
             if (kt + i < nk)
-                step(kt + i, ring(std::integral_constant<int, i>{}),
-                     ring(std::integral_constant<int, i + NS - 1>{}));
+                step(kt + i, gbuf(std::integral_constant<int, i>{}),
+                     gbuf(std::integral_constant<int, i + NS - 1>{}));
         });
     }
     if constexpr (RS) {   /* the product rows scaled by their row's scale */
@@ -744,12 +755,41 @@ __global__ void __launch_bounds__(64 * WVM * WVN) k_gemm_tile(const u16 *__restr
                 for (int k = 0; k < 16; k++)
                     acc[i][j][k] *= rs_sh[wm * WM + i * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3)];
     }
+    if constexpr (KG > 1) {
+        /* the K groups' partial tiles summed in group 0, in group order: groups
+         * 1.. store theirs to LDS (lane fastest), group 0 adds them */
+        static_assert((KG - 1) * NWV * TM * TN * 16 * 64 * 4 <= KG * STAGE * 2, "partials fit lds0");
+        float *red = (float *)lds0;
+        __syncthreads();   /* every group's last LDS reads are done */
+        if (kg > 0) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int k = 0; k < 16; k++)
+                        red[((((kg - 1) * NWV + wave) * TM + i) * TN * 16 + j * 16 + k) * 64 + lane] = acc[i][j][k];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int q = 1; q < KG; q++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int k = 0; k < 16; k++)
+                            acc[i][j][k] += red[((((q - 1) * NWV + wave) * TM + i) * TN * 16 + j * 16 + k) * 64 + lane];
+        }
+    }
     if (E == EPI_STORE) e.out += blockIdx.y * e.sstride;   /* this split's partial */
     if constexpr (E == EPI_GATE) {
         static_assert(BM * (BN / 2 + 8) <= STAGE, "gate staging fits one stage buffer");
-        gate_tile_lds<BM, BN, TM, TN, WVM, WVN>(acc, lds0, m0, n0, wm, wn, e);
+        gate_tile_lds<BM, BN, TM, TN, WVM, WVN, KG>(acc, lds0, m0, n0, wm, wn, e, kg == 0);
         return;
     }
+    if (KG > 1 && kg > 0) return;   /* (no barrier below for the store epilogue) */
     if constexpr (QKV_LDS) {
         qkv_tile_lds<BM, BN, TM, TN, QNI>(acc, (float *)lds0, (float *)lds1, m0, n0, wm, wn, e,
                                           TM == 1 ? &qpre : nullptr);
@@ -1047,6 +1087,15 @@ static constexpr int ring_depth(bool rows64, bool gate = false)
     return BM <= 64 && rows64 ? ((gate ? want : DEC_RING) < fit ? (gate ? want : DEC_RING) : fit) : 3;
 }
 
+/* Ring depth of a tile whose K is walked by G wave groups, each with its own
+ * stage buffers: at most 6 stages, as many as the LDS holds for G rings. */
+template <int BM, int BN, int G>
+static constexpr int ks_ring()
+{
+    constexpr int fit = 160 * 1024 / (G * (BM + BN) * 128);
+    return fit < 6 ? fit : 6;
+}
+
 template <int BM, int BN, int E, bool RS = false>
 static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                         int K, const EpiArgs &e)
@@ -1055,12 +1104,22 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
     if constexpr (BM == 256 && E != EPI_QKV) {   /* eight waves (4 x 2): two per SIMD */
         hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 4, RS>), dim3(tm * tn), dim3(512), 0, s, (const u16 *)A,
                            lda, (const u16 *)W, K, K, e, tm, tn);
-    } else if constexpr (BM == 32 && BN == 32) {   /* one wave */
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS, 1>),
-                           dim3(tm * tn), dim3(64), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
-    } else if constexpr (BM == 32) {               /* two waves (1 x 2) over 32 rows */
-        hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS>), dim3(tm * tn),
-                           dim3(128), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+    } else if constexpr (BM == 32 && BN == 32) {   /* one wave (per K group) */
+        constexpr int G = E == EPI_GATE && !RS ? LMK_GATE_KS : 1;
+        if (G > 1 && K % (G * BKH) == 0)
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ks_ring<BM, BN, G>(), 1, RS, 1, G>),
+                               dim3(tm * tn), dim3(64 * G), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+        else
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS, 1>),
+                               dim3(tm * tn), dim3(64), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+    } else if constexpr (BM == 32) {               /* two waves (1 x 2) over 32 rows (per K group) */
+        constexpr int G = E == EPI_GATE && !RS ? LMK_GATE_KS : 1;
+        if (G > 1 && K % (G * BKH) == 0)
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ks_ring<BM, BN, G>(), 1, RS, 2, G>), dim3(tm * tn),
+                               dim3(128 * G), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+        else
+            hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true, E == EPI_GATE), 1, RS>), dim3(tm * tn),
+                               dim3(128), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
     } else {
         if (M <= 64 && BM == 64)
             hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2, RS>), dim3(tm * tn),
@@ -1108,8 +1167,13 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * without a work-group takes 32 x 32 tiles of one wave instead (twice the
  * work-groups; each 32-column tile is 16 W1 rows and their 16 W3 partners):
  * C2 0.4618-0.4627 -> 0.4580-0.4583 ms/step, while the scaled model's 176
- * gate tiles of 32 rows lost 1.6% as 352 one-wave tiles.  K is a multiple of
- * the 64-wide stage. */
+ * gate tiles of 32 rows lost 1.6% as 352 one-wave tiles.  The decode-row gate
+ * tiles (32 x 32 and 32 x 64) walk K in LMK_GATE_KS wave groups, each with its
+ * own ring over a contiguous K chunk, their partial tiles summed in LDS before
+ * the gate epilogue (the gate cannot be split over work-groups): two groups
+ * took C2 0.442-0.444 -> 0.437-0.438 ms/step and C4 1.142-1.143 -> 1.137-1.138
+ * (same box, two alternating runs each); four were 0.3% faster again at C2 and
+ * 1% slower at C4.  K is a multiple of the 64-wide stage. */
 template <int E, bool RS = false>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
