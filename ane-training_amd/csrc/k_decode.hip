@@ -1322,14 +1322,18 @@ __global__ void __launch_bounds__(WG) k_cls(
     __shared__ int bis[NB][NWAVE];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
     const int row0 = blockIdx.x * CLS_ROWS_PER_WG + wv * 2 * CLS_PAIRS_PER_WAVE;
+    /* x and the gain first: the norm's sums and barrier then run while the
+     * weight rows are still arriving */
+    NormIn<D, NB> in;
+    norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
+    __builtin_amdgcn_sched_barrier(0);
     uint4 wr[CLS_PAIRS_PER_WAVE][D / 256];
 #pragma unroll
     for (int pp = 0; pp < CLS_PAIRS_PER_WAVE; pp++) {
         const int rl = min(row0 + 2 * pp + half, V - 1);
         hw_load<D>(W + (size_t)rl * D, hl, wr[pp]);
     }
-    NormIn<D, NB> in;
-    norm_load<D, NB>(x, nullptr, nullptr, rms_w, B, in);
+    __builtin_amdgcn_sched_barrier(0);
     float scale[NB];
     norm_to_lds_unscaled<D, NB>(in, B, nullptr, false, xs, scale);
     float bv[NB];
