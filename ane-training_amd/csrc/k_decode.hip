@@ -1233,7 +1233,9 @@ __global__ void __launch_bounds__(WG) k_w2_residual(
 
 /* ---- classifier + argmax ----------------------------------------------------- */
 
+#ifndef CLS_PAIRS_PER_WAVE
 #define CLS_PAIRS_PER_WAVE 4
+#endif
 #define CLS_ROWS_PER_WG (2 * CLS_PAIRS_PER_WAVE * NWAVE)
 
 /* The argmax reduction inside the classifier launch (k_cls with fold.tw): the
