@@ -1124,7 +1124,12 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
         if (M <= 64 && BM == 64)
             hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2, RS>), dim3(tm * tn),
                                dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
-        else
+        else if (E == EPI_GATE && !RS && BM == 64 && BN == 64 && K % (2 * BKH) == 0) {
+            /* prefill-row gate: K in two wave groups (eight waves, two per SIMD) */
+            if constexpr (E == EPI_GATE && !RS && BM == 64 && BN == 64)
+                hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2, false, 2, 2>), dim3(tm * tn), dim3(2 * GT), 0, s,
+                                   (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
+        } else
             hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2, RS>), dim3(tm * tn), dim3(GT), 0, s, (const u16 *)A,
                                lda, (const u16 *)W, K, K, e, tm, tn);
     }
@@ -1173,7 +1178,10 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * the gate epilogue (the gate cannot be split over work-groups): two groups
  * took C2 0.442-0.444 -> 0.437-0.438 ms/step and C4 1.142-1.143 -> 1.137-1.138
  * (same box, two alternating runs each); four were 0.3% faster again at C2 and
- * 1% slower at C4.  K is a multiple of the 64-wide stage. */
+ * 1% slower at C4.  The 64 x 64 gate tiles of prefill rows (not row-scaled)
+ * take two K groups as well, eight waves, two per SIMD: C1 0.474-0.489 ->
+ * 0.467-0.479 ms; the K-split Wo and W2 of those rows in two groups as well
+ * gave part of it back (0.470-0.482).  K is a multiple of the 64-wide stage. */
 template <int E, bool RS = false>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
