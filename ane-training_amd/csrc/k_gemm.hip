@@ -459,7 +459,7 @@ __device__ __forceinline__ void qkv_item_rope(QkvItem (&it)[NI], int n0, const E
 template <int BM, int BN, int TM, int TN, int NI>
 __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float *b0, float *b1,
                                              int m0, int n0, int wm, int wn, const EpiArgs &e,
-                                             const QkvItem (*pre)[NI])
+                                             const QkvItem (*pre)[NI], bool own = true)
 {
     constexpr int WM = BM / 2, WN = BN / 2, C4 = BN / 4;
     static_assert(NI * GT == 64 * C4, "items per thread");
@@ -468,25 +468,29 @@ __device__ __forceinline__ void qkv_tile_lds(const f32x16 (&acc)[TM][TN], float 
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         float *buf = (i & 1) ? b1 : b0;
-        /* buf row wm*32 + r holds tile row m0 + wm*WM + i*32 + r */
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const int r = wm * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
-                buf[r * BN + wn * WN + j * 32 + (lane & 31)] = acc[i][j][k];
-            }
+        /* buf row wm*32 + r holds tile row m0 + wm*WM + i*32 + r; the waves
+         * of other K groups (own false) only keep the barriers */
         QkvItem its[NI];
-        if (i == 0 && pre) {
+        if (own) {
 #pragma unroll
-            for (int k = 0; k < NI; k++) its[k] = (*pre)[k];
-        } else {
-            qkv_item_rows<BM, BN, NI>(its, i, m0, e);
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    const int r = wm * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
+                    buf[r * BN + wn * WN + j * 32 + (lane & 31)] = acc[i][j][k];
+                }
+            if (i == 0 && pre) {
+#pragma unroll
+                for (int k = 0; k < NI; k++) its[k] = (*pre)[k];
+            } else {
+                qkv_item_rows<BM, BN, NI>(its, i, m0, e);
+            }
+            qkv_item_rope<BN, NI>(its, n0, e);
         }
-        qkv_item_rope<BN, NI>(its, n0, e);
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < NI; k++) {
+            if (!own) break;
             const int idx = threadIdx.x + k * GT, r = idx / C4, c4 = idx % C4;
             const int row = m0 + (r >> 5) * WM + i * 32 + (r & 31);
             const int n = n0 + 4 * c4;
@@ -538,7 +542,8 @@ __global__ void __launch_bounds__(64 * WVM * WVN * KG) k_gemm_tile(const u16 *__
     static_assert((WVM == 2 && WVN == 2) || E != EPI_QKV, "wave layout");
     static_assert(WVN == 1 || WVN == 2, "one or two waves along N");
     static_assert(NS >= 3 && NS <= 8 && LDW * (NS - 2) <= 63, "ring depth (vmcnt holds 63)");
-    static_assert(KG == 1 || ((E == EPI_GATE || E == EPI_STORE) && !RS), "K groups: gate or store epilogue");
+    static_assert(KG == 1 || ((E == EPI_GATE || E == EPI_STORE || E == EPI_QKV) && !RS),
+                  "K groups: gate, store or QKV epilogue");
     /* the NS stage buffers are separate arrays (not one indexed ring) so that
      * the compiler can tell a stage's LDS reads from the direct loads in flight
      * into the others and does not wait for those loads */
@@ -680,6 +685,7 @@ __global__ void __launch_bounds__(64 * WVM * WVN * KG) k_gemm_tile(const u16 *__
     if constexpr (QKV_LDS && TM == 1) {
 #pragma unroll
         for (int k = 0; k < QNI; k++) {
+            if (KG > 1 && kg > 0) break;
             const int r = (threadIdx.x + k * GT) / (BN / 4);
             const int row = min(m0 + (r >> 5) * WM + (r & 31), M - 1);
             qpre[k].p = e.pos[row];
@@ -789,12 +795,12 @@ __global__ void __launch_bounds__(64 * WVM * WVN * KG) k_gemm_tile(const u16 *__
         gate_tile_lds<BM, BN, TM, TN, WVM, WVN, KG>(acc, lds0, m0, n0, wm, wn, e, kg == 0);
         return;
     }
-    if (KG > 1 && kg > 0) return;   /* (no barrier below for the store epilogue) */
     if constexpr (QKV_LDS) {
         qkv_tile_lds<BM, BN, TM, TN, QNI>(acc, (float *)lds0, (float *)lds1, m0, n0, wm, wn, e,
-                                          TM == 1 ? &qpre : nullptr);
+                                          TM == 1 ? &qpre : nullptr, kg == 0);
         return;
     }
+    if (KG > 1 && kg > 0) return;   /* (no barrier below for the store epilogue) */
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1124,9 +1130,11 @@ static void launch_tile(hipStream_t s, const uint16_t *A, int lda, const uint16_
         if (M <= 64 && BM == 64)
             hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, ring_depth<BM, BN>(true), 2, RS>), dim3(tm * tn),
                                dim3(GT), 0, s, (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
-        else if (E == EPI_GATE && !RS && BM == 64 && BN == 64 && K % (2 * BKH) == 0) {
-            /* prefill-row gate: K in two wave groups (eight waves, two per SIMD) */
-            if constexpr (E == EPI_GATE && !RS && BM == 64 && BN == 64)
+        else if ((E == EPI_GATE || E == EPI_QKV) && !RS && BM == 64 && BN == 64 && tm * tn <= 256 &&
+                 K % (2 * BKH) == 0) {
+            /* prefill-row gate or QKV, one round of tiles: K in two wave
+             * groups (eight waves, two per SIMD) */
+            if constexpr ((E == EPI_GATE || E == EPI_QKV) && !RS && BM == 64 && BN == 64)
                 hipLaunchKernelGGL((k_gemm_tile<BM, BN, E, 3, 2, false, 2, 2>), dim3(tm * tn), dim3(2 * GT), 0, s,
                                    (const u16 *)A, lda, (const u16 *)W, K, K, e, tm, tn);
         } else
@@ -1178,10 +1186,12 @@ static void launch_tile_split(hipStream_t s, const uint16_t *A, int lda, const u
  * the gate epilogue (the gate cannot be split over work-groups): two groups
  * took C2 0.442-0.444 -> 0.437-0.438 ms/step and C4 1.142-1.143 -> 1.137-1.138
  * (same box, two alternating runs each); four were 0.3% faster again at C2 and
- * 1% slower at C4.  The 64 x 64 gate tiles of prefill rows (not row-scaled)
- * take two K groups as well, eight waves, two per SIMD: C1 0.474-0.489 ->
- * 0.467-0.479 ms; the K-split Wo and W2 of those rows in two groups as well
- * gave part of it back (0.470-0.482).  K is a multiple of the 64-wide stage. */
+ * 1% slower at C4.  The 64 x 64 gate and QKV tiles of prefill rows (not
+ * row-scaled), when they fit one round (at most 256 tiles), take two K groups
+ * as well, eight waves, two per SIMD: C1 0.474-0.489 -> 0.467-0.479 ms with
+ * the gate, -> 0.461-0.468 with both; the K-split Wo and W2 of those rows in
+ * two groups as well gave part of it back.  K is a multiple of the 64-wide
+ * stage. */
 template <int E, bool RS = false>
 static int launch_gemm(hipStream_t s, const uint16_t *A, int lda, const uint16_t *W, int M, int N,
                        int K, const EpiArgs &e)
