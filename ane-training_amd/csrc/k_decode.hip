@@ -696,8 +696,10 @@ __device__ __forceinline__ void attn_head(
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 8; j++) qf[j] = sqkv[0][dq * 8 + j];
-        /* the current position's score, its k rounded as the cache would */
-        if (wv == 0) {
+        /* the current position's score, its k rounded as the cache would, by
+         * the last wave (tiles go to the waves in turn, so it has the fewest);
+         * it is read only at the merge, after the barrier */
+        if (wv == NWAVE - 1) {
             float d = 0.f;
 #pragma unroll
             for (int j = lane; j < HD; j += 64) d = fmaf(sqkv[0][j], kv_round<KT>(sqkv[1][j]), d);
