@@ -50,11 +50,15 @@ def test_gemm_split_partials(lm, M, N, K, nsplit):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 4096, 768), (7, 4096, 768), (32, 11264, 2048), (1, 512, 512),
-                                   (256, 4096, 768), (2048, 4096, 768), (130, 1024, 1024), (33, 2048, 256)])
+                                   (256, 4096, 768), (2048, 4096, 768), (130, 1024, 1024), (33, 2048, 256),
+                                   (64, 1024, 192), (20, 512, 320), (200, 1024, 320), (300, 4096, 64)])
 def test_gemm_gate_epilogue(lm, M, N, K):
     """The W1/W3 GEMM with the SiLU-gate epilogue (decode-row tiles, 64x64
     prefill tiles and 256x128 tiles of eight waves, by M) against float64:
-    silu(h1) * h3 rounded to fp16, W1/W3 rows interleaved in blocks of 16."""
+    silu(h1) * h3 rounded to fp16, W1/W3 rows interleaved in blocks of 16.
+    The decode-row and one-round prefill tiles walk K in two wave groups when
+    K is a multiple of 128; the shapes with K = 192, 320 and 64 take the
+    one-group tiles instead."""
     rng = np.random.default_rng(M + 5 * N + 7 * K)
     A = rng.standard_normal((M, K)).astype(np.float16)
     W = (0.02 * rng.standard_normal((N, K))).astype(np.float16)
