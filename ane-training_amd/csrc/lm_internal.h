@@ -67,11 +67,17 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * launch last microseconds; the limit only ends a launch that cannot make
  * progress. */
 #define LM_HANDOFF_US 100000
+/* Copies (C0, one layer per launch, same box, two alternating runs each,
+ * us/token with the fp32 cache): 4 and 4 153.1-153.9, 1 and 8 150.2-150.5,
+ * 1 and 4 151.0-152.9, 2 and 8 150.4-150.7 (another box), 8 and 8 worse, x
+ * in 12 or 16 copies worse.  The 512 W1/W3 readers of x gain from more
+ * copies; the 96 readers of the head outputs and of the gate lose more to
+ * their writers' extra stores than they gain. */
 #ifndef LM_TA_COPIES
-#define LM_TA_COPIES 4
+#define LM_TA_COPIES 1
 #endif
 #ifndef LM_TX_COPIES
-#define LM_TX_COPIES 4
+#define LM_TX_COPIES 8
 #endif
 #define LM_TAG_WORDS(NQ, NKV, D, F) \
     ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * ((NQ) + (F)) + LM_TX_COPIES * (D)))
