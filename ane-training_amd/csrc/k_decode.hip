@@ -994,7 +994,7 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
     float acc[NB], h1[NB], h3[NB];
     hw_dot<D, NB>(wv, xs, hl, acc);
     pair_reduce<NB>(acc, h1, h3);
-    if (lane < LM_TA_COPIES) {
+    if (lane < LM_TG_COPIES) {
         unsigned long long *dst = tg.tgt + (size_t)lane * LM_TAG_B * F + i;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
@@ -1009,7 +1009,7 @@ __device__ __forceinline__ void w13_role(const float *__restrict__ rms_w, const 
 
 /* W2 role of k_qkv_attn (the FFN in the launch), work-group a of the role, a
  * row pair per wave as in k_w2_residual: x[b, r..r+1] = x'[b, r..r+1] +
- * W2[r..r+1, :] . g[b], g from copy a % LM_TA_COPIES of its tagged words. */
+ * W2[r..r+1, :] . g[b], g from copy a % LM_TG_COPIES of its tagged words. */
 template <int D, int NB, int F>
 __device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__restrict__ W2, int B,
                                         const QkvTagged &tg, int a, float *xs)
@@ -1022,8 +1022,8 @@ __device__ __forceinline__ void w2_role(float *__restrict__ x, const u16 *__rest
     hw_load<F>(W2 + (size_t)(r + half) * F, hl, wv);
     const unsigned tag = qkv_tag(tg);
     const unsigned long long *txc = tg.tx + (size_t)(a % LM_TX_COPIES) * LM_TAG_B * D + r;
-    const unsigned long long *tgc = tg.tgt + (size_t)(a % LM_TA_COPIES) * LM_TAG_B * F;
-    tag_doorbell(tgc, B * F, a / LM_TA_COPIES, tag, tg.err);
+    const unsigned long long *tgc = tg.tgt + (size_t)(a % LM_TG_COPIES) * LM_TAG_B * F;
+    tag_doorbell(tgc, B * F, a / LM_TG_COPIES, tag, tg.err);
     /* x' of this row pair (written before any gate word) with the gate */
     unsigned long long v0[NB], v1[NB];
 #pragma unroll
@@ -1088,7 +1088,7 @@ __global__ void __launch_bounds__(WG) k_qkv_attn(
     QkvTagged tg, float *__restrict__ out, const u16 *__restrict__ Wo, FfnArgs ffn)
 {
     static_assert(F == 0 || WO, "the FFN roles take x' from the Wo role");
-    static_assert(LM_TA_COPIES <= 64 && LM_TX_COPIES <= 64, "a wave's lanes store the copies");
+    static_assert(LM_TA_COPIES <= 64 && LM_TX_COPIES <= 64 && LM_TG_COPIES <= 64, "a wave's lanes store the copies");
     if ((int)blockIdx.x < nprod) {
         qkv_rows<D, NB, KT>(x, emb, tok, rms_w, W, NQ, NKV, HD, rc, rs, pos, B, nullptr, kc, vc,
                             max_seq, npairs, &tg, !WO);

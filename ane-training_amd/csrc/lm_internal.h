@@ -58,7 +58,7 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
 
 /* Tagged hand-off words of the batch 1-4 chain (LM_TAG_WORDS of them): q, k
  * and v of up to LM_TAG_B rows, then LM_TA_COPIES copies of the head
- * outputs, LM_TX_COPIES of x after Wo and LM_TA_COPIES of the FFN gate, each
+ * outputs, LM_TX_COPIES of x after Wo and LM_TG_COPIES of the FFN gate, each
  * reading work-group taking one copy, so that the readers of one value spread
  * over more memory channels. */
 #define LM_TAG_B 4
@@ -67,20 +67,26 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * launch last microseconds; the limit only ends a launch that cannot make
  * progress. */
 #define LM_HANDOFF_US 100000
-/* Copies (C0, one layer per launch, same box, two alternating runs each,
- * us/token with the fp32 cache): 4 and 4 153.1-153.9, 1 and 8 150.2-150.5,
- * 1 and 4 151.0-152.9, 2 and 8 150.4-150.7 (another box), 8 and 8 worse, x
- * in 12 or 16 copies worse.  The 512 W1/W3 readers of x gain from more
- * copies; the 96 readers of the head outputs and of the gate lose more to
- * their writers' extra stores than they gain. */
+/* Copies of the head outputs (LM_TA_COPIES), x after Wo (LM_TX_COPIES) and
+ * the gate (LM_TG_COPIES).  C0 with one layer per launch, same-box A/Bs, two
+ * alternating runs each, us/token with the fp32 cache: 4/4/4 153.1-153.9
+ * against 1/8/1 150.2-150.5; then 1/8/1 152.9-153.1 against 2/8/1
+ * 151.7-151.8, 1/8/2 153.2-153.3, 1/8/4 153.6-153.9; then 2/8/1 150.6-150.8
+ * against 4/8/1 151.4-151.6 and 8/8/1 150.5-150.7 (binary16 K/V 1.2 us
+ * slower); x in 12 or 16 copies 154-157.  Each copy costs its writers one
+ * more partial-line store per value: the 512 W1/W3 readers of x gain from
+ * more, the 96 readers of the gate, written by 512 work-groups, do not. */
 #ifndef LM_TA_COPIES
-#define LM_TA_COPIES 1
+#define LM_TA_COPIES 2
 #endif
 #ifndef LM_TX_COPIES
 #define LM_TX_COPIES 8
 #endif
+#ifndef LM_TG_COPIES
+#define LM_TG_COPIES 1
+#endif
 #define LM_TAG_WORDS(NQ, NKV, D, F) \
-    ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * ((NQ) + (F)) + LM_TX_COPIES * (D)))
+    ((size_t)LM_TAG_B * ((NQ) + 2 * (NKV) + LM_TA_COPIES * (NQ) + LM_TG_COPIES * (F) + LM_TX_COPIES * (D)))
 
 /* lmk_qkv_rope and the attention of every (head, row) in one launch: the
  * QKV work-groups hand q, k, v of the current position to the attention
