@@ -75,7 +75,10 @@ int lmk_qkv_rope(hipStream_t s, float *x, const uint16_t *emb, const int *tok,
  * against 4/8/1 151.4-151.6 and 8/8/1 150.5-150.7 (binary16 K/V 1.2 us
  * slower); x in 12 or 16 copies 154-157.  Each copy costs its writers one
  * more partial-line store per value: the 512 W1/W3 readers of x gain from
- * more, the 96 readers of the gate, written by 512 work-groups, do not. */
+ * more, the 96 readers of the gate, written by 512 work-groups, do not.
+ * Reader a takes copy a % copies: with work-group ids going to XCDs mod 8,
+ * each XCD's readers of x share one copy (spreading a copy's readers over
+ * the XCDs cost 4 us/token). */
 #ifndef LM_TA_COPIES
 #define LM_TA_COPIES 2
 #endif
