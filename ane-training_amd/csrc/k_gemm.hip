@@ -820,12 +820,14 @@ __global__ void __launch_bounds__(64 * WVM * WVN * KG) k_gemm_tile(const u16 *__
  * c*256 + 4l .. +3 (c < D/256) as float4 groups, so every access is a 16-byte
  * (x, partials, gain) or 8-byte (embedding, xn) lane segment, and the sum of
  * squares is a wave reduction (no LDS, no barrier).  Partials are loaded four
- * at a time.  Used from 512 rows: 4.5 against 6.3 us for one work-group per row
- * at 2048 rows with one partial (C3 2-3% faster); below that the work-group
- * per row spreads the rows over more CUs (C1 and 32 decode rows of 2048 were
- * faster with it in the full forward). */
-template <int D>
-__global__ void __launch_bounds__(256) k_rownorm(float *__restrict__ x, int M,
+ * at a time.  RPW rows (waves) per work-group.  Four from 512 rows: 4.5
+ * against 6.3 us for a 256-thread work-group per row at 2048 rows with one
+ * partial (C3 2-3% faster).  One (a work-group per row, spread over more CUs)
+ * for 65-511 rows: C1's 256-token prefill 0.468-0.476 -> 0.465-0.473 ms.  Up
+ * to 64 rows the 256-thread work-group per row (k_rownorm_blk) stays, since
+ * the one-wave form cost the scaled model's 32 decode rows of 2048 6%. */
+template <int D, int RPW = 4>
+__global__ void __launch_bounds__(64 * RPW) k_rownorm(float *__restrict__ x, int M,
                                                    const u16 *__restrict__ emb,
                                                    const int *__restrict__ tok,
                                                    const float *__restrict__ sp, int ns,
@@ -836,7 +838,7 @@ __global__ void __launch_bounds__(256) k_rownorm(float *__restrict__ x, int M,
     constexpr int C4 = D / 256;
     static_assert(D % 256 == 0, "row width");
     const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int m = blockIdx.x * RPW + (threadIdx.x >> 6);
     if (m >= M) return;                       /* wave-uniform; no barrier below */
     float *xr = x + (size_t)m * D + 4 * lane;
     float4 gv[C4];                            /* gain, loaded first: its latency */
@@ -1040,6 +1042,18 @@ extern "C" int lmk_rownorm(hipStream_t s, float *x, int D, int M, const uint16_t
 {
     if (M < 1 || (emb && !tok) || !gain || !xn || ns < 0 || (ns && (!sp || emb)))
         return hipErrorInvalidValue;
+    if (M > 64 && M < 512) {   /* a one-wave work-group per row */
+        dim3 grid(M);
+        switch (D) {
+        case 256: hipLaunchKernelGGL((k_rownorm<256, 1>), grid, dim3(64), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 512: hipLaunchKernelGGL((k_rownorm<512, 1>), grid, dim3(64), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 768: hipLaunchKernelGGL((k_rownorm<768, 1>), grid, dim3(64), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 1024: hipLaunchKernelGGL((k_rownorm<1024, 1>), grid, dim3(64), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        case 2048: hipLaunchKernelGGL((k_rownorm<2048, 1>), grid, dim3(64), 0, s, x, M, emb, tok, sp, ns, sstride, gain, xn); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if (M < 512) {   /* a work-group per row */
         dim3 grid(M);
         switch (D) {
